@@ -1,0 +1,142 @@
+/*
+ * msa.h — C ABI of the MI355X sparse prefill attention library (libmsa.so).
+ *
+ * The reference (white-jim/MInference-NPU) exposes this path only as Python
+ * functions; it has no FFI.  Each entry point below replaces one of those
+ * Python call sites and is bound from Python through ctypes
+ * (minference-npu_amd/minference/_abi.py).  Paths below are relative to
+ * MInference-NPU/ in the reference tree.
+ *
+ * Conventions
+ *   - Every tensor pointer is a DEVICE pointer; the caller owns every buffer.
+ *     The library allocates nothing and never synchronises the stream.
+ *   - Tensors are 4-D [B, H, S, D] views described by msa_tensor4 (strides in
+ *     elements).  The innermost (D) stride must be 1 and rows must be 16-byte
+ *     aligned, so the HF BNSD views of a fused qkv projection are read in place.
+ *   - Return value: 0 = launched; negative MSA_E_* = host-side validation
+ *     failed and nothing was launched; positive = hipError_t reported by the
+ *     runtime right after the launch.
+ *   - Calls on the same stream are ordered; calls that share a workspace on
+ *     different streams race.
+ */
+#ifndef MSA_H_
+#define MSA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSA_ABI_VERSION 1
+
+/* status codes (negative: validation, nothing launched) */
+#define MSA_OK 0
+#define MSA_E_NULL (-1)        /* a required pointer is NULL */
+#define MSA_E_RANK (-2)        /* shape mismatch between q/k/v/o */
+#define MSA_E_DTYPE (-3)       /* unsupported or mismatched dtype */
+#define MSA_E_HEAD_DIM (-4)    /* D not in {64, 96, 128} */
+#define MSA_E_ALIGN (-5)       /* D stride != 1 or rows not 16-byte aligned */
+#define MSA_E_BLOCK (-6)       /* block size other than 64 */
+#define MSA_E_TOPK (-7)        /* topk < 1 or topk > n_kv_blocks */
+#define MSA_E_HEADS (-8)       /* bad head count / head index / kind */
+#define MSA_E_WORKSPACE (-9)   /* workspace missing or too small */
+#define MSA_E_SEQ (-10)        /* S_q > S_k, S_q == 0, or too long */
+#define MSA_E_SLOTS (-11)      /* block-sparse head without an index slot */
+
+/* element types */
+#define MSA_DTYPE_BF16 1
+#define MSA_DTYPE_FP16 2
+#define MSA_DTYPE_FP32 3
+
+/* head kinds (pattern names of the per-head JSON) */
+#define MSA_KIND_DENSE 0  /* "dense"        */
+#define MSA_KIND_STREAM 1 /* "stream_llm"   */
+#define MSA_KIND_BLOCK 2  /* "block_sparse" */
+
+#define MSA_MAX_HEADS 128 /* head descriptors per msa_layer_attention call */
+#define MSA_BLOCK 64      /* the only supported block size */
+
+typedef struct msa_tensor4 {
+  void* data;
+  int64_t size[4];   /* B, H, S, D */
+  int64_t stride[4]; /* elements */
+  int32_t dtype;     /* MSA_DTYPE_* */
+  int32_t reserved;
+} msa_tensor4;
+
+/* One attention head of a layer.
+ *   kind   = MSA_KIND_*
+ *   p1, p2 = stream_llm: n_init, n_local;  block_sparse: topk (unused here), 0
+ *   slot   = block_sparse: row of idx/cnt written by msa_block_estimate; else -1
+ *   scale  = softmax scale applied to q.k (the caller decides)
+ * Mirrors the per-head record [type, p1, p2, score] parsed at
+ * minference/modules/minference_forward.py:187-198, 404-419. */
+typedef struct msa_head_desc {
+  int32_t kind;
+  int32_t p1;
+  int32_t p2;
+  int32_t slot;
+  float scale;
+  int32_t reserved;
+} msa_head_desc;
+
+typedef struct ihipStream_t* msa_stream_t; /* == hipStream_t */
+
+int msa_abi_version(void);
+const char* msa_status_str(int status);
+
+/* Bytes of workspace msa_block_estimate needs (pooled Q and K^T, fp32). */
+size_t msa_estimate_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_q,
+                                    int64_t s_k, int32_t head_dim);
+
+/* Block top-k estimator for the block_sparse heads of a layer (one call for
+ * all of them).  Replaces _select_block_sparse_topk_indices
+ * (minference/ops/block_sparse_kernel_npu.py:230-263): 64-token mean pooling
+ * of Q and K in the input dtype (rounded to it), fp32 pooled scores
+ * q_pool.k_pool * score_scale, block-causal mask in the q-block frame, top-k
+ * per query block, ids sorted ascending.  Ties break to the lower block id.
+ *   slot_heads[s] (host array) = head index in q for slot s, s < n_slots
+ *   slot_topk[s]  (host array or NULL = all topk_max) = top-k of slot s,
+ *                 1 <= slot_topk[s] <= topk_max <= n_kv_blocks (the caller
+ *                 clamps topk_blocks to n_kv_blocks as the reference does)
+ *   idx  [B][n_slots][n_qb][topk_max] int32 (device): the first cnt entries
+ *        are the selected causal block ids ascending, entries cnt..topk-1 are
+ *        the next future ids bq+1, bq+2, ... (never attended), entries
+ *        topk..topk_max-1 are left untouched
+ *   cnt  [B][n_slots][n_qb] int32 (device): min(topk, bq+1) */
+int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k,
+                       const int32_t* slot_heads, const int32_t* slot_topk,
+                       int32_t n_slots, int32_t block, int32_t topk_max,
+                       float score_scale, int32_t* idx, int32_t* cnt,
+                       void* workspace, size_t workspace_bytes,
+                       msa_stream_t stream);
+
+/* Bytes of workspace msa_layer_attention needs (V^T staged as fp16). */
+size_t msa_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t s_k,
+                                     int32_t head_dim);
+
+/* All heads of one layer in one attention launch (plus one V staging launch).
+ * Replaces the grouped dispatch of minference/modules/minference_forward.py:398-487
+ * and the three ops it calls:
+ *   streaming_forward       minference/ops/streaming_kernel_npu.py:349-397
+ *   block_sparse attention  minference/ops/block_sparse_kernel_npu.py:441-601
+ *   dense_attention         minference/backend_npu/attention.py:192-255
+ * heads[h] (host array, n_heads == H of q) describes head h.  idx/cnt are the
+ * msa_block_estimate outputs (or caller-built lists sorted ascending; entries
+ * outside [0, n_kv_blocks), repeated or in the causal future are skipped);
+ * they may be NULL when no head is block_sparse.  o may be bf16/fp16 (== q's
+ * dtype) or fp32.  Rows with no visible key are written as 0. */
+int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k,
+                        const msa_tensor4* v, const msa_tensor4* o,
+                        const msa_head_desc* heads, int32_t n_heads,
+                        const int32_t* idx, const int32_t* cnt, int32_t idx_slots,
+                        int32_t topk_max, void* workspace, size_t workspace_bytes,
+                        msa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSA_H_ */

@@ -1,0 +1,294 @@
+// C ABI (include/msa.h): host-side validation, argument packing and launches.
+// Nothing here allocates device memory or synchronises the stream.
+
+#include <math.h>
+#include <string.h>
+
+#include "../../include/msa.h"
+#include "msa_kernels.h"
+
+using namespace msa;
+
+namespace {
+
+constexpr int64_t kMaxSeq = int64_t(1) << 20;  // 1M tokens: 16384 blocks
+
+int elem_size(int dtype) {
+  switch (dtype) {
+    case MSA_DTYPE_BF16:
+    case MSA_DTYPE_FP16: return 2;
+    case MSA_DTYPE_FP32: return 4;
+    default: return 0;
+  }
+}
+
+bool head_dim_ok(int64_t d) { return d == 64 || d == 96 || d == 128; }
+
+// D contiguous, every row and the base 16-byte aligned.
+bool aligned(const msa_tensor4* t) {
+  const int es = elem_size(t->dtype);
+  if (es == 0 || t->stride[3] != 1) return false;
+  if ((reinterpret_cast<uintptr_t>(t->data) & 15u) != 0) return false;
+  for (int i = 0; i < 3; ++i)
+    if (t->size[i] > 1 && ((t->stride[i] * es) & 15) != 0) return false;
+  return true;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int check_qk(const msa_tensor4* q, const msa_tensor4* k) {
+  if (!q || !k || !q->data || !k->data) return MSA_E_NULL;
+  for (int i = 0; i < 4; ++i)
+    if (q->size[i] <= 0 || k->size[i] <= 0) return MSA_E_RANK;
+  if (q->size[0] != k->size[0] || q->size[3] != k->size[3]) return MSA_E_RANK;
+  if (q->size[1] % k->size[1] != 0) return MSA_E_RANK;
+  if (q->dtype != k->dtype) return MSA_E_DTYPE;
+  if (q->dtype != MSA_DTYPE_BF16 && q->dtype != MSA_DTYPE_FP16) return MSA_E_DTYPE;
+  if (!head_dim_ok(q->size[3])) return MSA_E_HEAD_DIM;
+  if (!aligned(q) || !aligned(k)) return MSA_E_ALIGN;
+  if (q->size[2] > kMaxSeq || k->size[2] > kMaxSeq) return MSA_E_SEQ;
+  return MSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int msa_abi_version(void) { return MSA_ABI_VERSION; }
+
+const char* msa_status_str(int status) {
+  switch (status) {
+    case MSA_OK: return "ok";
+    case MSA_E_NULL: return "a required pointer is NULL";
+    case MSA_E_RANK: return "shape mismatch between q, k, v and o";
+    case MSA_E_DTYPE: return "unsupported or mismatched dtype (q/k/v must be bf16 or fp16; o same or fp32)";
+    case MSA_E_HEAD_DIM: return "head_dim must be 64, 96 or 128";
+    case MSA_E_ALIGN: return "head_dim stride must be 1 and rows 16-byte aligned";
+    case MSA_E_BLOCK: return "block size must be 64";
+    case MSA_E_TOPK: return "topk must be in [1, n_kv_blocks]";
+    case MSA_E_HEADS: return "bad head count, head index or head kind";
+    case MSA_E_WORKSPACE: return "workspace missing or too small";
+    case MSA_E_SEQ: return "sequence lengths must satisfy 0 < S_q <= S_k <= 2^20";
+    case MSA_E_SLOTS: return "block_sparse head without a valid index slot or idx/cnt buffers";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
+  return "unknown status";
+}
+
+size_t msa_estimate_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_q, int64_t s_k,
+                                    int32_t head_dim) {
+  if (batch <= 0 || n_slots <= 0 || s_q <= 0 || s_k <= 0 || head_dim <= 0) return 0;
+  const int64_t sb = batch * n_slots;
+  const int64_t bytes = sb * (cdiv(s_q, MSA_BLOCK) + cdiv(s_k, MSA_BLOCK)) * head_dim * 4;
+  return size_t((bytes + 255) / 256 * 256);
+}
+
+int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t* slot_heads,
+                       const int32_t* slot_topk, int32_t n_slots, int32_t block,
+                       int32_t topk_max, float score_scale, int32_t* idx, int32_t* cnt,
+                       void* workspace, size_t workspace_bytes, msa_stream_t stream) {
+  int st = check_qk(q, k);
+  if (st != MSA_OK) return st;
+  if (block != MSA_BLOCK) return MSA_E_BLOCK;
+  if (!slot_heads || !idx || !cnt) return MSA_E_NULL;
+  if (n_slots <= 0 || n_slots > kMaxHeads) return MSA_E_HEADS;
+  const int H = int(q->size[1]);
+  for (int s = 0; s < n_slots; ++s)
+    if (slot_heads[s] < 0 || slot_heads[s] >= H) return MSA_E_HEADS;
+  const int n_qb = int(cdiv(q->size[2], MSA_BLOCK));
+  const int n_kb = int(cdiv(k->size[2], MSA_BLOCK));
+  if (topk_max < 1 || topk_max > n_kb) return MSA_E_TOPK;
+  if (slot_topk)
+    for (int s = 0; s < n_slots; ++s)
+      if (slot_topk[s] < 1 || slot_topk[s] > topk_max) return MSA_E_TOPK;
+  if (!(score_scale > 0.0f) || !isfinite(score_scale)) return MSA_E_TOPK;
+  if (score_rows_for(n_kb) == 0) return MSA_E_SEQ;
+  const int D = int(q->size[3]);
+  const size_t need = msa_estimate_workspace_bytes(q->size[0], n_slots, q->size[2], k->size[2], D);
+  if (!workspace || workspace_bytes < need) return MSA_E_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
+  if (q->size[0] * n_slots > 65535) return MSA_E_HEADS;
+
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  const int64_t sb = q->size[0] * n_slots;
+  float* q_pool = static_cast<float*>(workspace);
+  float* k_poolT = q_pool + sb * n_qb * D;
+
+  PoolParams pp;
+  memset(&pp, 0, sizeof(pp));
+  pp.q = q->data;
+  pp.k = k->data;
+  pp.q_sb = q->stride[0]; pp.q_sh = q->stride[1]; pp.q_ss = q->stride[2];
+  pp.k_sb = k->stride[0]; pp.k_sh = k->stride[1]; pp.k_ss = k->stride[2];
+  pp.s_q = q->size[2];
+  pp.s_k = k->size[2];
+  pp.n_qb = n_qb;
+  pp.n_kb = n_kb;
+  pp.batch = int(q->size[0]);
+  pp.n_slots = n_slots;
+  pp.kv_group = int(q->size[1] / k->size[1]);
+  pp.q_pool = q_pool;
+  pp.k_poolT = k_poolT;
+  for (int s = 0; s < n_slots; ++s) pp.slot_heads[s] = int16_t(slot_heads[s]);
+  hipError_t e = launch_pool(pp, q->dtype, D, hs);
+  if (e != hipSuccess) return int(e);
+
+  ScoreParams sp;
+  sp.q_pool = q_pool;
+  sp.k_poolT = k_poolT;
+  sp.idx = idx;
+  sp.cnt = cnt;
+  sp.n_qb = n_qb;
+  sp.n_kb = n_kb;
+  sp.topk_max = topk_max;
+  sp.batch = int(q->size[0]);
+  sp.n_slots = n_slots;
+  sp.scale = score_scale;
+  for (int s = 0; s < n_slots; ++s) sp.slot_topk[s] = int16_t(slot_topk ? slot_topk[s] : topk_max);
+  e = launch_score(sp, D, hs);
+  return e == hipSuccess ? MSA_OK : int(e);
+}
+
+size_t msa_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t s_k,
+                                     int32_t head_dim) {
+  if (batch <= 0 || kv_heads <= 0 || s_k <= 0 || head_dim <= 0) return 0;
+  const int64_t bytes = batch * kv_heads * head_dim * cdiv(s_k, MSA_BLOCK) * MSA_BLOCK * 2;
+  return size_t((bytes + 255) / 256 * 256);
+}
+
+int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
+                        const msa_tensor4* o, const msa_head_desc* heads, int32_t n_heads,
+                        const int32_t* idx, const int32_t* cnt, int32_t idx_slots,
+                        int32_t topk_max, void* workspace, size_t workspace_bytes,
+                        msa_stream_t stream) {
+  int st = check_qk(q, k);
+  if (st != MSA_OK) return st;
+  if (!v || !o || !v->data || !o->data || !heads) return MSA_E_NULL;
+  for (int i = 0; i < 4; ++i) {
+    if (v->size[i] != k->size[i]) return MSA_E_RANK;
+    if (o->size[i] != q->size[i]) return MSA_E_RANK;
+  }
+  if (v->dtype != q->dtype) return MSA_E_DTYPE;
+  if (o->dtype != q->dtype && o->dtype != MSA_DTYPE_FP32) return MSA_E_DTYPE;
+  if (!aligned(v) || !aligned(o)) return MSA_E_ALIGN;
+  const int64_t B = q->size[0], H = q->size[1], Hkv = k->size[1];
+  const int64_t Sq = q->size[2], Sk = k->size[2];
+  const int D = int(q->size[3]);
+  if (Sq > Sk) return MSA_E_SEQ;
+  if (n_heads != H || H > kMaxHeads) return MSA_E_HEADS;
+  const int n_qb = int(cdiv(Sq, MSA_BLOCK));
+  const int n_kb = int(cdiv(Sk, MSA_BLOCK));
+  bool any_block = false;
+  for (int h = 0; h < n_heads; ++h) {
+    const msa_head_desc& hd = heads[h];
+    if (hd.kind != MSA_KIND_DENSE && hd.kind != MSA_KIND_STREAM && hd.kind != MSA_KIND_BLOCK)
+      return MSA_E_HEADS;
+    if (!(hd.scale > 0.0f) || !isfinite(hd.scale)) return MSA_E_HEADS;
+    if (hd.kind == MSA_KIND_BLOCK) {
+      any_block = true;
+      if (hd.slot < 0 || hd.slot >= idx_slots) return MSA_E_SLOTS;
+    }
+  }
+  if (any_block && (!idx || !cnt || topk_max < 1)) return MSA_E_SLOTS;
+  const size_t need = msa_attention_workspace_bytes(B, Hkv, Sk, D);
+  if (!workspace || workspace_bytes < need) return MSA_E_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
+  if (int64_t(n_qb) * B * H > 0x7fffffffLL) return MSA_E_SEQ;
+  if (B * Hkv > 65535) return MSA_E_HEADS;
+
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  uint16_t* vt = static_cast<uint16_t*>(workspace);
+
+  VtParams vp;
+  vp.v = v->data;
+  vp.v_sb = v->stride[0]; vp.v_sh = v->stride[1]; vp.v_ss = v->stride[2];
+  vp.vt = vt;
+  vp.batch = int(B);
+  vp.kv_heads = int(Hkv);
+  vp.s_k = int(Sk);
+  vp.s_pad = n_kb * MSA_BLOCK;
+  hipError_t e = launch_vt(vp, v->dtype, D, hs);
+  if (e != hipSuccess) return int(e);
+
+  AttnParams ap;
+  memset(&ap, 0, sizeof(ap));
+  ap.q = q->data;
+  ap.k = k->data;
+  ap.vt = vt;
+  ap.o = o->data;
+  ap.q_sb = q->stride[0]; ap.q_sh = q->stride[1]; ap.q_ss = q->stride[2];
+  ap.k_sb = k->stride[0]; ap.k_sh = k->stride[1]; ap.k_ss = k->stride[2];
+  ap.o_sb = o->stride[0]; ap.o_sh = o->stride[1]; ap.o_ss = o->stride[2];
+  ap.batch = int(B);
+  ap.heads = int(H);
+  ap.kv_group = int(H / Hkv);
+  ap.s_q = int(Sq);
+  ap.s_k = int(Sk);
+  ap.n_qb = n_qb;
+  ap.n_kb = n_kb;
+  ap.s_pad = n_kb * MSA_BLOCK;
+  ap.idx = idx;
+  ap.cnt = cnt;
+  ap.idx_slots = idx_slots;
+  ap.topk_max = topk_max;
+  const double log2e = 1.4426950408889634;
+  for (int h = 0; h < n_heads; ++h) {
+    ap.hd[h].kind = int16_t(heads[h].kind);
+    ap.hd[h].slot = int16_t(heads[h].kind == MSA_KIND_BLOCK ? heads[h].slot : 0);
+    ap.hd[h].p1 = heads[h].p1;
+    ap.hd[h].p2 = heads[h].p2;
+    ap.hd[h].scale_log2 = float(double(heads[h].scale) * log2e);
+  }
+
+  // Spread (batch, head) pairs over the 8 XCDs (round-robin workgroup
+  // dispatch) so each XCD's L2 serves a fixed head subset and the estimated
+  // work per XCD is balanced (greedy longest-processing-time assignment).
+  const int BH = int(B * H);
+  if (BH % 8 == 0 && BH <= kMaxHeads) {
+    const int per = BH / 8;
+    double cost[kMaxHeads];
+    for (int hh = 0; hh < BH; ++hh) {
+      const msa_head_desc& hd = heads[hh % H];
+      const double nb = double(n_kb);
+      if (hd.kind == MSA_KIND_DENSE) cost[hh] = nb * (nb + 1) / 2;
+      else if (hd.kind == MSA_KIND_STREAM) {
+        const double band = fmin(nb, double(hd.p2) / 64.0 + 1.0);
+        const double sink = fmin(nb, ceil(fmax(double(hd.p1), 0.0) / 64.0));
+        cost[hh] = nb * (band + sink);
+      } else {
+        const double kk = fmin(nb, double(topk_max));
+        cost[hh] = nb * kk - kk * (kk - 1) / 2;
+      }
+    }
+    int order[kMaxHeads];
+    for (int i = 0; i < BH; ++i) order[i] = i;
+    for (int i = 1; i < BH; ++i) {  // insertion sort, descending cost
+      const int x = order[i];
+      int j = i - 1;
+      while (j >= 0 && cost[order[j]] < cost[x]) {
+        order[j + 1] = order[j];
+        --j;
+      }
+      order[j + 1] = x;
+    }
+    double load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int fill[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < BH; ++i) {
+      int best = -1;
+      for (int x = 0; x < 8; ++x)
+        if (fill[x] < per && (best < 0 || load[x] < load[best])) best = x;
+      ap.head_order[best * per + fill[best]] = int16_t(order[i]);
+      ++fill[best];
+      load[best] += cost[order[i]];
+    }
+    ap.xcd_heads = per;
+  } else {
+    ap.xcd_heads = 0;
+  }
+
+  e = launch_attention(ap, q->dtype, o->dtype, D, hs);
+  return e == hipSuccess ? MSA_OK : int(e);
+}
+
+}  // extern "C"

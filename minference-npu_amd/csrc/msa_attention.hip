@@ -1,0 +1,475 @@
+// Unified tile-list flash attention for one prefill layer (all heads, one grid).
+//
+// Work item = (head, 64-row query block).  Each item walks a list of 64-key
+// tiles whose shape depends on the head kind:
+//   dense        : every causal tile 0..diag              (backend_npu/attention.py:192-255)
+//   stream_llm   : sink tiles, then the local band tiles  (ops/streaming_kernel_npu.py:94-146)
+//   block_sparse : the estimator's block ids              (ops/block_sparse_kernel_npu.py:266-348,
+//                                                          ops/tilelang_sparse_attention_h1.py:367-683)
+// Token visibility (exact reference masks; row a is the absolute position
+// i + S_k - S_q):
+//   all kinds : j <= a and j < S_k
+//   stream    : and (j > a - n_local or j < n_init)
+// Rows with no visible key produce 0 (the reference's nan_to_num).
+//
+// CDNA4 mapping (one workgroup = 2 wave64, 64 query rows):
+//   wave w owns keys [32w, 32w+32) of every tile and all 64 rows, keeping a
+//   private online-softmax state; the two states merge once at the end.
+//   S^T = K.Q^T on v_mfma_f32_32x32x16_{bf16,f16} (A = K tile from LDS,
+//   B = Q from registers) so that the accumulator layout (one query row per
+//   lane) is directly the B operand of O^T = V^T.P^T on v_mfma_f32_32x32x16_f16.
+//   P is rounded to fp16 (11-bit mantissa) and the row sum uses the rounded P.
+//   V is staged once per layer as fp16 V^T with keys permuted inside each
+//   16-key group so every PV A operand is one 16-byte LDS read.
+//   Row max / sum need one lane^32 exchange per tile.
+
+#include "msa_common.h"
+#include "msa_kernels.h"
+
+namespace msa {
+
+constexpr int KIND_DENSE = 0;
+constexpr int KIND_STREAM = 1;
+constexpr int KIND_BLOCK = 2;
+
+// Position of key p inside its 16-key group in the staged V^T rows: quads 1
+// and 2 are swapped (an involution, so it also maps position -> key).
+__device__ inline int vt_perm(int p) {
+  const int q = (p >> 2) & 3;
+  const int qs = ((q & 1) << 1) | (q >> 1);
+  return (p & ~12) | (qs << 2);
+}
+
+// ---------------------------------------------------------------------------
+// V [B][Hkv][S][D] (bf16/fp16) -> V^T [B*Hkv][D][s_pad] fp16, keys permuted,
+// zero padded to s_pad = 64 * n_kb.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(256) void vt_kernel(VtParams P) {
+  constexpr int KCH = D / 8;
+  constexpr int LP = D + 8;  // padded LDS row (halves)
+  __shared__ __align__(16) uint16_t tile[kBlock * LP];
+  const int j0 = blockIdx.x * kBlock;
+  const int bk = blockIdx.y;  // b * kv_heads + kvh
+  const int b = bk / P.kv_heads, kvh = bk - b * P.kv_heads;
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(P.v) + b * P.v_sb + kvh * P.v_sh;
+  for (int ci = threadIdx.x; ci < kBlock * KCH; ci += 256) {
+    const int r = ci / KCH, c = ci - r * KCH;
+    const int j = j0 + r;
+    u32x4 out = zero_u32x4();
+    if (j < P.s_k) {
+      const u32x4 in = load16(src + int64_t(j) * P.v_ss + c * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const _Float16 lo = to_f16_sat<T>(uint16_t(in[e] & 0xffffu));
+        const _Float16 hi = to_f16_sat<T>(uint16_t(in[e] >> 16));
+        out[e] = uint32_t(__builtin_bit_cast(uint16_t, lo)) |
+                 (uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16);
+      }
+    }
+    store16(&tile[r * LP + c * 8], out);
+  }
+  __syncthreads();
+  uint16_t* dst = P.vt + int64_t(bk) * D * P.s_pad;
+  for (int ci = threadIdx.x; ci < D * 8; ci += 256) {
+    const int d = ci >> 3, c = ci & 7;
+    u32x4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int p0 = c * 8 + 2 * e;
+      const uint16_t lo = tile[vt_perm(p0) * LP + d];
+      const uint16_t hi = tile[vt_perm(p0 + 1) * LP + d];
+      out[e] = uint32_t(lo) | (uint32_t(hi) << 16);
+    }
+    store16(dst + int64_t(d) * P.s_pad + j0 + c * 8, out);
+  }
+}
+
+template <typename T, int D>
+static hipError_t launch_vt_t(const VtParams& p, hipStream_t st) {
+  dim3 grid(p.s_pad / kBlock, p.batch * p.kv_heads);
+  hipLaunchKernelGGL((vt_kernel<T, D>), grid, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_vt(const VtParams& p, int dtype, int D, hipStream_t st) {
+  if (dtype == Bf16::id) {
+    if (D == 64) return launch_vt_t<Bf16, 64>(p, st);
+    if (D == 96) return launch_vt_t<Bf16, 96>(p, st);
+    return launch_vt_t<Bf16, 128>(p, st);
+  }
+  if (D == 64) return launch_vt_t<F16, 64>(p, st);
+  if (D == 96) return launch_vt_t<F16, 96>(p, st);
+  return launch_vt_t<F16, 128>(p, st);
+}
+
+// ---------------------------------------------------------------------------
+// attention
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ inline f32x16 mfma_qk(u32x4 a, u32x4 b, f32x16 c);
+
+template <>
+__device__ inline f32x16 mfma_qk<Bf16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <>
+__device__ inline f32x16 mfma_qk<F16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+__device__ inline f32x16 mfma_pv(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// LDS slot swizzles (16-byte granules) that keep the MFMA operand reads free
+// of bank conflicts for 8- and 16-lane LDS phases.
+__device__ inline int k_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+__device__ inline int v_swz(int d) { return (d ^ (d >> 3)) & 7; }
+
+struct TileIter {
+  int kind;
+  int i, n;
+  int nsink, lo;
+  int last_tile;
+  int prev;
+  const int32_t* list;
+
+  __device__ int next() {
+    if (kind == KIND_BLOCK) {
+      while (i < n) {
+        const int t = list[i++];
+        if (t > last_tile) {
+          i = n;
+          return -1;
+        }
+        if (t >= 0 && t > prev) {
+          prev = t;
+          return t;
+        }
+      }
+      return -1;
+    }
+    if (i >= n) return -1;
+    const int t = (kind == KIND_STREAM && i >= nsink) ? lo + (i - nsink) : i;
+    ++i;
+    return t;
+  }
+};
+
+template <typename TO>
+__device__ inline void store_out4(TO* dst, float a, float b, float c, float d);
+
+template <>
+__device__ inline void store_out4<float>(float* dst, float a, float b, float c, float d) {
+  *reinterpret_cast<float4*>(dst) = make_float4(a, b, c, d);
+}
+
+template <typename T>
+__device__ inline void store_out4_16(uint16_t* dst, float a, float b, float c, float d) {
+  uint2 v;
+  v.x = uint32_t(T::from_float(a)) | (uint32_t(T::from_float(b)) << 16);
+  v.y = uint32_t(T::from_float(c)) | (uint32_t(T::from_float(d)) << 16);
+  *reinterpret_cast<uint2*>(dst) = v;
+}
+
+template <typename T, bool OUT_F32, int D>
+__global__ __launch_bounds__(128) void attn_kernel(AttnParams P) {
+  constexpr int KCH = D / 8;   // 16-byte chunks per K row
+  constexpr int NKS = D / 16;  // QK^T k-steps (16 dims each)
+  constexpr int NDB = D / 32;  // PV output blocks of 32 dims
+  constexpr int STG = D / 16;  // staged chunks per thread for K and for V^T
+  constexpr int TILE_BYTES = 2 * kBlock * D * 2;
+  constexpr int MERGE_BYTES = (2 * NDB * 16 * 64 + 4 * 64) * 4;
+  constexpr int LDS_BYTES = TILE_BYTES > MERGE_BYTES ? TILE_BYTES : MERGE_BYTES;
+  __shared__ __align__(16) unsigned char lds[LDS_BYTES];
+  u32x4* ks = reinterpret_cast<u32x4*>(lds);
+  u32x4* vs = ks + kBlock * KCH;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int n = lane & 31;
+  const int g = lane >> 5;
+  const int w = tid >> 6;
+
+  // ---- work item: query blocks longest-first, heads spread over the XCDs
+  const int BH = P.batch * P.heads;
+  const int item = blockIdx.x;
+  int hh, bq;
+  if (P.xcd_heads) {
+    const int r = item >> 3;
+    bq = P.n_qb - 1 - r / P.xcd_heads;
+    hh = P.head_order[(item & 7) * P.xcd_heads + r % P.xcd_heads];
+  } else {
+    bq = P.n_qb - 1 - item / BH;
+    hh = item % BH;
+  }
+  const int b = hh / P.heads;
+  const int h = hh - b * P.heads;
+  const int kvh = h / P.kv_group;
+  const HeadArg hd = P.hd[h];
+  const int kind = hd.kind;
+
+  const int q0 = bq * kBlock;
+  const int nrows = min(kBlock, P.s_q - q0);
+  const int off = P.s_k - P.s_q;
+  const int a0 = q0 + off;
+  const int a1 = q0 + nrows - 1 + off;
+  const int last_tile = min(a1 >> 6, P.n_kb - 1);
+  const int n_init = hd.p1;
+  const int n_local = hd.p2;
+
+  TileIter it;
+  it.kind = kind;
+  it.i = 0;
+  it.prev = -1;
+  it.last_tile = last_tile;
+  it.nsink = 0;
+  it.lo = 0;
+  it.list = nullptr;
+  if (kind == KIND_BLOCK) {
+    const int64_t base = (int64_t(b) * P.idx_slots + hd.slot) * P.n_qb + bq;
+    it.n = min(P.cnt[base], P.topk_max);
+    it.list = P.idx + base * P.topk_max;
+  } else if (kind == KIND_STREAM) {
+    const int band_lo = max(a0 - n_local + 1, 0);
+    it.lo = min(band_lo >> 6, last_tile + 1);
+    const int sink_keys = min(max(n_init, 0), P.s_k);
+    it.nsink = min((sink_keys + 63) >> 6, it.lo);
+    it.n = it.nsink + (last_tile - it.lo + 1);
+  } else {
+    it.n = last_tile + 1;
+  }
+
+  const uint16_t* kbase =
+      reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + int64_t(kvh) * P.k_sh;
+  const uint16_t* vtbase =
+      P.vt + (int64_t(b) * (P.heads / P.kv_group) + kvh) * D * int64_t(P.s_pad);
+
+  // ---- Q as the B operand: lane (n, g) holds Q[row][16ks + 8g .. +7]
+  u32x4 qb[2][NKS];
+  {
+    const uint16_t* qbase =
+        reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + int64_t(h) * P.q_sh;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int row = q0 + 32 * rb + n;
+#pragma unroll
+      for (int kk = 0; kk < NKS; ++kk)
+        qb[rb][kk] = row < P.s_q ? load16(qbase + int64_t(row) * P.q_ss + 16 * kk + 8 * g)
+                                 : zero_u32x4();
+    }
+  }
+
+  u32x4 kr[STG], vr[STG];
+  auto load_tile = [&](int t) {
+    const int j0 = t * kBlock;
+#pragma unroll
+    for (int u = 0; u < STG; ++u) {
+      const int ci = tid + 128 * u;
+      const int r = ci / KCH, c = ci - (ci / KCH) * KCH;
+      const int j = j0 + r;
+      kr[u] = j < P.s_k ? load16(kbase + int64_t(j) * P.k_ss + 8 * c) : zero_u32x4();
+      const int d = ci >> 3, c2 = ci & 7;
+      vr[u] = load16(vtbase + int64_t(d) * P.s_pad + j0 + 8 * c2);
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int u = 0; u < STG; ++u) {
+      const int ci = tid + 128 * u;
+      const int r = ci / KCH, c = ci - (ci / KCH) * KCH;
+      ks[r * KCH + (c ^ k_swz(r))] = kr[u];
+      const int d = ci >> 3, c2 = ci & 7;
+      vs[d * 8 + (c2 ^ v_swz(d))] = vr[u];
+    }
+  };
+
+  f32x16 o[NDB][2];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[db][rb][i] = 0.0f;
+  float m[2] = {-1e30f, -1e30f};
+  float l[2] = {0.0f, 0.0f};
+  const float c_log2 = hd.scale_log2;
+
+  int t = it.next();
+  if (t >= 0) {
+    load_tile(t);
+    store_tile();
+  }
+  __syncthreads();
+
+  const int krow = 32 * w + n;  // this lane's key row inside the tile (A operand)
+  while (t >= 0) {
+    const int tn = it.next();
+    if (tn >= 0) load_tile(tn);
+
+    // S^T[key][row] for keys 32w..32w+31
+    f32x16 s[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[rb][i] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < NKS; ++kk) {
+      const u32x4 a = ks[krow * KCH + ((2 * kk + g) ^ k_swz(krow))];
+      s[0] = mfma_qk<T>(a, qb[0][kk], s[0]);
+      s[1] = mfma_qk<T>(a, qb[1][kk], s[1]);
+    }
+
+    const int j0 = t * kBlock;
+    const int j1 = j0 + kBlock - 1;
+    bool full = (j1 <= a0) && (j1 < P.s_k);
+    if (kind == KIND_STREAM) full = full && ((j0 >= a1 - n_local + 1) || (j1 < n_init));
+    if (!full) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const int arow = a0 + 32 * rb + n;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int j = j0 + 32 * w + 8 * (i >> 2) + 4 * g + (i & 3);
+          bool vis = (j <= arow) && (j < P.s_k);
+          if (kind == KIND_STREAM) vis = vis && ((j >= arow - n_local + 1) || (j < n_init));
+          if (!vis) s[rb][i] = -__builtin_inff();
+        }
+      }
+    }
+
+    // online softmax (base 2), P rounded to fp16
+    u32x4 pb[2][2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s[rb][i] *= c_log2;
+        mx = fmaxf(mx, s[rb][i]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(m[rb], mx);
+      const float alpha = __builtin_amdgcn_exp2f(m[rb] - mnew);
+      m[rb] = mnew;
+      float sum = 0.0f;
+      uint16_t hbits[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const _Float16 ph = static_cast<_Float16>(__builtin_amdgcn_exp2f(s[rb][i] - mnew));
+        sum += float(ph);
+        hbits[i] = __builtin_bit_cast(uint16_t, ph);
+      }
+      l[rb] = l[rb] * alpha + sum;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][rb][i] *= alpha;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          pb[rb][tt][e] = uint32_t(hbits[8 * tt + 2 * e]) | (uint32_t(hbits[8 * tt + 2 * e + 1]) << 16);
+    }
+
+    // O^T[d][row] += V^T[d][key] . P^T[key][row]
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int d = 32 * db + n;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const u32x4 a = vs[d * 8 + ((4 * w + 2 * tt + g) ^ v_swz(d))];
+        o[db][0] = mfma_pv(a, pb[0][tt], o[db][0]);
+        o[db][1] = mfma_pv(a, pb[1][tt], o[db][1]);
+      }
+    }
+
+    __syncthreads();
+    if (tn >= 0) {
+      store_tile();
+      __syncthreads();
+    }
+    t = tn;
+  }
+
+  // ---- merge the two waves' partial states; wave w finishes row block w
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) l[rb] += __shfl_xor(l[rb], 32, 64);
+  float* mo = reinterpret_cast<float*>(lds);    // [dest wave][NDB][16][64]
+  float* mm = mo + 2 * NDB * 16 * 64;           // [dest wave][64]
+  float* ml = mm + 2 * 64;                      // [dest wave][64]
+  const int dest = 1 - w;
+  __syncthreads();
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      mo[((dest * NDB + db) * 16 + i) * 64 + lane] = (w == 0) ? o[db][1][i] : o[db][0][i];
+  mm[dest * 64 + lane] = (w == 0) ? m[1] : m[0];
+  ml[dest * 64 + lane] = (w == 0) ? l[1] : l[0];
+  __syncthreads();
+
+  const float m_self = (w == 0) ? m[0] : m[1];
+  const float l_self = (w == 0) ? l[0] : l[1];
+  const float m_oth = mm[w * 64 + lane];
+  const float l_oth = ml[w * 64 + lane];
+  const float mt = fmaxf(m_self, m_oth);
+  const float f0 = __builtin_amdgcn_exp2f(m_self - mt);
+  const float f1 = __builtin_amdgcn_exp2f(m_oth - mt);
+  const float lt = l_self * f0 + l_oth * f1;
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  const float s0 = f0 * inv, s1 = f1 * inv;
+
+  const int row = q0 + 32 * w + n;
+  if (row < P.s_q) {
+    const int64_t obase = b * P.o_sb + int64_t(h) * P.o_sh + int64_t(row) * P.o_ss;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        float v4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * qd + e;
+          const float self = (w == 0) ? o[db][0][i] : o[db][1][i];
+          v4[e] = self * s0 + mo[((w * NDB + db) * 16 + i) * 64 + lane] * s1;
+        }
+        const int d = 32 * db + 8 * qd + 4 * g;
+        if constexpr (OUT_F32) {
+          store_out4<float>(reinterpret_cast<float*>(P.o) + obase + d, v4[0], v4[1], v4[2], v4[3]);
+        } else {
+          store_out4_16<T>(reinterpret_cast<uint16_t*>(P.o) + obase + d, v4[0], v4[1], v4[2], v4[3]);
+        }
+      }
+    }
+  }
+}
+
+template <typename T, bool OUT_F32, int D>
+static hipError_t launch_attn_t(const AttnParams& p, hipStream_t st) {
+  const int64_t items = int64_t(p.n_qb) * p.batch * p.heads;
+  hipLaunchKernelGGL((attn_kernel<T, OUT_F32, D>), dim3(uint32_t(items)), dim3(128), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T, bool OUT_F32>
+static hipError_t launch_attn_d(const AttnParams& p, int D, hipStream_t st) {
+  if (D == 64) return launch_attn_t<T, OUT_F32, 64>(p, st);
+  if (D == 96) return launch_attn_t<T, OUT_F32, 96>(p, st);
+  return launch_attn_t<T, OUT_F32, 128>(p, st);
+}
+
+hipError_t launch_attention(const AttnParams& p, int dtype, int out_dtype, int D,
+                            hipStream_t st) {
+  const bool f32 = out_dtype == 3;
+  if (dtype == Bf16::id)
+    return f32 ? launch_attn_d<Bf16, true>(p, D, st) : launch_attn_d<Bf16, false>(p, D, st);
+  return f32 ? launch_attn_d<F16, true>(p, D, st) : launch_attn_d<F16, false>(p, D, st);
+}
+
+}  // namespace msa

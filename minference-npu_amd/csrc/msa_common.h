@@ -1,0 +1,56 @@
+// Shared device helpers for the MI355X (gfx950) sparse prefill attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace msa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlock = 64;      // token block == q tile == k tile
+constexpr int kMaxHeads = 128;  // head descriptors carried in the kernel arguments
+
+// Element tags for the 16-bit input types.
+struct Bf16 {
+  static constexpr int id = 1;
+  __device__ static float to_float(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+  // Round-to-nearest-even fp32 -> bf16 (finite inputs).
+  __device__ static uint16_t from_float(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u) return uint16_t(u >> 16);  // inf/nan pass through
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+  }
+};
+
+struct F16 {
+  static constexpr int id = 2;
+  __device__ static float to_float(uint16_t b) {
+    return float(__builtin_bit_cast(_Float16, b));
+  }
+  __device__ static uint16_t from_float(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+};
+
+// 16-bit to fp16, saturating at the fp16 finite range.
+template <typename T>
+__device__ inline _Float16 to_f16_sat(uint16_t b) {
+  float f = T::to_float(b);
+  f = fminf(fmaxf(f, -65504.0f), 65504.0f);
+  return static_cast<_Float16>(f);
+}
+
+__device__ inline u32x4 zero_u32x4() { return u32x4{0u, 0u, 0u, 0u}; }
+
+__device__ inline u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ inline void store16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+}  // namespace msa

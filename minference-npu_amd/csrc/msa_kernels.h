@@ -1,0 +1,74 @@
+// Kernel parameter blocks and launchers shared by the C ABI (msa_abi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "msa_common.h"
+
+namespace msa {
+
+struct PoolParams {
+  const void* q;
+  const void* k;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t s_q, s_k;
+  int n_qb, n_kb;
+  int batch, n_slots, kv_group;
+  float* q_pool;   // [batch*n_slots][n_qb][D]
+  float* k_poolT;  // [batch*n_slots][D][n_kb]
+  int16_t slot_heads[kMaxHeads];  // head of q for each slot (kernel-argument copy)
+};
+
+struct ScoreParams {
+  const float* q_pool;
+  const float* k_poolT;
+  int32_t* idx;  // [batch*n_slots][n_qb][topk_max]
+  int32_t* cnt;  // [batch*n_slots][n_qb]
+  int n_qb, n_kb, topk_max, batch, n_slots;
+  float scale;
+  int16_t slot_topk[kMaxHeads];
+};
+
+struct HeadArg {
+  int16_t kind;
+  int16_t slot;
+  int32_t p1;  // stream: n_init
+  int32_t p2;  // stream: n_local
+  float scale_log2;  // softmax scale * log2(e)
+};
+
+struct AttnParams {
+  const void* q;
+  const void* k;
+  const uint16_t* vt;  // [batch*kv_heads][D][s_pad] fp16, keys permuted within 16
+  void* o;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int batch, heads, kv_group, s_q, s_k, n_qb, n_kb, s_pad;
+  const int32_t* idx;
+  const int32_t* cnt;
+  int idx_slots, topk_max;
+  int xcd_heads;  // 0: plain order; else heads per XCD (order taken from head_order)
+  int16_t head_order[kMaxHeads];  // batch*heads <= kMaxHeads when xcd_heads != 0
+  HeadArg hd[kMaxHeads];
+};
+
+struct VtParams {
+  const void* v;
+  int64_t v_sb, v_sh, v_ss;
+  uint16_t* vt;
+  int batch, kv_heads, s_k, s_pad;
+};
+
+hipError_t launch_pool(const PoolParams& p, int dtype, int D, hipStream_t st);
+hipError_t launch_score(const ScoreParams& p, int D, hipStream_t st);
+int score_rows_for(int n_kb);
+size_t score_smem_bytes(int R, int D, int n_kb);
+hipError_t launch_vt(const VtParams& p, int dtype, int D, hipStream_t st);
+hipError_t launch_attention(const AttnParams& p, int dtype, int out_dtype, int D,
+                            hipStream_t st);
+
+}  // namespace msa

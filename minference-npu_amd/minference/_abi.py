@@ -1,0 +1,274 @@
+"""ctypes binding of libmsa.so (C ABI declared in include/msa.h).
+
+The library is loaded from ``minference/_lib/libmsa.so`` (built in-tree by
+``minference._build``).  There is no fallback: if the library or a GPU is
+missing, every op raises.  Torch is used only to own device memory and to
+name the current HIP stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional, Sequence
+
+import torch
+
+from ._build import LIB_PATH
+
+# status codes (include/msa.h)
+MSA_OK = 0
+MSA_E_NULL = -1
+MSA_E_RANK = -2
+MSA_E_DTYPE = -3
+MSA_E_HEAD_DIM = -4
+MSA_E_ALIGN = -5
+MSA_E_BLOCK = -6
+MSA_E_TOPK = -7
+MSA_E_HEADS = -8
+MSA_E_WORKSPACE = -9
+MSA_E_SEQ = -10
+MSA_E_SLOTS = -11
+
+MSA_DTYPE_BF16 = 1
+MSA_DTYPE_FP16 = 2
+MSA_DTYPE_FP32 = 3
+
+MSA_KIND_DENSE = 0
+MSA_KIND_STREAM = 1
+MSA_KIND_BLOCK = 2
+
+MSA_MAX_HEADS = 128
+MSA_BLOCK = 64
+ABI_VERSION = 1
+
+_DTYPE_CODE = {
+    torch.bfloat16: MSA_DTYPE_BF16,
+    torch.float16: MSA_DTYPE_FP16,
+    torch.float32: MSA_DTYPE_FP32,
+}
+
+# every symbol include/msa.h declares
+EXPORTED_SYMBOLS = (
+    "msa_abi_version",
+    "msa_status_str",
+    "msa_estimate_workspace_bytes",
+    "msa_block_estimate",
+    "msa_attention_workspace_bytes",
+    "msa_layer_attention",
+)
+
+
+class MsaTensor4(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("size", ctypes.c_int64 * 4),
+        ("stride", ctypes.c_int64 * 4),
+        ("dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class MsaHeadDesc(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("p1", ctypes.c_int32),
+        ("p2", ctypes.c_int32),
+        ("slot", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class MsaError(RuntimeError):
+    """Raised for a non-zero status from libmsa."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"libmsa status {status}: {message}")
+        self.status = status
+
+
+_LIB = None
+_LIB_LOCK = threading.Lock()
+
+
+def library_path() -> str:
+    return os.environ.get("MINFERENCE_MSA_LIB", LIB_PATH)
+
+
+def load_library() -> ctypes.CDLL:
+    """Load libmsa.so once; raises ImportError with the build command if absent."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    with _LIB_LOCK:
+        if _LIB is not None:
+            return _LIB
+        path = library_path()
+        if not os.path.exists(path):
+            raise ImportError(
+                f"libmsa.so not found at {path}; build it with "
+                "`python -m minference._build` (run from minference-npu_amd/)"
+            )
+        lib = ctypes.CDLL(path)
+        lib.msa_abi_version.restype = ctypes.c_int
+        lib.msa_abi_version.argtypes = []
+        lib.msa_status_str.restype = ctypes.c_char_p
+        lib.msa_status_str.argtypes = [ctypes.c_int]
+        lib.msa_estimate_workspace_bytes.restype = ctypes.c_size_t
+        lib.msa_estimate_workspace_bytes.argtypes = [
+            ctypes.c_int64, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+        ]
+        lib.msa_block_estimate.restype = ctypes.c_int
+        lib.msa_block_estimate.argtypes = [
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.msa_attention_workspace_bytes.restype = ctypes.c_size_t
+        lib.msa_attention_workspace_bytes.argtypes = [
+            ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+        ]
+        lib.msa_layer_attention.restype = ctypes.c_int
+        lib.msa_layer_attention.argtypes = [
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.POINTER(MsaHeadDesc), ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        ver = lib.msa_abi_version()
+        if ver != ABI_VERSION:
+            raise ImportError(f"libmsa ABI version {ver} != expected {ABI_VERSION}")
+        _LIB = lib
+        return lib
+
+
+def status_str(status: int) -> str:
+    return load_library().msa_status_str(int(status)).decode()
+
+
+def check(status: int) -> None:
+    if status == MSA_OK:
+        return
+    msg = status_str(status)
+    if status < 0:
+        raise ValueError(f"libmsa rejected the call (status {status}): {msg}")
+    raise MsaError(status, msg)
+
+
+def tensor4(t: torch.Tensor) -> MsaTensor4:
+    if t.dim() != 4:
+        raise ValueError(f"expected a 4-D [B,H,S,D] tensor, got {t.dim()}-D")
+    code = _DTYPE_CODE.get(t.dtype)
+    if code is None:
+        raise TypeError(f"unsupported dtype {t.dtype}")
+    d = MsaTensor4()
+    d.data = t.data_ptr()
+    for i in range(4):
+        d.size[i] = int(t.shape[i])
+        d.stride[i] = int(t.stride(i))
+    d.dtype = code
+    return d
+
+
+def require_device(*tensors: torch.Tensor) -> None:
+    """The MI355X path has no CPU fallback: inputs must live on the GPU."""
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(
+                "minference (MI355X build) runs on the GPU only; got a tensor on "
+                f"{t.device}.  Move q/k/v to the HIP device."
+            )
+    dev = tensors[0].device
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise RuntimeError("q, k and v must be on the same device")
+
+
+def current_stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def estimate_workspace_bytes(batch: int, n_slots: int, s_q: int, s_k: int, head_dim: int) -> int:
+    return int(load_library().msa_estimate_workspace_bytes(batch, n_slots, s_q, s_k, head_dim))
+
+
+def attention_workspace_bytes(batch: int, kv_heads: int, s_k: int, head_dim: int) -> int:
+    return int(load_library().msa_attention_workspace_bytes(batch, kv_heads, s_k, head_dim))
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Caller-owned workspace (256-byte aligned by the caching allocator)."""
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def block_estimate(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    slot_heads: Sequence[int],
+    slot_topk: Sequence[int],
+    topk_max: int,
+    score_scale: float,
+    idx: torch.Tensor,
+    cnt: torch.Tensor,
+    ws: Optional[torch.Tensor] = None,
+) -> None:
+    """Launch msa_block_estimate on the current stream (no sync)."""
+    lib = load_library()
+    n_slots = len(slot_heads)
+    if len(slot_topk) != n_slots:
+        raise ValueError("slot_topk must have one entry per slot")
+    heads_arr = (ctypes.c_int32 * max(n_slots, 1))(*[int(h) for h in slot_heads])
+    topk_arr = (ctypes.c_int32 * max(n_slots, 1))(*[int(t) for t in slot_topk])
+    need = estimate_workspace_bytes(q.shape[0], n_slots, q.shape[2], k.shape[2], q.shape[3])
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, q.device)
+    qd, kd = tensor4(q), tensor4(k)
+    st = lib.msa_block_estimate(
+        ctypes.byref(qd), ctypes.byref(kd), heads_arr, topk_arr, n_slots, MSA_BLOCK,
+        int(topk_max),
+        float(score_scale), idx.data_ptr(), cnt.data_ptr(), ws.data_ptr(), ws.numel(),
+        current_stream_handle(q.device),
+    )
+    check(st)
+
+
+def layer_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    out: torch.Tensor,
+    heads: Sequence[tuple],
+    idx: Optional[torch.Tensor] = None,
+    cnt: Optional[torch.Tensor] = None,
+    idx_slots: int = 0,
+    topk_max: int = 0,
+    ws: Optional[torch.Tensor] = None,
+) -> None:
+    """Launch msa_layer_attention.  ``heads`` = [(kind, p1, p2, slot, scale)] * H."""
+    lib = load_library()
+    n = len(heads)
+    arr = (MsaHeadDesc * max(n, 1))()
+    for i, (kind, p1, p2, slot, scale) in enumerate(heads):
+        arr[i].kind = int(kind)
+        arr[i].p1 = int(p1)
+        arr[i].p2 = int(p2)
+        arr[i].slot = int(slot)
+        arr[i].scale = float(scale)
+    need = attention_workspace_bytes(k.shape[0], k.shape[1], k.shape[2], k.shape[3])
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, q.device)
+    qd, kd, vd, od = tensor4(q), tensor4(k), tensor4(v), tensor4(out)
+    st = lib.msa_layer_attention(
+        ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ctypes.byref(od),
+        arr, n,
+        idx.data_ptr() if idx is not None else None,
+        cnt.data_ptr() if cnt is not None else None,
+        int(idx_slots), int(topk_max), ws.data_ptr(), ws.numel(),
+        current_stream_handle(q.device),
+    )
+    check(st)

@@ -1,0 +1,250 @@
+"""Patched attention forward: per-head pattern dispatch in one launch per layer.
+
+Drop-in for MInference-NPU/minference/modules/minference_forward.py:
+  init_minference_parameters  :175-213  (per-layer pattern load)
+  minference_forward          :258-502  (the patched forward)
+The reference groups heads by (type, params) and runs gather -> op -> scatter
+per group (:398-487).  Here the layer's heads become a descriptor table
+(LayerPlan); the block_sparse heads share one estimator launch and all heads
+share one attention launch that writes the output in [B, S, H, D] order, so
+the o_proj input needs no transpose copy.
+
+Written against the installed transformers (5.x): the attention module gets
+``position_embeddings`` from the model and returns a 2-tuple.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+import warnings
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from .. import _abi
+from ..ops.common import dense_scale, sparse_scale
+
+__all__ = [
+    "DEFAULT_PATTERN",
+    "LayerPlan",
+    "build_layer_plan",
+    "init_minference_parameters",
+    "load_layer_patterns",
+    "minference_forward",
+    "run_layer_attention",
+]
+
+# A head missing from the JSON gets this record (reference :229-231, :405-407).
+DEFAULT_PATTERN = ("vertical_and_slash", 1000, 6096, 1)
+
+_KIND = {
+    "dense": _abi.MSA_KIND_DENSE,
+    "stream_llm": _abi.MSA_KIND_STREAM,
+    "block_sparse": _abi.MSA_KIND_BLOCK,
+}
+
+
+def load_layer_patterns(config_path: str, layer_idx: int) -> Dict[int, list]:
+    """``{head: [type, p1, p2, score]}`` of one layer from the pattern JSON
+    (a list with one ``{"head": record}`` dict per layer; reference :187-198).
+    A missing file or layer yields ``{}``."""
+    if not config_path or not os.path.exists(config_path):
+        return {}
+    with open(config_path) as f:
+        all_patterns = json.load(f)
+    if layer_idx < len(all_patterns):
+        return {int(h): rec for h, rec in all_patterns[layer_idx].items()}
+    return {}
+
+
+@dataclass(frozen=True)
+class LayerPlan:
+    """Head descriptor table of one layer for a given K length.
+
+    heads[h] = (kind, p1, p2, slot, scale) as passed to msa_layer_attention;
+    block_heads[s] / block_topk[s] = head and clamped top-k of estimator slot s.
+    """
+
+    heads: Tuple[tuple, ...]
+    block_heads: Tuple[int, ...]
+    block_topk: Tuple[int, ...]
+    topk_max: int
+    all_dense: bool
+
+
+def build_layer_plan(patterns: Dict[int, Sequence], n_heads: int, head_dim: int,
+                     s_k: int, layer_idx: Optional[int] = None) -> LayerPlan:
+    """Per-head semantics of the reference dispatcher (:404-419, :228-250):
+
+    * ``stream_llm``  : p1 = n_init, p2 = n_local, scale (padded D)**-0.5
+    * ``block_sparse``: p1 = top-k key blocks, clamped to [1, n_k_blocks],
+                        scale (padded D)**-0.5 (selector and attention)
+    * ``dense``       : causal dense, scale 1/sqrt(D)
+    * ``vertical_and_slash`` (also the default for a missing head) is not part
+      of this build and raises NotImplementedError; unknown types raise
+      ValueError as in the reference (:416-419).
+    """
+    n_kb = max(1, math.ceil(s_k / _abi.MSA_BLOCK))
+    s_sparse = sparse_scale(head_dim)
+    s_dense = dense_scale(head_dim)
+    heads: List[tuple] = []
+    block_heads: List[int] = []
+    block_topk: List[int] = []
+    for h in range(n_heads):
+        rec = patterns.get(h, DEFAULT_PATTERN)
+        ty, p1, p2 = rec[0], rec[1], rec[2]
+        if ty == "stream_llm":
+            heads.append((_abi.MSA_KIND_STREAM, int(p1), int(p2), -1, s_sparse))
+        elif ty == "block_sparse":
+            k = min(max(1, int(p1)), n_kb)
+            heads.append((_abi.MSA_KIND_BLOCK, k, 0, len(block_heads), s_sparse))
+            block_heads.append(h)
+            block_topk.append(k)
+        elif ty == "dense":
+            heads.append((_abi.MSA_KIND_DENSE, 0, 0, -1, s_dense))
+        elif ty == "vertical_and_slash":
+            raise NotImplementedError(
+                f"pattern 'vertical_and_slash' (layer={layer_idx} head={h}) is not part of "
+                "the MI355X build; use stream_llm / block_sparse / dense patterns"
+            )
+        else:
+            raise ValueError(f"unknown best_pattern type {ty!r} (layer={layer_idx} head={h})")
+    return LayerPlan(
+        heads=tuple(heads),
+        block_heads=tuple(block_heads),
+        block_topk=tuple(block_topk),
+        topk_max=max(block_topk) if block_topk else 0,
+        all_dense=all(hd[0] == _abi.MSA_KIND_DENSE for hd in heads),
+    )
+
+
+def dense_plan(n_heads: int, head_dim: int, scale: Optional[float] = None) -> LayerPlan:
+    s = dense_scale(head_dim) if scale is None else float(scale)
+    return LayerPlan(
+        heads=tuple((_abi.MSA_KIND_DENSE, 0, 0, -1, s) for _ in range(n_heads)),
+        block_heads=(), block_topk=(), topk_max=0, all_dense=True,
+    )
+
+
+def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: LayerPlan,
+                        out: torch.Tensor) -> torch.Tensor:
+    """Estimator launch (if any block head) + one attention launch for all heads.
+
+    q [B, H, S_q, D]; k/v [B, H_kv, S_k, D] (H % H_kv == 0, no repeat_kv copy);
+    out any [B, H, S_q, D] view with D contiguous (bf16/fp16 or fp32).
+    """
+    _abi.require_device(q, k, v)
+    B, H, S_q, _ = q.shape
+    idx = cnt = None
+    n_slots = len(plan.block_heads)
+    if n_slots:
+        n_qb = math.ceil(S_q / _abi.MSA_BLOCK)
+        idx = torch.empty((B, n_slots, n_qb, plan.topk_max), dtype=torch.int32, device=q.device)
+        cnt = torch.empty((B, n_slots, n_qb), dtype=torch.int32, device=q.device)
+        s_sparse = sparse_scale(q.shape[-1])
+        _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max, s_sparse,
+                            idx, cnt)
+    _abi.layer_attention(q, k, v, out, plan.heads, idx=idx, cnt=cnt, idx_slots=n_slots,
+                         topk_max=plan.topk_max)
+    return out
+
+
+def init_minference_parameters(self) -> None:
+    """Per-layer one-time setup (reference :175-213): reads starting_layer,
+    is_search, config_path and the attn type injected by the patch, and loads
+    this layer's patterns."""
+    if getattr(self, "_minference_initialized", False):
+        return
+    config = self.config.to_dict()
+    self.starting_layer = config.get("starting_layer", 0)
+    self.is_search = config.get("is_search", False)
+    self.config_path = config.get("config_path", "")
+    self._minference_attn_type = config.get("minference_attn_type", "minference")
+    self.best_pattern = load_layer_patterns(self.config_path, self.layer_idx)
+    self._minference_plans = {}
+    self._minference_initialized = True
+
+
+def _layer_plan(self, n_heads: int, head_dim: int, s_k: int) -> LayerPlan:
+    key = (n_heads, head_dim, s_k)
+    plan = self._minference_plans.get(key)
+    if plan is None:
+        plan = build_layer_plan(self.best_pattern, n_heads, head_dim, s_k, self.layer_idx)
+        self._minference_plans[key] = plan
+    return plan
+
+
+def _apply_rope(self, q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    from importlib import import_module
+
+    rope = getattr(import_module(self.__class__.__module__), "apply_rotary_pos_emb")
+    return rope(q, k, cos, sin)
+
+
+def minference_forward():
+    """Returns the forward bound onto each attention module by the patch."""
+
+    def forward(
+        self,
+        hidden_states: torch.Tensor,
+        position_embeddings: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+        attention_mask: Optional[torch.Tensor] = None,
+        past_key_values=None,
+        **kwargs,
+    ):
+        if past_key_values is None:
+            past_key_values = kwargs.pop("past_key_value", None)
+        self.init_minference_parameters()
+        cfg = self.config
+        bsz, q_len, _ = hidden_states.shape
+        n_heads = cfg.num_attention_heads
+        n_kv = cfg.num_key_value_heads
+        hd = self.head_dim
+
+        if "q_proj" in self._modules:
+            query = self.q_proj(hidden_states)
+            key = self.k_proj(hidden_states)
+            value = self.v_proj(hidden_states)
+        else:
+            qkv = self.qkv_proj(hidden_states)
+            qp = n_heads * hd
+            kp = n_kv * hd
+            query, key, value = qkv[..., :qp], qkv[..., qp:qp + kp], qkv[..., qp + kp:]
+        query = query.view(bsz, q_len, n_heads, hd).transpose(1, 2)
+        key = key.view(bsz, q_len, n_kv, hd).transpose(1, 2)
+        value = value.view(bsz, q_len, n_kv, hd).transpose(1, 2)
+
+        if position_embeddings is None:
+            position_embeddings = kwargs.get("position_embeddings")
+        if position_embeddings is None:
+            raise ValueError("position_embeddings (cos, sin) are required")
+        cos, sin = position_embeddings
+        query, key = _apply_rope(self, query, key, cos, sin)
+
+        if past_key_values is not None and hasattr(past_key_values, "update"):
+            key, value = past_key_values.update(key, value, self.layer_idx)
+
+        if self.is_search:
+            warnings.warn("is_search=True is not supported by the MI355X build; running the "
+                          "configured patterns", stacklevel=2)
+
+        # output written in [B, S, H, D] order; the kernel sees a [B, H, S, D] view
+        out_bshd = torch.empty((bsz, q_len, n_heads, hd), dtype=query.dtype,
+                               device=query.device)
+        out = out_bshd.transpose(1, 2)
+        if q_len == 1:
+            plan = dense_plan(n_heads, hd)  # decode: one query row sees every key
+        elif self._minference_attn_type == "dense" or self.layer_idx < self.starting_layer:
+            plan = dense_plan(n_heads, hd)
+        else:
+            plan = _layer_plan(self, n_heads, hd, key.shape[2])
+        run_layer_attention(query, key, value, plan, out)
+
+        attn_output = out_bshd.reshape(bsz, q_len, n_heads * hd)
+        attn_output = self.o_proj(attn_output)
+        return attn_output, None
+
+    return forward

@@ -1,0 +1,169 @@
+"""block_sparse attention on MI355X: GPU block top-k estimator + gather-free
+block-sparse flash kernel.
+
+Drop-in for MInference-NPU/minference/ops/block_sparse_kernel_npu.py:
+  block_sparse_attention                 :609-709
+  _select_block_sparse_topk_indices      :230-263
+  _block_sparse_tilelang_npu_with_indices :452-601 (fixed-index kernel call)
+The kernel walks each (head, 64-row query block)'s id list directly; there is
+no fold of heads into the batch, no token-index expansion and no padding of
+small head counts.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from .. import _abi
+from .common import check_bnsd, check_supported, head_chunks, kernel_view, make_out, sparse_scale
+
+__all__ = [
+    "block_sparse_attention",
+    "select_block_sparse_topk_indices",
+    "block_sparse_attention_with_indices",
+]
+
+_DEFAULT_BLOCK_SIZE = 64
+
+
+def _check_block_size(block_size: int) -> None:
+    if int(block_size) != _abi.MSA_BLOCK:
+        raise NotImplementedError(
+            f"block_size={block_size}: the MI355X kernels use 64-token blocks only"
+        )
+
+
+def _estimate(q: torch.Tensor, k: torch.Tensor, topk: int):
+    """Run the estimator for every head of q.
+
+    Returns a list of (h0, h1, idx, cnt) per head chunk of at most
+    MSA_MAX_HEADS heads, idx/cnt int32 contiguous [B, h1-h0, n_qb(, topk)].
+    """
+    B, H, S_q, _ = q.shape
+    n_qb = math.ceil(S_q / _abi.MSA_BLOCK)
+    scale = sparse_scale(q.shape[-1])
+    chunks = []
+    for h0, h1 in head_chunks(H):
+        n = h1 - h0
+        idx = torch.empty((B, n, n_qb, topk), dtype=torch.int32, device=q.device)
+        cnt = torch.empty((B, n, n_qb), dtype=torch.int32, device=q.device)
+        _abi.block_estimate(
+            q[:, h0:h1], k[:, h0:h1], list(range(n)), [topk] * n, topk, scale, idx, cnt
+        )
+        chunks.append((h0, h1, idx, cnt))
+    return chunks
+
+
+def select_block_sparse_topk_indices(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    topk_blocks: int,
+    block_size: int = _DEFAULT_BLOCK_SIZE,
+    *,
+    return_counts: bool = False,
+):
+    """Selected K-block ids per query block, ``[B, H, n_q_blocks, topk]`` int64.
+
+    Same pooling, scale and block-causal rule as the reference selector
+    (:230-263).  The first ``min(topk, bq+1)`` ids of each row are the chosen
+    causal blocks ascending (ties -> lower id).  The remaining slots (rows
+    with fewer causal blocks than ``topk``) hold the next future ids; the
+    reference fills them with ``torch.topk``'s choice among ``-inf`` scores,
+    and the token-level causal mask discards them in both implementations.
+    With ``return_counts=True`` also returns the per-row causal counts.
+    """
+    check_bnsd(q, k)
+    check_supported(q, k)
+    _check_block_size(block_size)
+    q, k = kernel_view(q), kernel_view(k)
+    n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
+    topk = min(max(1, int(topk_blocks)), n_kb)
+    chunks = _estimate(q, k, topk)
+    idx = torch.cat([c[2] for c in chunks], dim=1).long()
+    if return_counts:
+        return idx, torch.cat([c[3] for c in chunks], dim=1).long()
+    return idx
+
+
+# reference-private name kept for drop-in callers and tests
+_select_block_sparse_topk_indices = select_block_sparse_topk_indices
+
+
+def block_sparse_attention_with_indices(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    block_indices: torch.Tensor,
+    block_size: int = _DEFAULT_BLOCK_SIZE,
+    *,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Block-sparse attention for a fixed ``[B, H, n_q_blocks, topk]`` id tensor
+    (the kernel call of :452-601, minus its fp16-only and fold-into-batch
+    restrictions).  Ids outside [0, n_k_blocks) are ignored; duplicated ids
+    count once; future blocks are removed by the token causal mask."""
+    check_bnsd(q, k, v)
+    check_supported(q, k, v)
+    _check_block_size(block_size)
+    B, H, S_q, _ = q.shape
+    n_qb = math.ceil(S_q / _abi.MSA_BLOCK)
+    if tuple(block_indices.shape[:3]) != (B, H, n_qb):
+        raise ValueError(
+            "block_indices shape must be [B,H,n_q_blocks,topk_blocks]; "
+            f"got {tuple(block_indices.shape)} for q={tuple(q.shape)} block_size={block_size}"
+        )
+    q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
+    idx = torch.sort(block_indices.to(device=q.device, dtype=torch.int32), dim=-1).values
+    topk = idx.shape[-1]
+    chunks = []
+    for h0, h1 in head_chunks(H):
+        cnt = torch.full((B, h1 - h0, n_qb), topk, dtype=torch.int32, device=q.device)
+        chunks.append((h0, h1, idx[:, h0:h1].contiguous(), cnt))
+    result = make_out(q, out)
+    return _run(q, k, v, chunks, topk, result)
+
+
+def _run(q, k, v, chunks, topk, result):
+    scale = sparse_scale(q.shape[-1])
+    for h0, h1, idx, cnt in chunks:
+        n = h1 - h0
+        heads = [(_abi.MSA_KIND_BLOCK, topk, 0, s, scale) for s in range(n)]
+        _abi.layer_attention(
+            q[:, h0:h1], k[:, h0:h1], v[:, h0:h1], result[:, h0:h1], heads,
+            idx=idx, cnt=cnt, idx_slots=n, topk_max=topk,
+        )
+    return result
+
+
+def block_sparse_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    topk_blocks: int,
+    block_size: int = _DEFAULT_BLOCK_SIZE,
+    *,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Block-sparse causal attention.
+
+    Args:
+        q, k, v:     ``[B, H, S, D]`` (BNSD), RoPE applied, ``repeat_kv``-ed.
+        topk_blocks: K blocks kept per query block (clamped to >= 1 and to the
+                     number of K blocks, as in the reference).
+        block_size:  must be 64.
+        out:         optional output (q's dtype or float32).
+
+    Returns ``[B, H, S, D]`` in q's dtype (or ``out``).
+    """
+    check_bnsd(q, k, v)
+    check_supported(q, k, v)
+    _check_block_size(block_size)
+    q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
+    n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
+    topk = min(max(1, int(topk_blocks)), n_kb)
+    chunks = _estimate(q, k, topk)
+    result = make_out(q, out)
+    return _run(q, k, v, chunks, topk, result)

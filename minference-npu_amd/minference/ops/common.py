@@ -1,0 +1,100 @@
+"""Shared host helpers for the MI355X ops (argument checks, scale rule, output)."""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from .. import _abi
+
+# Head dims the reference pads to before computing the sparse-op scale
+# (minference/ops/streaming_kernel_npu.py:70-86; block_sparse_kernel_npu.py:56, 95-101).
+ALLOWED_HEAD_DIMS = (16, 32, 64, 128, 256, 512)
+
+SUPPORTED_HEAD_DIMS = (64, 96, 128)
+SUPPORTED_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def next_allowed_head_dim(d: int) -> int:
+    for cand in ALLOWED_HEAD_DIMS:
+        if cand >= d:
+            return cand
+    raise ValueError(
+        f"head_dim={d} exceeds the largest supported value {ALLOWED_HEAD_DIMS[-1]}"
+    )
+
+
+def sparse_scale(head_dim: int) -> float:
+    """Scale of stream_llm / block_sparse heads.  The reference zero-pads
+    head_dim to the next allowed size *before* computing 1/sqrt(D)
+    (streaming_kernel_npu.py:114 after :377-381; block_sparse_kernel_npu.py:254,
+    340 after :651-656), so Phi-3 (D=96) uses 128**-0.5.  Padding with zeros
+    does not change q.k, so the kernels run on the unpadded D with this scale."""
+    return next_allowed_head_dim(head_dim) ** -0.5
+
+
+def dense_scale(head_dim: int) -> float:
+    """dense_attention's default 1/sqrt(D), unpadded (backend_npu/attention.py:210-211)."""
+    return 1.0 / math.sqrt(head_dim)
+
+
+def check_bnsd(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor] = None) -> None:
+    """Rank / shape checks with the reference's AssertionError contract
+    (streaming_kernel_npu.py:369-372, block_sparse_kernel_npu.py:640-643)."""
+    assert q.dim() == 4, f"q must be 4-D [B,H,S,D], got {q.dim()}-D"
+    assert (
+        q.shape[0] == k.shape[0] and q.shape[1] == k.shape[1] and q.shape[-1] == k.shape[-1]
+    ), f"q/k B/H/D mismatch; q={tuple(q.shape)} k={tuple(k.shape)}"
+    if v is not None:
+        assert v.shape == k.shape, f"v shape {tuple(v.shape)} != k shape {tuple(k.shape)}"
+
+
+def check_supported(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor] = None) -> None:
+    tensors = (q, k) if v is None else (q, k, v)
+    _abi.require_device(*tensors)
+    for t in tensors:
+        if t.dtype not in SUPPORTED_DTYPES:
+            raise NotImplementedError(
+                f"the MI355X kernels take bf16 or fp16 inputs, got {t.dtype}"
+            )
+    if len({t.dtype for t in tensors}) != 1:
+        raise ValueError("q, k and v must share one dtype")
+    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
+        raise NotImplementedError(
+            f"head_dim={q.shape[-1]} is not supported by the MI355X kernels "
+            f"(supported: {SUPPORTED_HEAD_DIMS})"
+        )
+    if q.shape[2] > k.shape[2]:
+        raise ValueError(
+            f"prefill attention requires S_q <= S_k, got S_q={q.shape[2]}, S_k={k.shape[2]}"
+        )
+
+
+def kernel_view(t: torch.Tensor) -> torch.Tensor:
+    """A view the kernels can read in place (D contiguous, 16-byte rows)."""
+    if t.stride(-1) != 1 or (t.data_ptr() % 16) != 0 or any(
+        (t.stride(i) * t.element_size()) % 16 for i in range(3) if t.shape[i] > 1
+    ):
+        return t.contiguous()
+    return t
+
+
+def make_out(q: torch.Tensor, out: Optional[torch.Tensor]) -> torch.Tensor:
+    if out is None:
+        return torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if out.shape != q.shape:
+        raise ValueError(f"out shape {tuple(out.shape)} != q shape {tuple(q.shape)}")
+    if out.dtype not in (q.dtype, torch.float32):
+        raise ValueError(f"out dtype must be {q.dtype} or float32, got {out.dtype}")
+    if out.device != q.device:
+        raise ValueError("out must be on q's device")
+    return out
+
+
+def head_chunks(n_heads: int):
+    """Head ranges of at most MSA_MAX_HEADS per library call."""
+    step = _abi.MSA_MAX_HEADS
+    for h0 in range(0, n_heads, step):
+        yield h0, min(n_heads, h0 + step)

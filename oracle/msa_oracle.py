@@ -1,0 +1,346 @@
+"""numpy restatement of the reference's sparse prefill attention semantics.
+
+TEST INFRASTRUCTURE ONLY: the checker, never the thing measured or shipped.
+
+Reference files (paths relative to /root/reference/MInference-NPU/):
+  streaming  : minference/ops/streaming_kernel_npu.py:94-146 (CPU path), :349-397 (entry)
+  block      : minference/ops/block_sparse_kernel_npu.py:230-263 (selector),
+               :266-317 (token mask), :325-348 (CPU path), :609-709 (entry)
+  dense      : minference/backend_npu/attention.py:166-189 (CPU path), :192-255 (entry)
+  dispatch   : minference/modules/minference_forward.py:384-487
+
+Parity pins (each function is checked by tests/test_oracle.py against
+something other than its own formula):
+  pool_blocks         : torch's bf16/fp16 ``mean(dim=3)`` (the library call the
+                        reference makes), bit for bit
+  block_scores /
+  select_topk         : brute-force pure-Python loops; sortedness and causal
+                        count invariants (tests/test_block_sparse_kernel.py:186-211
+                        in the reference); constructed known answers (monotone
+                        scores, exact ties); torch.topk on torch.matmul scores
+                        with a near-tie exemption
+  streaming_attention : per-row brute force (reference tests/test_streaming_kernel.py:79-117);
+                        Q = 0 closed form (uniform mean over the visible set);
+                        n_local >= S equals causal dense; LSE-merge identity
+  block_sparse_from_indices : full top-k equals causal dense; Q = 0 closed form;
+                        per-row brute force over the expanded token set
+  dense_causal        : torch scaled_dot_product_attention(is_causal=True) in fp64
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Sequence
+
+import numpy as np
+
+__all__ = [
+    "ALLOWED_HEAD_DIMS",
+    "next_allowed_head_dim",
+    "sparse_scale",
+    "dense_scale",
+    "bf16_round",
+    "f16_round",
+    "round_to",
+    "pool_blocks",
+    "block_scores",
+    "select_topk",
+    "select_block_sparse_topk_indices",
+    "stream_visible",
+    "streaming_attention",
+    "block_token_visible",
+    "block_sparse_from_indices",
+    "dense_causal",
+    "masked_attention",
+    "layer_attention",
+    "stream_pairs",
+    "block_tiles",
+    "causal_pairs",
+]
+
+BLOCK = 64
+ALLOWED_HEAD_DIMS = (16, 32, 64, 128, 256, 512)
+
+
+# ---------------------------------------------------------------------------
+# scale quirk
+# ---------------------------------------------------------------------------
+def next_allowed_head_dim(d: int) -> int:
+    """Head dims are zero-padded to the next of (16, 32, 64, 128, 256, 512)
+    before the sparse ops compute their scale
+    (streaming_kernel_npu.py:70-86, 377-381; block_sparse_kernel_npu.py:95-101, 651-656)."""
+    for cand in ALLOWED_HEAD_DIMS:
+        if cand >= d:
+            return cand
+    raise ValueError(f"head_dim={d} exceeds {ALLOWED_HEAD_DIMS[-1]}")
+
+
+def sparse_scale(d: int) -> float:
+    """Softmax (and selector score) scale of stream_llm / block_sparse heads:
+    Dp ** -0.5 with Dp the padded dim (streaming_kernel_npu.py:114;
+    block_sparse_kernel_npu.py:254, 340).  Zero padding leaves q.k unchanged,
+    so only the scale differs from the unpadded computation."""
+    return next_allowed_head_dim(d) ** -0.5
+
+
+def dense_scale(d: int) -> float:
+    """dense_attention's default scale 1/sqrt(D) on unpadded D (attention.py:210-211)."""
+    return 1.0 / math.sqrt(d)
+
+
+# ---------------------------------------------------------------------------
+# rounding
+# ---------------------------------------------------------------------------
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 round-to-nearest-even, returned as float32 values."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    nonfinite = (u & 0x7F800000) == 0x7F800000
+    r = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    r = np.where(nonfinite, u & 0xFFFF0000, r).astype(np.uint32)
+    return r.view(np.float32)
+
+
+def f16_round(x: np.ndarray) -> np.ndarray:
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return bf16_round(x)
+    if dtype == "fp16":
+        return f16_round(x)
+    if dtype == "fp32":
+        return np.asarray(x, dtype=np.float32)
+    raise ValueError(dtype)
+
+
+# ---------------------------------------------------------------------------
+# block selector (block_sparse_kernel_npu.py:230-263)
+# ---------------------------------------------------------------------------
+def pool_blocks(x: np.ndarray, dtype: str, block: int = BLOCK) -> np.ndarray:
+    """Mean over consecutive ``block`` rows of x [..., S, D] in the input dtype.
+
+    The last partial block is zero padded and still divided by ``block``
+    (F.pad then reshape().mean(dim=3), :240-251).  The sum is formed in fp64
+    (exact for 16-bit inputs), rounded to fp32, divided by ``block`` and
+    rounded to the input dtype, which is what torch's CPU bf16/fp16 mean
+    produces; the result is returned as float32 (the ``.to(fp32)`` at :251).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    S = x.shape[-2]
+    pad = (-S) % block
+    if pad:
+        widths = [(0, 0)] * (x.ndim - 2) + [(0, pad), (0, 0)]
+        x = np.pad(x, widths)
+    nb = x.shape[-2] // block
+    xr = x.reshape(*x.shape[:-2], nb, block, x.shape[-1]).astype(np.float64)
+    s = xr.sum(axis=-2).astype(np.float32)
+    mean = (s * np.float32(1.0 / block)).astype(np.float32)
+    return round_to(mean, dtype)
+
+
+def block_scores(q_pool: np.ndarray, k_pool: np.ndarray, scale: float) -> np.ndarray:
+    """fp32 pooled scores q_pool . k_pool^T * scale with the block-causal mask
+    (bk > bq -> -inf, q-block frame) of :253-260.  The dot product is formed
+    in fp64 and rounded once to fp32 (exact for 16-bit pooled operands)."""
+    s = np.matmul(q_pool.astype(np.float64), np.swapaxes(k_pool.astype(np.float64), -1, -2))
+    s = s.astype(np.float32) * np.float32(scale)
+    n_bq, n_bk = s.shape[-2], s.shape[-1]
+    causal = np.arange(n_bq)[:, None] >= np.arange(n_bk)[None, :]
+    return np.where(causal, s, np.float32(-np.inf)).astype(np.float32)
+
+
+def select_topk(scores: np.ndarray, topk: int):
+    """Per query block: the ``topk`` largest scores, ties -> lower block id.
+
+    Returns (idx, cnt).  idx[..., bq, :cnt] are the selected causal ids
+    ascending (what torch.topk(...).indices.sort() yields on the causal part);
+    cnt = min(topk, bq + 1).  The reference fills the remaining slots with
+    -inf future ids chosen by torch.topk internals (:262-263); they are never
+    attended (token causal mask, :281-284), and here they are the next
+    future ids bq+1, bq+2, ... in ascending order.
+    """
+    *lead, n_bq, n_bk = scores.shape
+    topk = min(int(topk), n_bk)
+    flat = scores.reshape(-1, n_bq, n_bk)
+    idx = np.empty((flat.shape[0], n_bq, topk), dtype=np.int64)
+    cnt = np.empty((flat.shape[0], n_bq), dtype=np.int64)
+    for bq in range(n_bq):
+        n = min(bq + 1, n_bk)
+        c = min(topk, n)
+        row = flat[:, bq, :n]
+        # stable sort on -score keeps equal scores in ascending id order
+        order = np.argsort(-row.astype(np.float64), axis=-1, kind="stable")[:, :c]
+        sel = np.sort(order, axis=-1)
+        idx[:, bq, :c] = sel
+        if c < topk:
+            idx[:, bq, c:] = bq + 1 + np.arange(topk - c)
+        cnt[:, bq] = c
+    return idx.reshape(*lead, n_bq, topk), cnt.reshape(*lead, n_bq)
+
+
+def select_block_sparse_topk_indices(q: np.ndarray, k: np.ndarray, topk_blocks: int,
+                                     dtype: str, scale: float | None = None,
+                                     block: int = BLOCK):
+    """Full selector on [..., S, D] inputs (block_sparse_kernel_npu.py:230-263)."""
+    if scale is None:
+        scale = sparse_scale(q.shape[-1])
+    qp = pool_blocks(q, dtype, block)
+    kp = pool_blocks(k, dtype, block)
+    return select_topk(block_scores(qp, kp, scale), max(1, int(topk_blocks)))
+
+
+# ---------------------------------------------------------------------------
+# token visibility
+# ---------------------------------------------------------------------------
+def stream_visible(s_q: int, s_k: int, n_init: int, n_local: int) -> np.ndarray:
+    """visible(i, j) = j <= a and (j > a - n_local or j < n_init),
+    a = S_k - S_q + i (streaming_kernel_npu.py:127-136)."""
+    a = np.arange(s_k - s_q, s_k)[:, None]
+    j = np.arange(s_k)[None, :]
+    return (j <= a) & ((j > a - n_local) | (j < n_init))
+
+
+def block_token_visible(idx_row: np.ndarray, s_q: int, s_k: int, block: int = BLOCK) -> np.ndarray:
+    """Token mask of one head from block ids idx_row [n_bq, topk]
+    (block_sparse_kernel_npu.py:266-317; True = visible)."""
+    n_bq = idx_row.shape[0]
+    n_bk = -(-s_k // block)
+    attend = np.zeros((n_bq, n_bk), dtype=bool)
+    for bq in range(n_bq):
+        ids = idx_row[bq]
+        ids = ids[(ids >= 0) & (ids < n_bk)]
+        attend[bq, ids] = True
+    tok = np.repeat(np.repeat(attend, block, axis=0), block, axis=1)[:s_q, :s_k]
+    a = np.arange(s_k - s_q, s_k)[:, None]
+    j = np.arange(s_k)[None, :]
+    return tok & (j <= a)
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+def masked_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, visible: np.ndarray,
+                     scale: float, acc=np.float64) -> np.ndarray:
+    """softmax(q k^T * scale, masked) v with fully masked rows -> 0
+    (the reference's nan_to_num, streaming_kernel_npu.py:142,
+    block_sparse_kernel_npu.py:346).  q [S_q, D], k/v [S_k, D]."""
+    logits = (q.astype(acc) @ k.astype(acc).T) * acc(scale)
+    logits = np.where(visible, logits, -np.inf)
+    m = logits.max(axis=-1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0)
+    p = np.exp(logits - m)
+    den = p.sum(axis=-1, keepdims=True)
+    out = (p @ v.astype(acc)) / np.where(den > 0, den, 1.0)
+    return np.where(den > 0, out, 0.0).astype(acc)
+
+
+def _heads(x: np.ndarray):
+    """[B, H, S, D] -> iterator of (b, h)."""
+    B, H = x.shape[0], x.shape[1]
+    for b in range(B):
+        for h in range(H):
+            yield b, h
+
+
+def streaming_attention(q, k, v, n_init: int, n_local: int, scale: float | None = None,
+                        acc=np.float64, chunk_size_q: int | None = None) -> np.ndarray:
+    """stream_llm output for [B, H, S, D] inputs (streaming_kernel_npu.py:94-146),
+    chunked over queries with the reference's rule
+    chunk = max(64, min(S_q, 4M // S_k)) (:116-117)."""
+    if scale is None:
+        scale = sparse_scale(q.shape[-1])
+    B, H, s_q, D = q.shape
+    s_k = k.shape[2]
+    kvg = H // k.shape[1]
+    if chunk_size_q is None:
+        chunk_size_q = max(64, min(s_q, (4 * 1024 * 1024) // max(1, s_k)))
+    out = np.zeros((B, H, s_q, D), dtype=acc)
+    for b, h in _heads(q):
+        for c0 in range(0, s_q, chunk_size_q):
+            c1 = min(c0 + chunk_size_q, s_q)
+            a = np.arange(s_k - s_q + c0, s_k - s_q + c1)[:, None]
+            j = np.arange(s_k)[None, :]
+            vis = (j <= a) & ((j > a - n_local) | (j < n_init))
+            out[b, h, c0:c1] = masked_attention(q[b, h, c0:c1], k[b, h // kvg], v[b, h // kvg],
+                                                vis, scale, acc)
+    return out
+
+
+def block_sparse_from_indices(q, k, v, idx, scale: float | None = None,
+                              acc=np.float64) -> np.ndarray:
+    """Block-sparse attention for fixed block ids idx [B, H, n_bq, topk]
+    (reference tests/test_block_sparse_kernel.py:96-119 semantics; the ids
+    are expanded to tokens and intersected with the token causal mask)."""
+    if scale is None:
+        scale = sparse_scale(q.shape[-1])
+    B, H, s_q, D = q.shape
+    s_k = k.shape[2]
+    kvg = H // k.shape[1]
+    out = np.zeros((B, H, s_q, D), dtype=acc)
+    for b, h in _heads(q):
+        vis = block_token_visible(np.asarray(idx[b, h]), s_q, s_k)
+        out[b, h] = masked_attention(q[b, h], k[b, h // kvg], v[b, h // kvg], vis, scale, acc)
+    return out
+
+
+def dense_causal(q, k, v, scale: float | None = None, acc=np.float64) -> np.ndarray:
+    """Causal dense attention j <= i + (S_k - S_q) (attention.py:166-189)."""
+    if scale is None:
+        scale = dense_scale(q.shape[-1])
+    B, H, s_q, D = q.shape
+    s_k = k.shape[2]
+    kvg = H // k.shape[1]
+    a = np.arange(s_k - s_q, s_k)[:, None]
+    vis = np.arange(s_k)[None, :] <= a
+    out = np.zeros((B, H, s_q, D), dtype=acc)
+    for b, h in _heads(q):
+        out[b, h] = masked_attention(q[b, h], k[b, h // kvg], v[b, h // kvg], vis, scale, acc)
+    return out
+
+
+def layer_attention(q, k, v, patterns: Sequence[tuple], dtype: str,
+                    acc=np.float64):
+    """One patched layer (minference_forward.py:398-487): per head h,
+    patterns[h] = (type, p1, p2).  Returns (out, {head: (idx, cnt)})."""
+    B, H, s_q, D = q.shape
+    kvg = H // k.shape[1]
+    out = np.zeros((B, H, s_q, D), dtype=acc)
+    sel = {}
+    for h in range(H):
+        ty, p1, p2 = patterns[h][:3]
+        qh, kh, vh = q[:, h:h + 1], k[:, h // kvg:h // kvg + 1], v[:, h // kvg:h // kvg + 1]
+        if ty == "stream_llm":
+            out[:, h:h + 1] = streaming_attention(qh, kh, vh, int(p1), int(p2), acc=acc)
+        elif ty == "block_sparse":
+            idx, cnt = select_block_sparse_topk_indices(qh, kh, int(p1), dtype)
+            sel[h] = (idx, cnt)
+            out[:, h:h + 1] = block_sparse_from_indices(qh, kh, vh, idx, acc=acc)
+        elif ty == "dense":
+            out[:, h:h + 1] = dense_causal(qh, kh, vh, acc=acc)
+        else:
+            raise ValueError(f"unsupported pattern {ty!r}")
+    return out, sel
+
+
+# ---------------------------------------------------------------------------
+# algorithmic work (D unpadded)
+# ---------------------------------------------------------------------------
+def stream_pairs(s: int, n_init: int, n_local: int) -> int:
+    """Visible (query, key) pairs of one stream_llm head with S_q = S_k = s."""
+    i = np.arange(s, dtype=np.int64)
+    lo = np.maximum(0, i - n_local + 1)
+    return int(((i - lo + 1) + np.minimum(n_init, lo)).sum())
+
+
+def block_tiles(s: int, topk: int) -> int:
+    """Computed 64x64 tiles of one block_sparse head: sum_bq min(k, bq+1)."""
+    n_b = -(-s // BLOCK)
+    k = min(topk, n_b)
+    bq = np.arange(n_b, dtype=np.int64)
+    return int(np.minimum(k, bq + 1).sum())
+
+
+def causal_pairs(s: int) -> int:
+    return s * (s + 1) // 2

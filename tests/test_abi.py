@@ -1,0 +1,174 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+include/msa.h declares, and rejects bad arguments before any launch."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from minference import _abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "msa.h")
+
+FAKE = 0x10000  # never dereferenced: validation fails first
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(msa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_lists_expected_functions():
+    assert header_functions() == sorted(_abi.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_header_symbol():
+    lib = _abi.load_library()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_status_strings():
+    lib = _abi.load_library()
+    assert lib.msa_abi_version() == _abi.ABI_VERSION
+    for code in range(-11, 1):
+        s = _abi.status_str(code)
+        assert s and s != "unknown status"
+    assert _abi.status_str(-99) == "unknown status"
+
+
+def test_workspace_sizes():
+    # estimator: pooled Q + pooled K^T in fp32
+    assert _abi.estimate_workspace_bytes(1, 32, 16384, 16384, 96) == 32 * 512 * 96 * 4
+    assert _abi.estimate_workspace_bytes(1, 1, 100, 100, 64) == 1024  # 2*2*64*4 rounded to 256
+    # attention: V^T in fp16 padded to 64 keys
+    assert _abi.attention_workspace_bytes(1, 32, 65536, 96) == 32 * 96 * 65536 * 2
+    assert _abi.attention_workspace_bytes(1, 1, 65, 64) == 64 * 128 * 2
+    assert _abi.attention_workspace_bytes(0, 1, 65, 64) == 0
+
+
+def t4(shape, dtype=_abi.MSA_DTYPE_BF16, strides=None, data=FAKE):
+    d = _abi.MsaTensor4()
+    d.data = data
+    if strides is None:
+        strides = [shape[1] * shape[2] * shape[3], shape[2] * shape[3], shape[3], 1]
+    for i in range(4):
+        d.size[i] = shape[i]
+        d.stride[i] = strides[i]
+    d.dtype = dtype
+    return d
+
+
+def heads(n, kind=_abi.MSA_KIND_STREAM, slot=-1, scale=0.088):
+    arr = (_abi.MsaHeadDesc * n)()
+    for i in range(n):
+        arr[i].kind = kind
+        arr[i].p1 = 64
+        arr[i].p2 = 256
+        arr[i].slot = slot if slot >= 0 else -1
+        arr[i].scale = scale
+    return arr
+
+
+def attn(q, k, v, o, hd, n, idx=None, cnt=None, slots=0, topk=0, ws=FAKE, wsb=1 << 40):
+    lib = _abi.load_library()
+    return lib.msa_layer_attention(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v),
+                                   ctypes.byref(o), hd, n, idx, cnt, slots, topk, ws, wsb, None)
+
+
+def est(q, k, heads_list, topk_list, topk_max, scale=0.088, block=64, ws=FAKE, wsb=1 << 40,
+        idx=FAKE, cnt=FAKE):
+    lib = _abi.load_library()
+    n = len(heads_list)
+    ha = (ctypes.c_int32 * max(n, 1))(*heads_list)
+    ta = (ctypes.c_int32 * max(n, 1))(*topk_list) if topk_list is not None else None
+    return lib.msa_block_estimate(ctypes.byref(q), ctypes.byref(k), ha, ta, n, block, topk_max,
+                                  scale, idx, cnt, ws, wsb, None)
+
+
+SHAPE = [1, 4, 256, 96]
+
+
+@pytest.mark.parametrize(
+    "mutate,expected",
+    [
+        (lambda a: a.__setitem__("q", t4([1, 4, 256, 80])), _abi.MSA_E_RANK),
+        (lambda a: a.__setitem__("q", t4([1, 4, 256, 48]))
+         or a.__setitem__("k", t4([1, 4, 256, 48])) or a.__setitem__("v", t4([1, 4, 256, 48]))
+         or a.__setitem__("o", t4([1, 4, 256, 48])), _abi.MSA_E_HEAD_DIM),
+        (lambda a: a.__setitem__("q", t4(SHAPE, _abi.MSA_DTYPE_FP32)), _abi.MSA_E_DTYPE),
+        (lambda a: a.__setitem__("o", t4(SHAPE, _abi.MSA_DTYPE_FP16)), _abi.MSA_E_DTYPE),
+        (lambda a: a.__setitem__("k", t4(SHAPE, strides=[4 * 256 * 96, 256 * 96, 96, 2])), _abi.MSA_E_ALIGN),
+        (lambda a: a.__setitem__("q", t4(SHAPE, strides=[4 * 256 * 100, 256 * 100, 100, 1])), _abi.MSA_E_ALIGN),
+        (lambda a: a.__setitem__("q", t4(SHAPE, data=FAKE + 2)), _abi.MSA_E_ALIGN),
+        (lambda a: a.__setitem__("q", t4([1, 4, 512, 96])) or a.__setitem__("o", t4([1, 4, 512, 96])), _abi.MSA_E_SEQ),
+        (lambda a: a.__setitem__("n", 3), _abi.MSA_E_HEADS),
+        (lambda a: a.__setitem__("hd", heads(4, kind=7)), _abi.MSA_E_HEADS),
+        (lambda a: a.__setitem__("hd", heads(4, scale=0.0)), _abi.MSA_E_HEADS),
+        (lambda a: a.__setitem__("hd", heads(4, kind=_abi.MSA_KIND_BLOCK, slot=0)), _abi.MSA_E_SLOTS),
+        (lambda a: a.__setitem__("wsb", 100), _abi.MSA_E_WORKSPACE),
+        (lambda a: a.__setitem__("ws", None), _abi.MSA_E_WORKSPACE),
+        (lambda a: a.__setitem__("q", t4(SHAPE, data=0)), _abi.MSA_E_NULL),
+        (lambda a: a.__setitem__("k", t4([1, 3, 256, 96])) or a.__setitem__("v", t4([1, 3, 256, 96])), _abi.MSA_E_RANK),
+    ],
+)
+def test_attention_validation(mutate, expected):
+    a = {"q": t4(SHAPE), "k": t4(SHAPE), "v": t4(SHAPE), "o": t4(SHAPE), "hd": heads(4), "n": 4,
+         "ws": FAKE, "wsb": 1 << 40}
+    mutate(a)
+    assert attn(a["q"], a["k"], a["v"], a["o"], a["hd"], a["n"], ws=a["ws"], wsb=a["wsb"]) == expected
+
+
+def test_attention_block_slot_range():
+    hd = heads(4, kind=_abi.MSA_KIND_BLOCK, slot=0)
+    hd[3].slot = 4
+    st = attn(t4(SHAPE), t4(SHAPE), t4(SHAPE), t4(SHAPE), hd, 4, idx=FAKE, cnt=FAKE, slots=4, topk=2)
+    assert st == _abi.MSA_E_SLOTS
+
+
+@pytest.mark.parametrize(
+    "kw,expected",
+    [
+        ({"block": 32}, _abi.MSA_E_BLOCK),
+        ({"topk_max": 0}, _abi.MSA_E_TOPK),
+        ({"topk_max": 5}, _abi.MSA_E_TOPK),  # 256 tokens -> 4 blocks
+        ({"topk_list": [1, 9]}, _abi.MSA_E_TOPK),
+        ({"heads_list": [0, 4]}, _abi.MSA_E_HEADS),
+        ({"heads_list": []}, _abi.MSA_E_HEADS),
+        ({"scale": -1.0}, _abi.MSA_E_TOPK),
+        ({"wsb": 10}, _abi.MSA_E_WORKSPACE),
+        ({"idx": None}, _abi.MSA_E_NULL),
+    ],
+)
+def test_estimator_validation(kw, expected):
+    args = {"heads_list": [0, 1], "topk_list": [2, 2], "topk_max": 2}
+    args.update(kw)
+    if "topk_list" in kw or "heads_list" in kw:
+        n = len(args["heads_list"])
+        if "topk_list" not in kw:
+            args["topk_list"] = [2] * n
+    hl = args.pop("heads_list")
+    tl = args.pop("topk_list")
+    tm = args.pop("topk_max")
+    assert est(t4(SHAPE), t4(SHAPE), hl, tl, tm, **args) == expected
+
+
+def test_python_ops_refuse_cpu_tensors():
+    import torch
+
+    from minference import block_sparse_attention, dense_attention, streaming_forward
+
+    q = torch.randn(1, 2, 128, 96, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        streaming_forward(q, q, q, 64, 128)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        block_sparse_attention(q, q, q, 2)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        dense_attention(q, q, q)
+    with pytest.raises(AssertionError):
+        streaming_forward(q[0], q, q, 64, 128)

@@ -1,0 +1,216 @@
+"""GPU parity of the HIP kernels against the CPU oracle (small sizes).
+
+Bars: block ids bit-exact; attention outputs within 2e-3 max-abs when written
+in fp32 (bf16/fp16 inputs, fp32 accumulation); bf16 outputs within 2e-3 plus
+one bf16 rounding of the output.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from msa_data import dtype_tag, make_qkv, np32
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def to_dev(dev, *ts):
+    return [t.to(dev) for t in ts]
+
+
+def assert_close_f32(out: torch.Tensor, ref: np.ndarray, tol=TOL, what=""):
+    got = out.detach().float().cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    err = np.abs(got - ref).max()
+    assert err < tol, f"{what}: max abs err {err:.3e} >= {tol}"
+    return err
+
+
+def assert_close_lowp(out: torch.Tensor, ref: np.ndarray, what=""):
+    got = out.detach().float().cpu().numpy().astype(np.float64)
+    bound = TOL + np.abs(ref) * 2.0 ** -8
+    bad = np.abs(got - ref) > bound
+    assert not bad.any(), f"{what}: {bad.sum()} elements outside 2e-3 + bf16 rounding"
+
+
+# ---------------------------------------------------------------------------
+# estimator: bit-exact block ids
+# ---------------------------------------------------------------------------
+EST_CASES = [
+    # (B, H, S_q, S_k, D, topk, dtype, sink)
+    (1, 4, 1024, 1024, 96, 4, torch.bfloat16, None),
+    (2, 3, 1000, 1000, 96, 3, torch.bfloat16, 8.0),
+    (1, 2, 4096 + 17, 4096 + 17, 96, 16, torch.bfloat16, 8.0),
+    (1, 2, 2048, 2048, 64, 100, torch.bfloat16, None),
+    (1, 2, 2048, 2048, 128, 7, torch.float16, None),
+    (1, 4, 640, 640, 96, 1, torch.float16, 8.0),
+    (1, 2, 512, 1024, 96, 5, torch.bfloat16, None),
+]
+
+
+@pytest.mark.parametrize("case", EST_CASES, ids=[str(c[:6]) + dtype_tag(c[6]) for c in EST_CASES])
+def test_estimator_bit_exact(gpu_device, case):
+    from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
+
+    B, H, S_q, S_k, D, topk, dtype, sink = case
+    q, k, _ = make_qkv(B, H, S_q, S_k, D, dtype, seed=S_q + topk, sink_scale=sink)
+    idx, cnt = select_block_sparse_topk_indices(*to_dev(gpu_device, q, k), topk, return_counts=True)
+    ridx, rcnt = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, dtype_tag(dtype))
+    got_i = idx.cpu().numpy()
+    got_c = cnt.cpu().numpy()
+    assert got_i.shape == ridx.shape
+    assert np.array_equal(got_c, rcnt)
+    assert np.array_equal(got_i, ridx), f"{(got_i != ridx).sum()} ids differ"
+
+
+def test_estimator_ties_to_lower_id(gpu_device):
+    from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
+
+    S, D = 64 * 40, 96
+    blk = torch.randn(64, D)
+    k = blk.repeat(40, 1)[None, None].repeat(1, 2, 1, 1).to(torch.bfloat16)
+    q = torch.randn(1, 2, S, D).to(torch.bfloat16)
+    idx, cnt = select_block_sparse_topk_indices(*to_dev(gpu_device, q, k), 5, return_counts=True)
+    idx = idx.cpu().numpy()
+    for bq in range(40):
+        c = min(5, bq + 1)
+        assert list(idx[0, 0, bq, :c]) == list(range(c))
+
+
+# ---------------------------------------------------------------------------
+# stream_llm
+# ---------------------------------------------------------------------------
+STREAM_CASES = [
+    # (n_init, n_local, S_q, S_k, D, dtype)
+    (64, 512, 256, 256, 96, torch.bfloat16),      # S_k <= n_local: causal dense
+    (4, 8, 9, 9, 96, torch.bfloat16),
+    (0, 16, 32, 64, 96, torch.bfloat16),
+    (128, 512, 512, 1024, 96, torch.bfloat16),
+    (128, 256, 256, 512, 64, torch.float16),
+    (400, 128, 128, 512, 128, torch.bfloat16),
+    (64, 1, 128, 256, 96, torch.bfloat16),
+    (128, 1024, 4096, 4096, 96, torch.bfloat16),
+    (100, 800, 3000, 3000, 96, torch.bfloat16),
+    (0, 0, 200, 200, 96, torch.bfloat16),         # nothing visible: zeros
+]
+
+
+@pytest.mark.parametrize("case", STREAM_CASES, ids=[str(c[:5]) + dtype_tag(c[5]) for c in STREAM_CASES])
+def test_streaming_vs_oracle(gpu_device, case):
+    from minference import streaming_forward
+
+    n_init, n_local, s_q, s_k, D, dtype = case
+    q, k, v = make_qkv(1, 4, s_q, s_k, D, dtype, seed=42 + s_q)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    streaming_forward(dq, dk, dv, n_init, n_local, out=out32)
+    ref = O.streaming_attention(np32(q), np32(k), np32(v), n_init, n_local)
+    assert_close_f32(out32, ref, what=f"stream {case}")
+    out = streaming_forward(dq, dk, dv, n_init, n_local)
+    assert out.dtype == dtype and out.shape == q.shape
+    assert_close_lowp(out, ref, what=f"stream lowp {case}")
+
+
+# ---------------------------------------------------------------------------
+# block_sparse
+# ---------------------------------------------------------------------------
+BLOCK_CASES = [
+    # (B, H, S, D, topk, dtype, sink)
+    (1, 4, 1024, 96, 4, torch.bfloat16, 8.0),
+    (2, 2, 1000, 96, 3, torch.bfloat16, None),
+    (1, 2, 2048, 64, 100, torch.bfloat16, None),   # topk > n_blocks: causal dense
+    (1, 2, 2048, 128, 8, torch.float16, 8.0),
+    (1, 4, 4096, 96, 16, torch.bfloat16, 8.0),
+]
+
+
+@pytest.mark.parametrize("case", BLOCK_CASES, ids=[str(c[:5]) + dtype_tag(c[5]) for c in BLOCK_CASES])
+def test_block_sparse_vs_oracle(gpu_device, case):
+    from minference import block_sparse_attention
+
+    B, H, S, D, topk, dtype, sink = case
+    q, k, v = make_qkv(B, H, S, S, D, dtype, seed=11 + S, sink_scale=sink)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    block_sparse_attention(dq, dk, dv, topk, out=out32)
+    idx, _ = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, dtype_tag(dtype))
+    ref = O.block_sparse_from_indices(np32(q), np32(k), np32(v), idx)
+    assert_close_f32(out32, ref, what=f"block {case}")
+    out = block_sparse_attention(dq, dk, dv, topk)
+    assert out.dtype == dtype
+    assert_close_lowp(out, ref, what=f"block lowp {case}")
+
+
+def test_block_fixed_indices_with_future_and_duplicates(gpu_device):
+    from minference.ops.block_sparse_kernel import block_sparse_attention_with_indices
+
+    B, H, S, D, topk = 1, 3, 1024, 96, 6
+    q, k, v = make_qkv(B, H, S, S, D, torch.bfloat16, seed=5)
+    n = S // 64
+    g = np.random.default_rng(0)
+    idx = g.integers(-2, n + 3, size=(B, H, n, topk))  # out of range, future, duplicates
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    block_sparse_attention_with_indices(dq, dk, dv, torch.from_numpy(idx), out=out32)
+    ref = O.block_sparse_from_indices(np32(q), np32(k), np32(v), idx)
+    assert_close_f32(out32, ref, what="fixed indices")
+
+
+# ---------------------------------------------------------------------------
+# dense
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("s_q,s_k,D,dtype", [(1024, 1024, 96, torch.bfloat16),
+                                             (300, 700, 96, torch.bfloat16),
+                                             (1, 500, 96, torch.bfloat16),
+                                             (512, 512, 128, torch.float16),
+                                             (2000, 2000, 64, torch.bfloat16)])
+def test_dense_vs_oracle(gpu_device, s_q, s_k, D, dtype):
+    from minference import dense_attention
+
+    q, k, v = make_qkv(1, 3, s_q, s_k, D, dtype, seed=s_q)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    dense_attention(dq, dk, dv, out=out32)
+    ref = O.dense_causal(np32(q), np32(k), np32(v))
+    assert_close_f32(out32, ref, what="dense")
+
+
+# ---------------------------------------------------------------------------
+# one mixed layer through the dispatcher plan; strided (HF-like) views; GQA
+# ---------------------------------------------------------------------------
+def _mixed_patterns(H):
+    kinds = [("stream_llm", 64, 256), ("block_sparse", 5, 0), ("dense", 0, 0),
+             ("block_sparse", 2, 0), ("stream_llm", 0, 128), ("block_sparse", 100, 0)]
+    return {h: list(kinds[h % len(kinds)]) + [1.0] for h in range(H)}
+
+
+@pytest.mark.parametrize("S,H,H_kv", [(1024, 8, 8), (1000, 8, 2), (2048, 16, 16)])
+def test_mixed_layer_strided_views(gpu_device, S, H, H_kv):
+    from minference.modules.minference_forward import build_layer_plan, run_layer_attention
+
+    D = 96
+    pats = _mixed_patterns(H)
+    q, k, v = make_qkv(1, H, S, S, D, torch.bfloat16, seed=S + H, sink_scale=8.0)
+    k, v = k[:, :H_kv].contiguous(), v[:, :H_kv].contiguous()
+    # fused [B, S, (H + 2 H_kv) D] buffer and BNSD views into it, as HF's qkv_proj split
+    fused = torch.cat([q.transpose(1, 2).reshape(1, S, H * D),
+                       k.transpose(1, 2).reshape(1, S, H_kv * D),
+                       v.transpose(1, 2).reshape(1, S, H_kv * D)], dim=-1).to(gpu_device)
+    dq = fused[..., :H * D].view(1, S, H, D).transpose(1, 2)
+    dk = fused[..., H * D:(H + H_kv) * D].view(1, S, H_kv, D).transpose(1, 2)
+    dv = fused[..., (H + H_kv) * D:].view(1, S, H_kv, D).transpose(1, 2)
+    plan = build_layer_plan(pats, H, D, S)
+    out_bshd = torch.empty((1, S, H, D), dtype=torch.float32, device=gpu_device)
+    run_layer_attention(dq, dk, dv, plan, out_bshd.transpose(1, 2))
+    rep = H // H_kv
+    kr = np.repeat(np32(k), rep, axis=1)
+    vr = np.repeat(np32(v), rep, axis=1)
+    ref, _ = O.layer_attention(np32(q), kr, vr, [pats[h] for h in range(H)], "bf16")
+    assert_close_f32(out_bshd.transpose(1, 2), ref, what=f"mixed layer S={S} H={H} Hkv={H_kv}")
