@@ -1,0 +1,336 @@
+#!/usr/bin/env python3
+"""Sparse prefill attention benchmark: one Phi-3-mini layer on one MI355X.
+
+A step = the whole sparse attention of one layer, all heads, inputs resident
+in HBM: one estimator launch (block top-k for the block_sparse heads), one V
+staging launch and one attention launch.  QKV projection, RoPE and o_proj are
+outside the step (the reference's per-layer attention, BASELINE.json metric).
+
+Default workload ("headline"): S = 65536, 32 heads x 96, bf16, every head
+sparse, 16 stream_llm(n_init 128, n_local 4096) + 16 block_sparse(top-100)
+heads (seeded head assignment).  Q, K, V ~ N(0,1) from a seeded generator,
+RoPE theta 1e4 on Q and K, K rows 0-3 scaled 8x (attention sinks).
+
+Printed JSON line: value = algorithmic TFLOP/s of the whole step; roofline =
+the attention kernel alone (HIP events on the launch stream) against the
+bf16 MFMA peak; dense = same-GPU dense attention on the same tensors
+(PyTorch SDPA flash and this build's dense kind); cpu_baseline = the oracle's
+stream_llm restatement of the reference CPU path timed on
+the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "minference-npu_amd"), os.path.join(ROOT, "tests")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (no sparsity)
+BLOCK = 64
+
+WORKLOADS = {
+    # name: (S, n_stream, n_block, n_dense, n_init, n_local, topk)
+    "headline": (65536, 16, 16, 0, 128, 4096, 100),
+    "cfg2_block16k": (16384, 0, 32, 0, 128, 4096, 100),
+    "cfg3_stream64k": (65536, 32, 0, 0, 128, 4096, 100),
+}
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="headline")
+    ap.add_argument("--heads", type=int, default=32)
+    ap.add_argument("--dim", type=int, default=96)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-dense", action="store_true", help="skip the same-GPU dense baselines")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-heads", type=int, default=16,
+                    help="heads of BASELINE config 1 timed on the CPU (scaled to 32)")
+    return ap.parse_args()
+
+
+def stream_pairs(s, n_init, n_local):
+    import numpy as np
+
+    i = np.arange(s, dtype=np.int64)
+    lo = np.maximum(0, i - n_local + 1)
+    return int(((i - lo + 1) + np.minimum(n_init, lo)).sum())
+
+
+def block_tiles(s, topk):
+    nb = -(-s // BLOCK)
+    k = min(topk, nb)
+    return sum(min(k, b + 1) for b in range(nb))
+
+
+def make_inputs(S, H, D, seed, device):
+    import torch
+
+    from msa_data import rope
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    out = []
+    for name in ("q", "k", "v"):
+        x = torch.randn(1, H, S, D, generator=g, device=device, dtype=torch.float32)
+        if name != "v":
+            # RoPE by 4096-row slabs to bound the fp32 temporaries
+            for s0 in range(0, S, 4096):
+                x[:, :, s0:s0 + 4096] = rope(x[:, :, s0:s0 + 4096], offset=s0)
+        if name == "k":
+            x[:, :, :4] *= 8.0
+        out.append(x.to(torch.bfloat16))
+        del x
+    return out
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(n_heads_sample):
+    """BASELINE config 1 on the host: stream_llm, B=1, 32 heads, S=4096,
+    D=96, fp32, n_init=64, n_local=1024, through the oracle's restatement of
+    the reference CPU path (streaming_kernel_npu.py:94-146, same chunking).
+    Warmup 1 head, then 3 timed repeats over ``n_heads_sample`` heads, scaled
+    to 32 heads."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+    from msa_data import make_qkv, np32
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    S, D, n_init, n_local = 4096, 96, 64, 1024
+    q, k, v = make_qkv(1, n_heads_sample, S, S, D, torch.float32, seed=0)
+    q, k, v = np32(q), np32(k), np32(v)
+    O.streaming_attention(q[:, :1], k[:, :1], v[:, :1], n_init, n_local, acc=np.float32)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.streaming_attention(q, k, v, n_init, n_local, acc=np.float32)
+        times.append(time.perf_counter() - t0)
+    per_layer = (sum(times) / len(times)) * 32 / n_heads_sample
+    flops = 32 * stream_pairs(S, n_init, n_local) * 4 * D
+    return {
+        "value": round(flops / per_layer / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"BASELINE config 1 (stream_llm S=4096 n_init=64 n_local=1024 D=96 fp32) via the "
+                   f"oracle's numpy restatement of the reference CPU path; {n_heads_sample} of 32 "
+                   f"heads x 3 repeats, scaled to 32 heads"),
+        "ms_per_layer": round(per_layer * 1e3, 2),
+        "ms_min_max": [round(min(times) * 32 / n_heads_sample * 1e3, 2),
+                       round(max(times) * 32 / n_heads_sample * 1e3, 2)],
+        "cpu_model": cpu_model(),
+        "logical_cpus": os.cpu_count(),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
+              "multi-GPU path (heads would shard across GPUs with no communication inside "
+              "attention).", file=sys.stderr)
+        sys.exit(1)
+
+    import torch
+
+    from minference import _abi
+    from minference.modules.minference_forward import build_layer_plan
+    from minference.ops.common import sparse_scale
+
+    dev = torch.device("cuda:0")
+    S, n_stream, n_block, n_dense, n_init, n_local, topk = WORKLOADS[args.workload]
+    H, D = args.heads, args.dim
+    scale_h = H / (n_stream + n_block + n_dense)
+    n_stream, n_block = int(round(n_stream * scale_h)), int(round(n_block * scale_h))
+    n_dense = H - n_stream - n_block
+    kinds = (["stream_llm"] * n_stream + ["block_sparse"] * n_block + ["dense"] * n_dense)
+    import random
+
+    random.Random(args.seed).shuffle(kinds)
+    pats = {}
+    for h, kd in enumerate(kinds):
+        pats[h] = {"stream_llm": ["stream_llm", n_init, n_local, 1.0],
+                   "block_sparse": ["block_sparse", topk, 0, 1.0],
+                   "dense": ["dense", 0, 0, 1.0]}[kd]
+    plan = build_layer_plan(pats, H, D, S)
+
+    q, k, v = make_inputs(S, H, D, args.seed, dev)
+    out = torch.empty_like(q)
+    n_qb = math.ceil(S / BLOCK)
+    n_slots = len(plan.block_heads)
+    idx = torch.empty((1, max(n_slots, 1), n_qb, max(plan.topk_max, 1)), dtype=torch.int32, device=dev)
+    cnt = torch.empty((1, max(n_slots, 1), n_qb), dtype=torch.int32, device=dev)
+    ws_est = _abi.workspace(_abi.estimate_workspace_bytes(1, max(n_slots, 1), S, S, D), dev)
+    ws_att = _abi.workspace(_abi.attention_workspace_bytes(1, H, S, D), dev)
+    s_sparse = sparse_scale(D)
+    stream = torch.cuda.current_stream(dev)
+
+    def launch_est():
+        if n_slots:
+            _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max,
+                                s_sparse, idx, cnt, ws_est)
+
+    def launch_stage():
+        _abi.stage_v(v, ws_att)
+
+    def launch_attn():
+        _abi.layer_attention(q, k, v, out, plan.heads, idx=idx if n_slots else None,
+                             cnt=cnt if n_slots else None, idx_slots=n_slots,
+                             topk_max=plan.topk_max, ws=ws_att, staged=True)
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+
+    def step(e=None):
+        if e:
+            e[0].record(stream)
+        launch_est()
+        if e:
+            e[1].record(stream)
+        launch_stage()
+        if e:
+            e[2].record(stream)
+        launch_attn()
+        if e:
+            e[3].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(ev[i])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    t_est = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    t_stage = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    t_attn = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+
+    flop_stream = n_stream * stream_pairs(S, n_init, n_local) * 4 * D
+    flop_block = n_block * block_tiles(S, topk) * 4 * BLOCK * BLOCK * D
+    flop_dense_heads = n_dense * (S * (S + 1) // 2) * 4 * D
+    flop = flop_stream + flop_block + flop_dense_heads
+    achieved_attn = flop / (t_attn * 1e-3) / 1e12
+    value = flop / (ms_step * 1e-3) / 1e12
+    est_bytes = 2 * n_slots * S * D * 2 + n_slots * n_qb * (plan.topk_max + 1) * 4
+
+    result = {
+        "metric": "sparse prefill attn ms/layer + effective TFLOP/s (% MFMA peak) vs dense, Phi-3 64K",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) Q/K/V, RoPE, K rows 0-3 x8)",
+        "config": {
+            "workload": args.workload,
+            "model": "Phi-3-mini layer attention (32 heads x 96)",
+            "seq_len": S,
+            "heads": H,
+            "head_dim": D,
+            "mix": {"stream_llm(%d,%d)" % (n_init, n_local): n_stream,
+                    "block_sparse(top-%d)" % topk: n_block, "dense": n_dense},
+            "global_batch": 1,
+            "parallelism": "single GPU",
+        },
+        "ms_per_layer": round(ms_step, 4),
+        "pct_mfma_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "algorithmic_flop": flop,
+        "kernels_ms": {"estimator": round(t_est, 4), "stage_v": round(t_stage, 4),
+                       "attention": round(t_attn, 4)},
+        "estimator_gbps": round(est_bytes / (t_est * 1e-3) / 1e9, 1) if n_slots else None,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved_attn, 3),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved_attn / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "kernel": "msa::attn_kernel<Bf16,false,96>",
+        },
+    }
+
+    if not args.no_dense:
+        result["dense"] = dense_baselines(q, k, v, S, H, D, ms_step)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_heads)
+    print(json.dumps(result), flush=True)
+
+
+def dense_baselines(q, k, v, S, H, D, ms_sparse):
+    """Same-GPU dense causal attention on the same tensors: PyTorch SDPA
+    (flash / memory-efficient backends only) and this build's dense kind."""
+    import torch
+    import torch.nn.functional as F
+
+    from minference import _abi
+
+    flop = H * (S * (S + 1) // 2) * 4 * D
+    res = {"flop": flop}
+
+    def timeit(fn, reps=3):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / reps
+
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            ms = timeit(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True))
+        res["sdpa_ms"] = round(ms, 3)
+        res["sdpa_tflops"] = round(flop / (ms * 1e-3) / 1e12, 2)
+        res["speedup_vs_sdpa"] = round(ms / ms_sparse, 2)
+    except Exception as e:  # noqa: BLE001
+        res["sdpa_error"] = f"{type(e).__name__}: {e}"[:200]
+    torch.cuda.empty_cache()
+
+    out = torch.empty_like(q)
+    ws = _abi.workspace(_abi.attention_workspace_bytes(1, H, S, D), q.device)
+    heads = [(_abi.MSA_KIND_DENSE, 0, 0, -1, 1.0 / math.sqrt(D))] * H
+    ms = timeit(lambda: _abi.layer_attention(q, k, v, out, heads, ws=ws))
+    res["own_dense_ms"] = round(ms, 3)
+    res["own_dense_tflops"] = round(flop / (ms * 1e-3) / 1e12, 2)
+    res["speedup_vs_own_dense"] = round(ms / ms_sparse, 2)
+    return res
+
+
+if __name__ == "__main__":
+    main()

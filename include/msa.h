@@ -135,6 +135,23 @@ int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k,
                         int32_t topk_max, void* workspace, size_t workspace_bytes,
                         msa_stream_t stream);
 
+/* The two launches msa_layer_attention makes, callable separately (so a
+ * caller can time the attention kernel alone, or reuse one staged V^T):
+ *   msa_stage_v: V [B][H_kv][S_k][D] -> fp16 V^T in the workspace
+ *                (msa_attention_workspace_bytes bytes);
+ *   msa_layer_attention_staged: same arguments and checks as
+ *                msa_layer_attention, reads V^T staged by msa_stage_v from
+ *                the same workspace on the same stream (v gives shapes only).
+ * Same reference counterpart as msa_layer_attention. */
+int msa_stage_v(const msa_tensor4* v, void* workspace, size_t workspace_bytes,
+                msa_stream_t stream);
+int msa_layer_attention_staged(const msa_tensor4* q, const msa_tensor4* k,
+                               const msa_tensor4* v, const msa_tensor4* o,
+                               const msa_head_desc* heads, int32_t n_heads,
+                               const int32_t* idx, const int32_t* cnt,
+                               int32_t idx_slots, int32_t topk_max, void* workspace,
+                               size_t workspace_bytes, msa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

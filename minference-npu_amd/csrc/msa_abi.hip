@@ -157,11 +157,43 @@ size_t msa_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t s_
   return size_t((bytes + 255) / 256 * 256);
 }
 
-int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
-                        const msa_tensor4* o, const msa_head_desc* heads, int32_t n_heads,
-                        const int32_t* idx, const int32_t* cnt, int32_t idx_slots,
-                        int32_t topk_max, void* workspace, size_t workspace_bytes,
-                        msa_stream_t stream) {
+static int stage_v(const msa_tensor4* v, void* workspace, size_t workspace_bytes,
+                   hipStream_t hs) {
+  if (!v || !v->data) return MSA_E_NULL;
+  for (int i = 0; i < 4; ++i)
+    if (v->size[i] <= 0) return MSA_E_RANK;
+  if (v->dtype != MSA_DTYPE_BF16 && v->dtype != MSA_DTYPE_FP16) return MSA_E_DTYPE;
+  if (!head_dim_ok(v->size[3])) return MSA_E_HEAD_DIM;
+  if (!aligned(v)) return MSA_E_ALIGN;
+  if (v->size[2] > kMaxSeq) return MSA_E_SEQ;
+  const int64_t B = v->size[0], Hkv = v->size[1], Sk = v->size[2];
+  const int D = int(v->size[3]);
+  if (B * Hkv > 65535) return MSA_E_HEADS;
+  const size_t need = msa_attention_workspace_bytes(B, Hkv, Sk, D);
+  if (!workspace || workspace_bytes < need) return MSA_E_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
+  VtParams vp;
+  vp.v = v->data;
+  vp.v_sb = v->stride[0]; vp.v_sh = v->stride[1]; vp.v_ss = v->stride[2];
+  vp.vt = static_cast<uint16_t*>(workspace);
+  vp.batch = int(B);
+  vp.kv_heads = int(Hkv);
+  vp.s_k = int(Sk);
+  vp.s_pad = int(cdiv(Sk, MSA_BLOCK) * MSA_BLOCK);
+  const hipError_t e = launch_vt(vp, v->dtype, D, hs);
+  return e == hipSuccess ? MSA_OK : int(e);
+}
+
+int msa_stage_v(const msa_tensor4* v, void* workspace, size_t workspace_bytes,
+                msa_stream_t stream) {
+  return stage_v(v, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
+                                const msa_tensor4* o, const msa_head_desc* heads, int32_t n_heads,
+                                const int32_t* idx, const int32_t* cnt, int32_t idx_slots,
+                                int32_t topk_max, void* workspace, size_t workspace_bytes,
+                                msa_stream_t stream, bool stage) {
   int st = check_qk(q, k);
   if (st != MSA_OK) return st;
   if (!v || !o || !v->data || !o->data || !heads) return MSA_E_NULL;
@@ -199,17 +231,10 @@ int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_te
 
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   uint16_t* vt = static_cast<uint16_t*>(workspace);
-
-  VtParams vp;
-  vp.v = v->data;
-  vp.v_sb = v->stride[0]; vp.v_sh = v->stride[1]; vp.v_ss = v->stride[2];
-  vp.vt = vt;
-  vp.batch = int(B);
-  vp.kv_heads = int(Hkv);
-  vp.s_k = int(Sk);
-  vp.s_pad = n_kb * MSA_BLOCK;
-  hipError_t e = launch_vt(vp, v->dtype, D, hs);
-  if (e != hipSuccess) return int(e);
+  if (stage) {
+    st = stage_v(v, workspace, workspace_bytes, hs);
+    if (st != MSA_OK) return st;
+  }
 
   AttnParams ap;
   memset(&ap, 0, sizeof(ap));
@@ -287,8 +312,26 @@ int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_te
     ap.xcd_heads = 0;
   }
 
-  e = launch_attention(ap, q->dtype, o->dtype, D, hs);
+  const hipError_t e = launch_attention(ap, q->dtype, o->dtype, D, hs);
   return e == hipSuccess ? MSA_OK : int(e);
+}
+
+int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
+                        const msa_tensor4* o, const msa_head_desc* heads, int32_t n_heads,
+                        const int32_t* idx, const int32_t* cnt, int32_t idx_slots,
+                        int32_t topk_max, void* workspace, size_t workspace_bytes,
+                        msa_stream_t stream) {
+  return layer_attention_impl(q, k, v, o, heads, n_heads, idx, cnt, idx_slots, topk_max,
+                              workspace, workspace_bytes, stream, true);
+}
+
+int msa_layer_attention_staged(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
+                               const msa_tensor4* o, const msa_head_desc* heads, int32_t n_heads,
+                               const int32_t* idx, const int32_t* cnt, int32_t idx_slots,
+                               int32_t topk_max, void* workspace, size_t workspace_bytes,
+                               msa_stream_t stream) {
+  return layer_attention_impl(q, k, v, o, heads, n_heads, idx, cnt, idx_slots, topk_max,
+                              workspace, workspace_bytes, stream, false);
 }
 
 }  // extern "C"

@@ -178,23 +178,26 @@ __device__ inline void store_out4_16(uint16_t* dst, float a, float b, float c, f
 }
 
 template <typename T, bool OUT_F32, int D>
-__global__ __launch_bounds__(128) void attn_kernel(AttnParams P) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void attn_kernel(AttnParams P) {
   constexpr int KCH = D / 8;   // 16-byte chunks per K row
   constexpr int NKS = D / 16;  // QK^T k-steps (16 dims each)
   constexpr int NDB = D / 32;  // PV output blocks of 32 dims
-  constexpr int STG = D / 16;  // staged chunks per thread for K and for V^T
-  constexpr int TILE_BYTES = 2 * kBlock * D * 2;
-  constexpr int MERGE_BYTES = (2 * NDB * 16 * 64 + 4 * 64) * 4;
-  constexpr int LDS_BYTES = TILE_BYTES > MERGE_BYTES ? TILE_BYTES : MERGE_BYTES;
+  constexpr int STG = D / 32;  // staged chunks per thread for K and for V^T
+  constexpr int TILE_SLOTS = 2 * kBlock * KCH;  // K tile + V^T tile, 16-byte slots
+  constexpr int MERGE_FLOATS = 2 * NDB * 16 * 64 + 4 * 64;
+  constexpr int LDS_BYTES = (2 * TILE_SLOTS * 16 > MERGE_FLOATS * 4) ? 2 * TILE_SLOTS * 16
+                                                                     : MERGE_FLOATS * 4;
   __shared__ __align__(16) unsigned char lds[LDS_BYTES];
-  u32x4* ks = reinterpret_cast<u32x4*>(lds);
-  u32x4* vs = ks + kBlock * KCH;
+  u32x4* const tiles = reinterpret_cast<u32x4*>(lds);  // [2 buffers][K slots | V^T slots]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int n = lane & 31;
   const int g = lane >> 5;
   const int w = tid >> 6;
+  const int rh = w >> 1;  // query rows 32rh .. 32rh+31
+  const int kh = w & 1;   // keys 32kh .. 32kh+31 of every tile
 
   // ---- work item: query blocks longest-first, heads spread over the XCDs
   const int BH = P.batch * P.heads;
@@ -250,27 +253,25 @@ __global__ __launch_bounds__(128) void attn_kernel(AttnParams P) {
   const uint16_t* vtbase =
       P.vt + (int64_t(b) * (P.heads / P.kv_group) + kvh) * D * int64_t(P.s_pad);
 
-  // ---- Q as the B operand: lane (n, g) holds Q[row][16ks + 8g .. +7]
-  u32x4 qb[2][NKS];
+  // ---- Q rows 32rh.. as the B operand: lane (n, g) holds Q[row][16ks + 8g .. +7]
+  u32x4 qb[NKS];
   {
     const uint16_t* qbase =
         reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + int64_t(h) * P.q_sh;
+    const int row = q0 + 32 * rh + n;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const int row = q0 + 32 * rb + n;
-#pragma unroll
-      for (int kk = 0; kk < NKS; ++kk)
-        qb[rb][kk] = row < P.s_q ? load16(qbase + int64_t(row) * P.q_ss + 16 * kk + 8 * g)
-                                 : zero_u32x4();
-    }
+    for (int kk = 0; kk < NKS; ++kk)
+      qb[kk] = row < P.s_q ? load16(qbase + int64_t(row) * P.q_ss + 16 * kk + 8 * g)
+                           : zero_u32x4();
   }
 
+  // ---- tile staging: global -> registers -> LDS (swizzled 16-byte slots)
   u32x4 kr[STG], vr[STG];
   auto load_tile = [&](int t) {
     const int j0 = t * kBlock;
 #pragma unroll
     for (int u = 0; u < STG; ++u) {
-      const int ci = tid + 128 * u;
+      const int ci = tid + 256 * u;
       const int r = ci / KCH, c = ci - (ci / KCH) * KCH;
       const int j = j0 + r;
       kr[u] = j < P.s_k ? load16(kbase + int64_t(j) * P.k_ss + 8 * c) : zero_u32x4();
@@ -278,10 +279,12 @@ __global__ __launch_bounds__(128) void attn_kernel(AttnParams P) {
       vr[u] = load16(vtbase + int64_t(d) * P.s_pad + j0 + 8 * c2);
     }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](int buf) {
+    u32x4* ks = tiles + buf * TILE_SLOTS;
+    u32x4* vs = ks + kBlock * KCH;
 #pragma unroll
     for (int u = 0; u < STG; ++u) {
-      const int ci = tid + 128 * u;
+      const int ci = tid + 256 * u;
       const int r = ci / KCH, c = ci - (ci / KCH) * KCH;
       ks[r * KCH + (c ^ k_swz(r))] = kr[u];
       const int d = ci >> 3, c2 = ci & 7;
@@ -289,143 +292,131 @@ __global__ __launch_bounds__(128) void attn_kernel(AttnParams P) {
     }
   };
 
-  f32x16 o[NDB][2];
+  f32x16 o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][rb][i] = 0.0f;
-  float m[2] = {-1e30f, -1e30f};
-  float l[2] = {0.0f, 0.0f};
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+  // m is the running max in scaled log2 units; it only moves when the row
+  // max exceeds it by more than 8, so P stays <= 2^8 between rescales.
+  float m = -1e30f;
+  float l = 0.0f;
   const float c_log2 = hd.scale_log2;
+  const int krow = 32 * kh + n;    // A-operand key row of this lane in the tile
+  const int arow = a0 + 32 * rh + n;  // absolute position of this lane's query row
 
   int t = it.next();
   if (t >= 0) {
     load_tile(t);
-    store_tile();
+    store_tile(0);
   }
   __syncthreads();
 
-  const int krow = 32 * w + n;  // this lane's key row inside the tile (A operand)
+  int buf = 0;
   while (t >= 0) {
     const int tn = it.next();
     if (tn >= 0) load_tile(tn);
+    const u32x4* ks = tiles + buf * TILE_SLOTS;
+    const u32x4* vs = ks + kBlock * KCH;
 
-    // S^T[key][row] for keys 32w..32w+31
-    f32x16 s[2];
+    // S^T[key][row]: 32 keys (this wave's half) x 32 rows
+    f32x16 s;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int i = 0; i < 16; ++i) s[i] = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[rb][i] = 0.0f;
-#pragma unroll
-    for (int kk = 0; kk < NKS; ++kk) {
-      const u32x4 a = ks[krow * KCH + ((2 * kk + g) ^ k_swz(krow))];
-      s[0] = mfma_qk<T>(a, qb[0][kk], s[0]);
-      s[1] = mfma_qk<T>(a, qb[1][kk], s[1]);
-    }
+    for (int kk = 0; kk < NKS; ++kk)
+      s = mfma_qk<T>(ks[krow * KCH + ((2 * kk + g) ^ k_swz(krow))], qb[kk], s);
 
     const int j0 = t * kBlock;
     const int j1 = j0 + kBlock - 1;
     bool full = (j1 <= a0) && (j1 < P.s_k);
     if (kind == KIND_STREAM) full = full && ((j0 >= a1 - n_local + 1) || (j1 < n_init));
     if (!full) {
+      const int jb = j0 + 32 * kh + 4 * g;
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int arow = a0 + 32 * rb + n;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int j = j0 + 32 * w + 8 * (i >> 2) + 4 * g + (i & 3);
-          bool vis = (j <= arow) && (j < P.s_k);
-          if (kind == KIND_STREAM) vis = vis && ((j >= arow - n_local + 1) || (j < n_init));
-          if (!vis) s[rb][i] = -__builtin_inff();
-        }
+      for (int i = 0; i < 16; ++i) {
+        const int j = jb + 8 * (i >> 2) + (i & 3);
+        bool vis = (j <= arow) && (j < P.s_k);
+        if (kind == KIND_STREAM) vis = vis && ((j >= arow - n_local + 1) || (j < n_init));
+        if (!vis) s[i] = -__builtin_inff();
       }
     }
 
-    // online softmax (base 2), P rounded to fp16
-    u32x4 pb[2][2];
+    // row max of the raw scores (lanes n and n+32 hold the two 16-key halves)
+    float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      float mx = -__builtin_inff();
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        s[rb][i] *= c_log2;
-        mx = fmaxf(mx, s[rb][i]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m[rb], mx);
-      const float alpha = __builtin_amdgcn_exp2f(m[rb] - mnew);
-      m[rb] = mnew;
-      float sum = 0.0f;
-      uint16_t hbits[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const _Float16 ph = static_cast<_Float16>(__builtin_amdgcn_exp2f(s[rb][i] - mnew));
-        sum += float(ph);
-        hbits[i] = __builtin_bit_cast(uint16_t, ph);
-      }
-      l[rb] = l[rb] * alpha + sum;
+    for (int i = 3; i < 15; i += 2) mx = fmaxf(fmaxf(mx, s[i]), s[i + 1]);
+    mx = fmaxf(mx, s[15]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c_log2;
+    if (__builtin_amdgcn_read_exec() &&
+        __ballot(mx > m + 8.0f)) {  // wave-uniform: some row grew past the slack
+      const float mnew = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+      m = mnew;
+      l *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][rb][i] *= alpha;
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          pb[rb][tt][e] = uint32_t(hbits[8 * tt + 2 * e]) | (uint32_t(hbits[8 * tt + 2 * e + 1]) << 16);
+        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
     }
+
+    // P = 2^(s*c - m) rounded to fp16; the row sum uses fp32 P
+    u32x4 pb[2];
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c_log2, -m));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i + 1], c_log2, -m));
+      psum += p0 + p1;
+      typedef float f2 __attribute__((ext_vector_type(2)));
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const h2 hp = __builtin_convertvector(f2{p0, p1}, h2);
+      pb[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(uint32_t, hp);
+    }
+    l += psum;
 
     // O^T[d][row] += V^T[d][key] . P^T[key][row]
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       const int d = 32 * db + n;
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const u32x4 a = vs[d * 8 + ((4 * w + 2 * tt + g) ^ v_swz(d))];
-        o[db][0] = mfma_pv(a, pb[0][tt], o[db][0]);
-        o[db][1] = mfma_pv(a, pb[1][tt], o[db][1]);
-      }
+      for (int tt = 0; tt < 2; ++tt)
+        o[db] = mfma_pv(vs[d * 8 + ((4 * kh + 2 * tt + g) ^ v_swz(d))], pb[tt], o[db]);
     }
 
+    if (tn >= 0) store_tile(buf ^ 1);
     __syncthreads();
-    if (tn >= 0) {
-      store_tile();
-      __syncthreads();
-    }
+    buf ^= 1;
     t = tn;
   }
 
-  // ---- merge the two waves' partial states; wave w finishes row block w
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) l[rb] += __shfl_xor(l[rb], 32, 64);
-  float* mo = reinterpret_cast<float*>(lds);    // [dest wave][NDB][16][64]
-  float* mm = mo + 2 * NDB * 16 * 64;           // [dest wave][64]
-  float* ml = mm + 2 * 64;                      // [dest wave][64]
-  const int dest = 1 - w;
+  // ---- merge the two key halves of each row half; kh == 0 writes the rows
+  l += __shfl_xor(l, 32, 64);
+  float* mo = reinterpret_cast<float*>(lds);  // [rh][NDB][16][64]
+  float* mm = mo + 2 * NDB * 16 * 64;         // [rh][64]
+  float* ml = mm + 2 * 64;                    // [rh][64]
   __syncthreads();
+  if (kh == 1) {
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      mo[((dest * NDB + db) * 16 + i) * 64 + lane] = (w == 0) ? o[db][1][i] : o[db][0][i];
-  mm[dest * 64 + lane] = (w == 0) ? m[1] : m[0];
-  ml[dest * 64 + lane] = (w == 0) ? l[1] : l[0];
+      for (int i = 0; i < 16; ++i) mo[((rh * NDB + db) * 16 + i) * 64 + lane] = o[db][i];
+    mm[rh * 64 + lane] = m;
+    ml[rh * 64 + lane] = l;
+  }
   __syncthreads();
+  if (kh == 1) return;
 
-  const float m_self = (w == 0) ? m[0] : m[1];
-  const float l_self = (w == 0) ? l[0] : l[1];
-  const float m_oth = mm[w * 64 + lane];
-  const float l_oth = ml[w * 64 + lane];
-  const float mt = fmaxf(m_self, m_oth);
-  const float f0 = __builtin_amdgcn_exp2f(m_self - mt);
+  const float m_oth = mm[rh * 64 + lane];
+  const float l_oth = ml[rh * 64 + lane];
+  const float mt = fmaxf(m, m_oth);
+  const float f0 = __builtin_amdgcn_exp2f(m - mt);
   const float f1 = __builtin_amdgcn_exp2f(m_oth - mt);
-  const float lt = l_self * f0 + l_oth * f1;
+  const float lt = l * f0 + l_oth * f1;
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   const float s0 = f0 * inv, s1 = f1 * inv;
 
-  const int row = q0 + 32 * w + n;
+  const int row = q0 + 32 * rh + n;
   if (row < P.s_q) {
     const int64_t obase = b * P.o_sb + int64_t(h) * P.o_sh + int64_t(row) * P.o_ss;
 #pragma unroll
@@ -436,8 +427,7 @@ __global__ __launch_bounds__(128) void attn_kernel(AttnParams P) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * qd + e;
-          const float self = (w == 0) ? o[db][0][i] : o[db][1][i];
-          v4[e] = self * s0 + mo[((w * NDB + db) * 16 + i) * 64 + lane] * s1;
+          v4[e] = o[db][i] * s0 + mo[((rh * NDB + db) * 16 + i) * 64 + lane] * s1;
         }
         const int d = 32 * db + 8 * qd + 4 * g;
         if constexpr (OUT_F32) {
@@ -453,7 +443,7 @@ __global__ __launch_bounds__(128) void attn_kernel(AttnParams P) {
 template <typename T, bool OUT_F32, int D>
 static hipError_t launch_attn_t(const AttnParams& p, hipStream_t st) {
   const int64_t items = int64_t(p.n_qb) * p.batch * p.heads;
-  hipLaunchKernelGGL((attn_kernel<T, OUT_F32, D>), dim3(uint32_t(items)), dim3(128), 0, st, p);
+  hipLaunchKernelGGL((attn_kernel<T, OUT_F32, D>), dim3(uint32_t(items)), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 

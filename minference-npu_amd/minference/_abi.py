@@ -57,6 +57,8 @@ EXPORTED_SYMBOLS = (
     "msa_block_estimate",
     "msa_attention_workspace_bytes",
     "msa_layer_attention",
+    "msa_stage_v",
+    "msa_layer_attention_staged",
 )
 
 
@@ -132,13 +134,19 @@ def load_library() -> ctypes.CDLL:
         lib.msa_attention_workspace_bytes.argtypes = [
             ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
         ]
-        lib.msa_layer_attention.restype = ctypes.c_int
-        lib.msa_layer_attention.argtypes = [
-            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
-            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
-            ctypes.POINTER(MsaHeadDesc), ctypes.c_int32,
-            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
-            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        for name in ("msa_layer_attention", "msa_layer_attention_staged"):
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [
+                ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+                ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+                ctypes.POINTER(MsaHeadDesc), ctypes.c_int32,
+                ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+            ]
+        lib.msa_stage_v.restype = ctypes.c_int
+        lib.msa_stage_v.argtypes = [
+            ctypes.POINTER(MsaTensor4), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
         ver = lib.msa_abi_version()
         if ver != ABI_VERSION:
@@ -237,6 +245,26 @@ def block_estimate(
     check(st)
 
 
+def head_descs(heads: Sequence[tuple]):
+    """ctypes array of msa_head_desc from [(kind, p1, p2, slot, scale)]."""
+    n = len(heads)
+    arr = (MsaHeadDesc * max(n, 1))()
+    for i, (kind, p1, p2, slot, scale) in enumerate(heads):
+        arr[i].kind = int(kind)
+        arr[i].p1 = int(p1)
+        arr[i].p2 = int(p2)
+        arr[i].slot = int(slot)
+        arr[i].scale = float(scale)
+    return arr
+
+
+def stage_v(v: torch.Tensor, ws: torch.Tensor) -> None:
+    """Launch msa_stage_v (V -> fp16 V^T in ``ws``) on the current stream."""
+    vd = tensor4(v)
+    check(load_library().msa_stage_v(ctypes.byref(vd), ws.data_ptr(), ws.numel(),
+                                     current_stream_handle(v.device)))
+
+
 def layer_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -248,22 +276,22 @@ def layer_attention(
     idx_slots: int = 0,
     topk_max: int = 0,
     ws: Optional[torch.Tensor] = None,
+    staged: bool = False,
 ) -> None:
-    """Launch msa_layer_attention.  ``heads`` = [(kind, p1, p2, slot, scale)] * H."""
+    """Launch msa_layer_attention (or, with ``staged=True``,
+    msa_layer_attention_staged reading the V^T already in ``ws``).
+    ``heads`` = [(kind, p1, p2, slot, scale)] * H."""
     lib = load_library()
     n = len(heads)
-    arr = (MsaHeadDesc * max(n, 1))()
-    for i, (kind, p1, p2, slot, scale) in enumerate(heads):
-        arr[i].kind = int(kind)
-        arr[i].p1 = int(p1)
-        arr[i].p2 = int(p2)
-        arr[i].slot = int(slot)
-        arr[i].scale = float(scale)
+    arr = head_descs(heads)
     need = attention_workspace_bytes(k.shape[0], k.shape[1], k.shape[2], k.shape[3])
+    if staged and (ws is None or ws.numel() < need):
+        raise ValueError("staged attention needs the workspace filled by stage_v")
     if ws is None or ws.numel() < need:
         ws = workspace(need, q.device)
     qd, kd, vd, od = tensor4(q), tensor4(k), tensor4(v), tensor4(out)
-    st = lib.msa_layer_attention(
+    fn = lib.msa_layer_attention_staged if staged else lib.msa_layer_attention
+    st = fn(
         ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ctypes.byref(od),
         arr, n,
         idx.data_ptr() if idx is not None else None,

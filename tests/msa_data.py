@@ -10,8 +10,8 @@ def rope(x: torch.Tensor, theta: float = 10000.0, offset: int = 0) -> torch.Tens
     """HF rotate_half RoPE on [B, H, S, D] fp32, positions offset..offset+S-1."""
     D = x.shape[-1]
     S = x.shape[-2]
-    inv = 1.0 / (theta ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
-    pos = torch.arange(offset, offset + S, dtype=torch.float32)
+    inv = 1.0 / (theta ** (torch.arange(0, D, 2, dtype=torch.float32, device=x.device) / D))
+    pos = torch.arange(offset, offset + S, dtype=torch.float32, device=x.device)
     fr = torch.outer(pos, inv)
     emb = torch.cat([fr, fr], dim=-1)
     cos, sin = emb.cos(), emb.sin()
