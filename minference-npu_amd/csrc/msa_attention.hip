@@ -23,6 +23,8 @@
 //   16-key group so every PV A operand is one 16-byte LDS read.
 //   Row max / sum need one lane^32 exchange per tile.
 
+#include <type_traits>
+
 #include "msa_common.h"
 #include "msa_kernels.h"
 
@@ -131,33 +133,31 @@ __device__ inline f32x16 mfma_pv(u32x4 a, u32x4 b, f32x16 c) {
 __device__ inline int k_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 __device__ inline int v_swz(int d) { return (d ^ (d >> 3)) & 7; }
 
-struct TileIter {
-  int kind;
-  int i, n;
-  int nsink, lo;
-  int last_tile;
-  int prev;
+// Tile sequence of one work item as up to five segments: the first `nfull`
+// segments hold tiles that need no mask, the rest hold the boundary tiles.
+// For block_sparse heads the segments index the id list, otherwise they are
+// tile numbers.  Segment bounds are wave-uniform (scalar registers).
+struct Cursor {
+  int lo0, hi0, lo1, hi1, lo2, hi2, lo3, hi3, lo4, hi4;
+  int nfull;
+  int seg, i, hi;
+  int n_kb;
   const int32_t* list;
 
-  __device__ int next() {
-    if (kind == KIND_BLOCK) {
-      while (i < n) {
-        const int t = list[i++];
-        if (t > last_tile) {
-          i = n;
-          return -1;
-        }
-        if (t >= 0 && t > prev) {
-          prev = t;
-          return t;
-        }
-      }
-      return -1;
+  __device__ void bounds(int k, int& lo, int& hi_) const {
+    lo = k == 0 ? lo0 : k == 1 ? lo1 : k == 2 ? lo2 : k == 3 ? lo3 : lo4;
+    hi_ = k == 0 ? hi0 : k == 1 ? hi1 : k == 2 ? hi2 : k == 3 ? hi3 : hi4;
+  }
+  // next tile (clamped into [0, n_kb) for memory safety) or -1
+  __device__ int next(bool& masked) {
+    while (i >= hi) {
+      if (++seg >= 5) return -1;
+      bounds(seg, i, hi);
     }
-    if (i >= n) return -1;
-    const int t = (kind == KIND_STREAM && i >= nsink) ? lo + (i - nsink) : i;
+    masked = seg >= nfull;
+    const int t = list ? list[i] : i;
     ++i;
-    return t;
+    return min(max(t, 0), n_kb - 1);
   }
 };
 
@@ -184,12 +184,11 @@ void attn_kernel(AttnParams P) {
   constexpr int NKS = D / 16;  // QK^T k-steps (16 dims each)
   constexpr int NDB = D / 32;  // PV output blocks of 32 dims
   constexpr int STG = D / 32;  // staged chunks per thread for K and for V^T
-  constexpr int TILE_SLOTS = 2 * kBlock * KCH;  // K tile + V^T tile, 16-byte slots
-  constexpr int MERGE_FLOATS = 2 * NDB * 16 * 64 + 4 * 64;
-  constexpr int LDS_BYTES = (2 * TILE_SLOTS * 16 > MERGE_FLOATS * 4) ? 2 * TILE_SLOTS * 16
-                                                                     : MERGE_FLOATS * 4;
+  constexpr int K_BYTES = kBlock * D * 2;         // K tile
+  constexpr int TILE_BYTES = 2 * K_BYTES;         // K tile + V^T tile
+  constexpr int MERGE_BYTES = (2 * NDB * 16 * 64 + 4 * 64) * 4;
+  constexpr int LDS_BYTES = 2 * TILE_BYTES > MERGE_BYTES ? 2 * TILE_BYTES : MERGE_BYTES;
   __shared__ __align__(16) unsigned char lds[LDS_BYTES];
-  u32x4* const tiles = reinterpret_cast<u32x4*>(lds);  // [2 buffers][K slots | V^T slots]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -225,33 +224,53 @@ void attn_kernel(AttnParams P) {
   const int last_tile = min(a1 >> 6, P.n_kb - 1);
   const int n_init = hd.p1;
   const int n_local = hd.p2;
+  // tile t needs no mask for the causal / S_k bounds iff t < F
+  const int Fe = min(min((a0 + 1) >> 6, P.s_k >> 6), last_tile + 1);
 
-  TileIter it;
-  it.kind = kind;
-  it.i = 0;
-  it.prev = -1;
-  it.last_tile = last_tile;
-  it.nsink = 0;
-  it.lo = 0;
-  it.list = nullptr;
+  Cursor cur;
+  cur.lo0 = cur.hi0 = cur.lo1 = cur.hi1 = cur.lo2 = cur.hi2 = 0;
+  cur.lo3 = cur.hi3 = cur.lo4 = cur.hi4 = 0;
+  cur.seg = -1;
+  cur.i = cur.hi = 0;
+  cur.n_kb = P.n_kb;
+  cur.list = nullptr;
   if (kind == KIND_BLOCK) {
+    // canonical list: ascending causal ids, so the boundary ids come last
     const int64_t base = (int64_t(b) * P.idx_slots + hd.slot) * P.n_qb + bq;
-    it.n = min(P.cnt[base], P.topk_max);
-    it.list = P.idx + base * P.topk_max;
+    const int cnt = max(0, min(P.cnt[base], P.topk_max));
+    const int32_t* list = P.idx + base * P.topk_max;
+    int nf = cnt;
+    while (nf > 0 && list[nf - 1] >= Fe) --nf;
+    cur.list = list;
+    cur.hi0 = nf;
+    cur.lo1 = nf;
+    cur.hi1 = cnt;
+    cur.nfull = 1;
   } else if (kind == KIND_STREAM) {
-    const int band_lo = max(a0 - n_local + 1, 0);
-    it.lo = min(band_lo >> 6, last_tile + 1);
-    const int sink_keys = min(max(n_init, 0), P.s_k);
-    it.nsink = min((sink_keys + 63) >> 6, it.lo);
-    it.n = it.nsink + (last_tile - it.lo + 1);
+    const int lo = min(max(a0 - n_local + 1, 0) >> 6, last_tile + 1);
+    const int nsink = min((min(max(n_init, 0), P.s_k) + 63) >> 6, lo);
+    const int sf = max(0, min(nsink, min(n_init >> 6, Fe)));  // sink tiles below n_init
+    int bf0 = a1 - n_local + 1;                                 // band tiles in every row's band
+    bf0 = bf0 <= 0 ? 0 : (bf0 + 63) >> 6;
+    bf0 = min(max(bf0, lo), last_tile + 1);
+    const int fb_hi = max(bf0, Fe);
+    cur.hi0 = sf;                       // full sink
+    cur.lo1 = bf0; cur.hi1 = fb_hi;     // full band
+    cur.lo2 = sf; cur.hi2 = nsink;      // partial sink
+    cur.lo3 = lo; cur.hi3 = bf0;        // band tiles cut by the window start
+    cur.lo4 = fb_hi; cur.hi4 = last_tile + 1;  // diagonal / S_k boundary
+    cur.nfull = 2;
   } else {
-    it.n = last_tile + 1;
+    cur.hi0 = Fe;
+    cur.lo1 = Fe; cur.hi1 = last_tile + 1;
+    cur.nfull = 1;
   }
 
-  const uint16_t* kbase =
-      reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + int64_t(kvh) * P.k_sh;
-  const uint16_t* vtbase =
-      P.vt + (int64_t(b) * (P.heads / P.kv_group) + kvh) * D * int64_t(P.s_pad);
+  const unsigned char* kbytes = reinterpret_cast<const unsigned char*>(P.k) +
+                                2 * (b * P.k_sb + int64_t(kvh) * P.k_sh);
+  const unsigned char* vtbytes = reinterpret_cast<const unsigned char*>(P.vt) +
+                                 2 * ((int64_t(b) * (P.heads / P.kv_group) + kvh) * D * int64_t(P.s_pad));
+  const int64_t kss2 = 2 * P.k_ss;
 
   // ---- Q rows 32rh.. as the B operand: lane (n, g) holds Q[row][16ks + 8g .. +7]
   u32x4 qb[NKS];
@@ -265,30 +284,55 @@ void attn_kernel(AttnParams P) {
                            : zero_u32x4();
   }
 
-  // ---- tile staging: global -> registers -> LDS (swizzled 16-byte slots)
+  // ---- loop-invariant staging offsets (global bytes within a tile, LDS bytes)
+  uint32_t koff[STG], voff[STG], kslot[STG], vslot[STG];
+#pragma unroll
+  for (int u = 0; u < STG; ++u) {
+    const int ci = tid + 256 * u;
+    const int r = ci / KCH, c = ci - r * KCH;
+    koff[u] = uint32_t(r) * uint32_t(kss2) + 16u * c;
+    kslot[u] = 16u * (r * KCH + (c ^ k_swz(r)));
+    const int d = ci >> 3, c2 = ci & 7;
+    voff[u] = uint32_t(d) * uint32_t(2 * P.s_pad) + 16u * c2;
+    vslot[u] = K_BYTES + 16u * (d * 8 + (c2 ^ v_swz(d)));
+  }
+  // MFMA A-operand LDS offsets: K rows of this lane, V^T rows 32db + n
+  const int krow = 32 * kh + n;
+  const uint32_t ka0 = 16u * (krow * KCH + (g ^ k_swz(krow)));
+  const uint32_t ka1 = 16u * (krow * KCH + ((2 + g) ^ k_swz(krow)));
+  uint32_t va[NDB][2];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    const int d = 32 * db + n;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+      va[db][tt] = K_BYTES + 16u * (d * 8 + ((4 * kh + 2 * tt + g) ^ v_swz(d)));
+  }
+
+  // Tile staging through buffer loads: the descriptor is rebased on each tile
+  // (scalar work) and bounded so that K rows at or past S_k read as zero.
   u32x4 kr[STG], vr[STG];
   auto load_tile = [&](int t) {
     const int j0 = t * kBlock;
+    const int rows = min(kBlock, P.s_k - j0);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(kbytes + int64_t(j0) * kss2), short(0),
+        int(rows * kss2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(vtbytes + 2 * int64_t(j0)), short(0),
+        int(D * 2 * P.s_pad - 2 * j0), 0x00020000);
 #pragma unroll
     for (int u = 0; u < STG; ++u) {
-      const int ci = tid + 256 * u;
-      const int r = ci / KCH, c = ci - (ci / KCH) * KCH;
-      const int j = j0 + r;
-      kr[u] = j < P.s_k ? load16(kbase + int64_t(j) * P.k_ss + 8 * c) : zero_u32x4();
-      const int d = ci >> 3, c2 = ci & 7;
-      vr[u] = load16(vtbase + int64_t(d) * P.s_pad + j0 + 8 * c2);
+      kr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff[u], 0, 0));
+      vr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[u], 0, 0));
     }
   };
   auto store_tile = [&](int buf) {
-    u32x4* ks = tiles + buf * TILE_SLOTS;
-    u32x4* vs = ks + kBlock * KCH;
+    unsigned char* base = lds + buf * TILE_BYTES;
 #pragma unroll
     for (int u = 0; u < STG; ++u) {
-      const int ci = tid + 256 * u;
-      const int r = ci / KCH, c = ci - (ci / KCH) * KCH;
-      ks[r * KCH + (c ^ k_swz(r))] = kr[u];
-      const int d = ci >> 3, c2 = ci & 7;
-      vs[d * 8 + (c2 ^ v_swz(d))] = vr[u];
+      *reinterpret_cast<u32x4*>(base + kslot[u]) = kr[u];
+      *reinterpret_cast<u32x4*>(base + vslot[u]) = vr[u];
     }
   };
 
@@ -302,37 +346,46 @@ void attn_kernel(AttnParams P) {
   float m = -1e30f;
   float l = 0.0f;
   const float c_log2 = hd.scale_log2;
-  const int krow = 32 * kh + n;    // A-operand key row of this lane in the tile
   const int arow = a0 + 32 * rh + n;  // absolute position of this lane's query row
 
-  int t = it.next();
+  bool mt = false;
+  int t = cur.next(mt);
   if (t >= 0) {
     load_tile(t);
     store_tile(0);
   }
   __syncthreads();
+  // Q is complete here; re-define it so no later wait is attributed to its loads.
+#pragma unroll
+  for (int kk = 0; kk < NKS; ++kk) asm volatile("" : "+v"(qb[kk]));
 
   int buf = 0;
   while (t >= 0) {
-    const int tn = it.next();
+    bool mtn = false;
+    const int tn = cur.next(mtn);
     if (tn >= 0) load_tile(tn);
-    const u32x4* ks = tiles + buf * TILE_SLOTS;
-    const u32x4* vs = ks + kBlock * KCH;
+    const unsigned char* tb = lds + buf * TILE_BYTES;
 
     // S^T[key][row]: 32 keys (this wave's half) x 32 rows
+    u32x4 ka[NKS];
+#pragma unroll
+    for (int kk = 0; kk < NKS; ++kk)
+      ka[kk] = *reinterpret_cast<const u32x4*>(tb + ((kk & 1) ? ka1 : ka0) + 64u * (kk >> 1));
     f32x16 s;
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = 0.0f;
 #pragma unroll
-    for (int kk = 0; kk < NKS; ++kk)
-      s = mfma_qk<T>(ks[krow * KCH + ((2 * kk + g) ^ k_swz(krow))], qb[kk], s);
+    for (int kk = 0; kk < NKS; ++kk) s = mfma_qk<T>(ka[kk], qb[kk], s);
+    // V^T operands do not depend on P: read them now, under the softmax
+    u32x4 vop[NDB][2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) vop[db][tt] = *reinterpret_cast<const u32x4*>(tb + va[db][tt]);
+    __builtin_amdgcn_sched_barrier(0);
 
-    const int j0 = t * kBlock;
-    const int j1 = j0 + kBlock - 1;
-    bool full = (j1 <= a0) && (j1 < P.s_k);
-    if (kind == KIND_STREAM) full = full && ((j0 >= a1 - n_local + 1) || (j1 < n_init));
-    if (!full) {
-      const int jb = j0 + 32 * kh + 4 * g;
+    if (mt) {
+      const int jb = t * kBlock + 32 * kh + 4 * g;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int j = jb + 8 * (i >> 2) + (i & 3);
@@ -341,15 +394,13 @@ void attn_kernel(AttnParams P) {
         if (!vis) s[i] = -__builtin_inff();
       }
     }
-
     // row max of the raw scores (lanes n and n+32 hold the two 16-key halves)
     float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
 #pragma unroll
     for (int i = 3; i < 15; i += 2) mx = fmaxf(fmaxf(mx, s[i]), s[i + 1]);
     mx = fmaxf(mx, s[15]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c_log2;
-    if (__builtin_amdgcn_read_exec() &&
-        __ballot(mx > m + 8.0f)) {  // wave-uniform: some row grew past the slack
+    if (__ballot(mx > m + 8.0f)) {  // wave-uniform: some row grew past the slack
       const float mnew = fmaxf(m, mx);
       const float alpha = __builtin_amdgcn_exp2f(m - mnew);
       m = mnew;
@@ -359,7 +410,6 @@ void attn_kernel(AttnParams P) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
     }
-
     // P = 2^(s*c - m) rounded to fp16; the row sum uses fp32 P
     u32x4 pb[2];
     float psum = 0.0f;
@@ -370,24 +420,21 @@ void attn_kernel(AttnParams P) {
       psum += p0 + p1;
       typedef float f2 __attribute__((ext_vector_type(2)));
       typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-      const h2 hp = __builtin_convertvector(f2{p0, p1}, h2);
-      pb[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(uint32_t, hp);
+      pb[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{p0, p1}, h2));
     }
     l += psum;
-
+    __builtin_amdgcn_sched_barrier(0);
     // O^T[d][row] += V^T[d][key] . P^T[key][row]
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int d = 32 * db + n;
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-        o[db] = mfma_pv(vs[d * 8 + ((4 * kh + 2 * tt + g) ^ v_swz(d))], pb[tt], o[db]);
-    }
+      for (int tt = 0; tt < 2; ++tt) o[db] = mfma_pv(vop[db][tt], pb[tt], o[db]);
 
     if (tn >= 0) store_tile(buf ^ 1);
     __syncthreads();
     buf ^= 1;
     t = tn;
+    mt = mtn;
   }
 
   // ---- merge the two key halves of each row half; kh == 0 writes the rows
@@ -395,7 +442,6 @@ void attn_kernel(AttnParams P) {
   float* mo = reinterpret_cast<float*>(lds);  // [rh][NDB][16][64]
   float* mm = mo + 2 * NDB * 16 * 64;         // [rh][64]
   float* ml = mm + 2 * 64;                    // [rh][64]
-  __syncthreads();
   if (kh == 1) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
@@ -409,9 +455,9 @@ void attn_kernel(AttnParams P) {
 
   const float m_oth = mm[rh * 64 + lane];
   const float l_oth = ml[rh * 64 + lane];
-  const float mt = fmaxf(m, m_oth);
-  const float f0 = __builtin_amdgcn_exp2f(m - mt);
-  const float f1 = __builtin_amdgcn_exp2f(m_oth - mt);
+  const float mt2 = fmaxf(m, m_oth);
+  const float f0 = __builtin_amdgcn_exp2f(m - mt2);
+  const float f1 = __builtin_amdgcn_exp2f(m_oth - mt2);
   const float lt = l * f0 + l_oth * f1;
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   const float s0 = f0 * inv, s1 = f1 * inv;

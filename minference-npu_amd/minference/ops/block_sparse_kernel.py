@@ -116,14 +116,34 @@ def block_sparse_attention_with_indices(
             f"got {tuple(block_indices.shape)} for q={tuple(q.shape)} block_size={block_size}"
         )
     q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
-    idx = torch.sort(block_indices.to(device=q.device, dtype=torch.int32), dim=-1).values
+    n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
+    idx, cnt = canonical_block_lists(block_indices.to(q.device), n_kb)
     topk = idx.shape[-1]
     chunks = []
     for h0, h1 in head_chunks(H):
-        cnt = torch.full((B, h1 - h0, n_qb), topk, dtype=torch.int32, device=q.device)
-        chunks.append((h0, h1, idx[:, h0:h1].contiguous(), cnt))
+        chunks.append((h0, h1, idx[:, h0:h1].contiguous(), cnt[:, h0:h1].contiguous()))
     result = make_out(q, out)
     return _run(q, k, v, chunks, topk, result)
+
+
+def canonical_block_lists(block_indices: torch.Tensor, n_kb: int):
+    """Turn arbitrary per-row block ids into the kernel's list format: the
+    distinct ids in [0, n_kb) ascending first, ``cnt`` = how many.  This is the
+    set semantics of the reference's scatter into a block mask
+    (block_sparse_kernel_npu.py:290-291): repeats count once and ids outside
+    the key range select nothing.  Returns int32 (idx, cnt)."""
+    ids = block_indices.long()
+    topk = ids.shape[-1]
+    valid = (ids >= 0) & (ids < n_kb)
+    ids = torch.where(valid, ids, torch.full_like(ids, n_kb)).sort(dim=-1).values
+    keep = ids < n_kb
+    keep[..., 1:] &= ids[..., 1:] != ids[..., :-1]
+    pos = torch.arange(topk, device=ids.device)
+    order = ((~keep).long() * (topk + 1) + pos).argsort(dim=-1)
+    ids = ids.gather(-1, order)
+    cnt = keep.sum(dim=-1)
+    ids = torch.where(pos < cnt[..., None], ids, torch.zeros_like(ids))
+    return ids.to(torch.int32).contiguous(), cnt.to(torch.int32).contiguous()
 
 
 def _run(q, k, v, chunks, topk, result):
