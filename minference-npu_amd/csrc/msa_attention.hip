@@ -12,16 +12,22 @@
 //   stream    : and (j > a - n_local or j < n_init)
 // Rows with no visible key produce 0 (the reference's nan_to_num).
 //
-// CDNA4 mapping (one workgroup = 2 wave64, 64 query rows):
-//   wave w owns keys [32w, 32w+32) of every tile and all 64 rows, keeping a
-//   private online-softmax state; the two states merge once at the end.
+// CDNA4 mapping (one workgroup = 4 wave64 = one 64-row query block):
+//   wave w = (row half rh, key half kh) owns query rows [32rh, 32rh+32) and
+//   keys [32kh, 32kh+32) of every tile, with a private online-softmax state;
+//   the two key halves of a row half merge once at the end.
 //   S^T = K.Q^T on v_mfma_f32_32x32x16_{bf16,f16} (A = K tile from LDS,
-//   B = Q from registers) so that the accumulator layout (one query row per
-//   lane) is directly the B operand of O^T = V^T.P^T on v_mfma_f32_32x32x16_f16.
-//   P is rounded to fp16 (11-bit mantissa) and the row sum uses the rounded P.
+//   B = Q from registers), so the accumulator layout (one query row per lane)
+//   is directly the B operand of O^T = V^T.P^T on v_mfma_f32_32x32x16_f16.
+//   P is rounded to fp16 (11-bit mantissa) for the PV product.
 //   V is staged once per layer as fp16 V^T with keys permuted inside each
 //   16-key group so every PV A operand is one 16-byte LDS read.
-//   Row max / sum need one lane^32 exchange per tile.
+//   K and V^T tiles are double-buffered in LDS (XOR-swizzled 16-byte slots,
+//   no bank conflicts) and the next tile is prefetched by buffer loads.
+//   The running max moves only when a row max grows by more than 2^8, so the
+//   O rescale is rare; the row max needs one lane^32 exchange per tile.
+//   Tiles that need no mask run first; boundary tiles (diagonal, band start,
+//   partial sink, S_k end) run last with the elementwise mask.
 
 #include <type_traits>
 
@@ -198,14 +204,16 @@ void attn_kernel(AttnParams P) {
   const int rh = w >> 1;  // query rows 32rh .. 32rh+31
   const int kh = w & 1;   // keys 32kh .. 32kh+31 of every tile
 
-  // ---- work item: query blocks longest-first, heads spread over the XCDs
+  // ---- work item.  Workgroups are dispatched round-robin over the 8 XCDs;
+  // each XCD walks its own heads one at a time (query blocks longest-first),
+  // so the K/V of the 8 heads in flight stay resident in L2 / Infinity Cache.
   const int BH = P.batch * P.heads;
   const int item = blockIdx.x;
   int hh, bq;
   if (P.xcd_heads) {
     const int r = item >> 3;
-    bq = P.n_qb - 1 - r / P.xcd_heads;
-    hh = P.head_order[(item & 7) * P.xcd_heads + r % P.xcd_heads];
+    bq = P.n_qb - 1 - r % P.n_qb;
+    hh = P.head_order[(item & 7) * P.xcd_heads + r / P.n_qb];
   } else {
     bq = P.n_qb - 1 - item / BH;
     hh = item % BH;
