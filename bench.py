@@ -37,6 +37,9 @@ for _p in (ROOT, os.path.join(ROOT, "minference-npu_amd"), os.path.join(ROOT, "t
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (no sparsity)
 BLOCK = 64
 
+# workload -> profile summary holding the calibrated HBM traffic of the attention kernel
+TRAFFIC_PROFILE = {"headline": "attn_kernel_headline64k_traffic.txt"}
+
 WORKLOADS = {
     # name: (S, n_stream, n_block, n_dense, n_init, n_local, topk)
     "headline": (65536, 16, 16, 0, 128, 4096, 100),
@@ -58,6 +61,9 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads of BASELINE config 1 timed on the CPU (scaled to 32)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (5 launches) to calibrate the "
+                         "FETCH_SIZE / WRITE_SIZE counters, then exit")
     return ap.parse_args()
 
 
@@ -93,6 +99,23 @@ def make_inputs(S, H, D, seed, device):
         out.append(x.to(torch.bfloat16))
         del x
     return out
+
+
+def profiled_traffic(workload):
+    """HBM bytes per attention launch measured by two rocprofv3 --pmc runs
+    (FETCH_SIZE, WRITE_SIZE; calibrated on a device copy), from profiles/."""
+    name = TRAFFIC_PROFILE.get(workload)
+    if not name:
+        return None
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for ln in f:
+                if ln.startswith("attn_kernel traffic_bytes_per_launch:"):
+                    return int(ln.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_model():
@@ -153,6 +176,17 @@ def cpu_baseline(n_heads_sample):
 
 def main():
     args = parse_args()
+    if args.calibrate_copy:
+        import torch
+
+        n = args.calibrate_copy * (1 << 20) // 2
+        src = torch.ones(n, dtype=torch.bfloat16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_mib": args.calibrate_copy, "launches": 5}))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
               "multi-GPU path (heads would shard across GPUs with no communication inside "
@@ -278,7 +312,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved_attn / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(args.workload),
             "kernel": "msa::attn_kernel<Bf16,false,96>",
         },
     }
