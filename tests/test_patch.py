@@ -1,0 +1,188 @@
+"""Host-side logic of the drop-in surface (CPU): configuration, pattern files,
+per-layer plans and the HF patch plumbing.
+
+The plumbing tests swap the device launch (``run_layer_attention``) for a CPU
+test double built on the oracle, so the patched forward's own work (QKV
+split, RoPE, cache update, output layout, o_proj) is compared with the
+unpatched HF model.  The product code itself has no CPU path."""
+
+from __future__ import annotations
+
+import json
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from minference import MInference, MInferenceConfig, get_support_models, patch_hf
+from minference import _abi
+from minference.configs import patterns as P
+from minference.modules import minference_forward as MF
+
+
+# ---------------------------------------------------------------------------
+# configuration and patterns
+# ---------------------------------------------------------------------------
+def test_config_semantics(tmp_path):
+    cfg = MInferenceConfig(attn_type="minference", model_name="microsoft/Phi-3-mini-128k-instruct")
+    assert cfg.config_path.endswith(".json")
+    assert cfg.attn_kwargs["starting_layer"] == -1 and cfg.kv_type == "dense"
+    assert MInferenceConfig(attn_type="dense").config_path == ""
+    assert MInferenceConfig(attn_type="minference_with_dense").attn_type == "dense"
+    with pytest.raises(AssertionError):
+        MInferenceConfig(attn_type="vllm")
+    with pytest.raises(AssertionError):
+        MInferenceConfig(attn_type="minference", model_name="unknown/model")
+    assert get_support_models() == ["microsoft/Phi-3-mini-128k-instruct"]
+    with pytest.raises(ValueError):
+        MInference(attn_type="streaming")
+    with pytest.raises(NotImplementedError):
+        patch_hf(torch.nn.Module(), attn_type="hf")
+
+
+def test_registered_config_is_headline_mix():
+    from minference.configs.model2path import MODEL2PATH
+
+    cfg = json.load(open(MODEL2PATH["microsoft/Phi-3-mini-128k-instruct"]))
+    assert len(cfg) == 32 and all(len(layer) == 32 for layer in cfg)
+    kinds = [rec[0] for layer in cfg for rec in layer.values()]
+    assert kinds.count("stream_llm") == 512 and kinds.count("block_sparse") == 512
+    assert cfg == P.headline_config(seed=0)
+
+
+def test_mixed_config_counts_and_seed():
+    mix = [(0.3, P.record("stream_llm", 128, 4096)), (0.6, P.record("block_sparse", 100)),
+           (0.1, P.record("dense"))]
+    a, b = P.mixed_config(mix, seed=3), P.mixed_config(mix, seed=3)
+    assert a == b
+    kinds = [rec[0] for layer in a for rec in layer.values()]
+    assert (kinds.count("stream_llm"), kinds.count("block_sparse"), kinds.count("dense")) == (307, 614, 103)
+
+
+def test_load_layer_patterns(tmp_path):
+    path = tmp_path / "p.json"
+    P.write(str(path), P.uniform_config("block_sparse", 8, n_layers=2, n_heads=3))
+    pats = MF.load_layer_patterns(str(path), 1)
+    assert pats == {0: ["block_sparse", 8, 0, 1.0], 1: ["block_sparse", 8, 0, 1.0],
+                    2: ["block_sparse", 8, 0, 1.0]}
+    assert MF.load_layer_patterns(str(path), 5) == {}
+    assert MF.load_layer_patterns(str(tmp_path / "missing.json"), 0) == {}
+
+
+def test_build_layer_plan_semantics():
+    pats = {0: ["stream_llm", 100, 800, 0.9], 1: ["block_sparse", 1000, 0, 1.0],
+            2: ["dense", 0, 0, 1.0], 3: ["block_sparse", 0, 0, 1.0]}
+    plan = MF.build_layer_plan(pats, 4, 96, 4096)
+    s_sp, s_de = 128 ** -0.5, 1.0 / math.sqrt(96)  # dense: 1/sqrt(D) as attention.py:210-211
+    assert plan.heads[0] == (_abi.MSA_KIND_STREAM, 100, 800, -1, s_sp)
+    assert plan.heads[1] == (_abi.MSA_KIND_BLOCK, 64, 0, 0, s_sp)   # clamped to n_blocks
+    assert plan.heads[2] == (_abi.MSA_KIND_DENSE, 0, 0, -1, s_de)
+    assert plan.heads[3] == (_abi.MSA_KIND_BLOCK, 1, 0, 1, s_sp)    # clamped to >= 1
+    assert plan.block_heads == (1, 3) and plan.block_topk == (64, 1) and plan.topk_max == 64
+    assert not plan.all_dense
+    with pytest.raises(NotImplementedError):
+        MF.build_layer_plan({0: pats[0]}, 2, 96, 4096)  # head 1 -> default vertical_and_slash
+    with pytest.raises(ValueError):
+        MF.build_layer_plan({0: ["a_shape", 1, 2, 3]}, 1, 96, 4096)
+
+
+# ---------------------------------------------------------------------------
+# HF patch plumbing on a tiny Phi-3 (CPU, test double for the launch)
+# ---------------------------------------------------------------------------
+def _oracle_launch(q, k, v, plan, out):
+    """CPU stand-in for run_layer_attention: the oracle per head kind."""
+    qn = q.detach().float().numpy()
+    kn = k.detach().float().numpy()
+    vn = v.detach().float().numpy()
+    H, Hkv = qn.shape[1], kn.shape[1]
+    rep = H // Hkv
+    kn, vn = np.repeat(kn, rep, 1), np.repeat(vn, rep, 1)
+    res = np.zeros(qn.shape)
+    for h, (kind, p1, p2, slot, scale) in enumerate(plan.heads):
+        sl = slice(h, h + 1)
+        if kind == _abi.MSA_KIND_STREAM:
+            res[:, sl] = O.streaming_attention(qn[:, sl], kn[:, sl], vn[:, sl], p1, p2, scale=scale)
+        elif kind == _abi.MSA_KIND_BLOCK:
+            idx, _ = O.select_block_sparse_topk_indices(qn[:, sl], kn[:, sl], p1, "fp32", scale)
+            res[:, sl] = O.block_sparse_from_indices(qn[:, sl], kn[:, sl], vn[:, sl], idx, scale=scale)
+        else:
+            res[:, sl] = O.dense_causal(qn[:, sl], kn[:, sl], vn[:, sl], scale=scale)
+    out.copy_(torch.from_numpy(res).to(out.dtype))
+    return out
+
+
+def _tiny_phi3(n_heads=2, n_kv=2, layers=2, seed=0):
+    from transformers import Phi3Config, Phi3ForCausalLM
+
+    torch.manual_seed(seed)
+    cfg = Phi3Config(hidden_size=96 * n_heads, intermediate_size=256, num_hidden_layers=layers,
+                     num_attention_heads=n_heads, num_key_value_heads=n_kv, vocab_size=128,
+                     max_position_embeddings=4096, pad_token_id=0, bos_token_id=1,
+                     eos_token_id=2)
+    return Phi3ForCausalLM(cfg).eval()
+
+
+@pytest.fixture
+def cpu_launch(monkeypatch):
+    monkeypatch.setattr(MF, "run_layer_attention", _oracle_launch)
+
+
+@pytest.mark.parametrize("n_kv", [2, 1])
+def test_patched_dense_matches_hf(tmp_path, cpu_launch, n_kv):
+    model = _tiny_phi3(n_kv=n_kv)
+    ids = torch.randint(3, 128, (1, 150), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        ref = model(ids).logits
+    path = tmp_path / "dense.json"
+    P.write(str(path), P.uniform_config("dense", n_layers=2, n_heads=2))
+    patched = MInference(attn_type="minference", config_path=str(path))(model)
+    assert patched.config._attn_implementation == "minference"
+    assert patched.config.minference_attn_type == "minference"
+    with torch.no_grad():
+        got = patched(ids).logits
+    assert torch.allclose(got, ref, atol=2e-4, rtol=1e-3), (got - ref).abs().max()
+
+
+def test_patched_decode_with_cache_matches_hf(tmp_path, cpu_launch):
+    model = _tiny_phi3()
+    ids = torch.randint(3, 128, (1, 40), generator=torch.Generator().manual_seed(2))
+    with torch.no_grad():
+        ref = model.generate(ids, max_new_tokens=4, do_sample=False, use_cache=True)
+    path = tmp_path / "dense.json"
+    P.write(str(path), P.uniform_config("dense", n_layers=2, n_heads=2))
+    patched = MInference(attn_type="minference", config_path=str(path))(model)
+    with torch.no_grad():
+        got = patched.generate(ids, max_new_tokens=4, do_sample=False, use_cache=True)
+    assert torch.equal(got, ref)
+
+
+def test_patched_sparse_layer_uses_plan(tmp_path, cpu_launch, monkeypatch):
+    """stream_llm / block_sparse heads reach the launch with the reference's
+    parameters and scale, and starting_layer keeps early layers dense."""
+    seen = []
+
+    def spy(q, k, v, plan, out):
+        seen.append(plan)
+        return _oracle_launch(q, k, v, plan, out)
+
+    monkeypatch.setattr(MF, "run_layer_attention", spy)
+    model = _tiny_phi3()
+    path = tmp_path / "mix.json"
+    cfg = [{"0": ["stream_llm", 16, 64, 1.0], "1": ["block_sparse", 2, 0, 1.0]}] * 2
+    P.write(str(path), cfg)
+    patched = patch_hf(model, "minference", {"config_path": str(path), "starting_layer": 1})
+    ids = torch.randint(3, 128, (1, 200), generator=torch.Generator().manual_seed(3))
+    with torch.no_grad():
+        patched(ids)
+    assert seen[0].all_dense and seen[0].heads[0][4] == 1.0 / math.sqrt(96)  # layer 0 < starting_layer
+    assert seen[1].heads[0] == (_abi.MSA_KIND_STREAM, 16, 64, -1, 128 ** -0.5)
+    assert seen[1].heads[1] == (_abi.MSA_KIND_BLOCK, 2, 0, 0, 128 ** -0.5)
+
+
+def test_hf_attn_type_leaves_model_unpatched():
+    model = _tiny_phi3()
+    fwd = model.model.layers[0].self_attn.forward
+    assert MInference(attn_type="hf")(model) is model
+    assert model.model.layers[0].self_attn.forward == fwd
