@@ -319,8 +319,8 @@ void attn_kernel(AttnParams P) {
 
   // Tile staging through buffer loads: the descriptor is rebased on each tile
   // (scalar work) and bounded so that K rows at or past S_k read as zero.
-  u32x4 kr[STG], vr[STG];
-  auto load_tile = [&](int t) {
+  // Two register sets alternate so each tile is loaded two tiles ahead.
+  auto load_tile = [&](int t, u32x4 (&kr)[STG], u32x4 (&vr)[STG]) {
     const int j0 = t * kBlock;
     const int rows = min(kBlock, P.s_k - j0);
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
@@ -335,7 +335,7 @@ void attn_kernel(AttnParams P) {
       vr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[u], 0, 0));
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int buf, const u32x4 (&kr)[STG], const u32x4 (&vr)[STG]) {
     unsigned char* base = lds + buf * TILE_BYTES;
 #pragma unroll
     for (int u = 0; u < STG; ++u) {
@@ -355,24 +355,13 @@ void attn_kernel(AttnParams P) {
   float l = 0.0f;
   const float c_log2 = hd.scale_log2;
   const int arow = a0 + 32 * rh + n;  // absolute position of this lane's query row
+  // per-lane mask bounds: causal and S_k end; the stream band start and sinks
+  const int key_hi = min(arow, P.s_k - 1);
+  const int band_lo = kind == KIND_STREAM ? arow - n_local + 1 : 0;
+  const int sink_hi = kind == KIND_STREAM ? n_init : 0;
 
-  bool mt = false;
-  int t = cur.next(mt);
-  if (t >= 0) {
-    load_tile(t);
-    store_tile(0);
-  }
-  __syncthreads();
-  // Q is complete here; re-define it so no later wait is attributed to its loads.
-#pragma unroll
-  for (int kk = 0; kk < NKS; ++kk) asm volatile("" : "+v"(qb[kk]));
-
-  int buf = 0;
-  while (t >= 0) {
-    bool mtn = false;
-    const int tn = cur.next(mtn);
-    if (tn >= 0) load_tile(tn);
-    const unsigned char* tb = lds + buf * TILE_BYTES;
+  // one tile: QK^T, mask (boundary tiles only), online softmax, PV
+  auto step = [&](const unsigned char* tb, int t, bool mt) {
 
     // S^T[key][row]: 32 keys (this wave's half) x 32 rows
     u32x4 ka[NKS];
@@ -392,22 +381,26 @@ void attn_kernel(AttnParams P) {
       for (int tt = 0; tt < 2; ++tt) vop[db][tt] = *reinterpret_cast<const u32x4*>(tb + va[db][tt]);
     __builtin_amdgcn_sched_barrier(0);
 
-    if (mt) {
+    if (mt) {  // visible iff j <= key_hi and (j >= band_lo or j < sink_hi)
       const int jb = t * kBlock + 32 * kh + 4 * g;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int j = jb + 8 * (i >> 2) + (i & 3);
-        bool vis = (j <= arow) && (j < P.s_k);
-        if (kind == KIND_STREAM) vis = vis && ((j >= arow - n_local + 1) || (j < n_init));
-        if (!vis) s[i] = -__builtin_inff();
+        const bool vis = (j <= key_hi) & ((j >= band_lo) | (j < sink_hi));
+        s[i] = vis ? s[i] : -__builtin_inff();
       }
     }
-    // row max of the raw scores (lanes n and n+32 hold the two 16-key halves)
+    // row max of the raw scores; lanes n and n+32 hold the two 16-key halves
+    // of row n and exchange them with one permlane32 swap
     float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
 #pragma unroll
     for (int i = 3; i < 15; i += 2) mx = fmaxf(fmaxf(mx, s[i]), s[i + 1]);
     mx = fmaxf(mx, s[15]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c_log2;
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                       false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c_log2;
+    }
     if (__ballot(mx > m + 8.0f)) {  // wave-uniform: some row grew past the slack
       const float mnew = fmaxf(m, mx);
       const float alpha = __builtin_amdgcn_exp2f(m - mnew);
@@ -438,15 +431,53 @@ void attn_kernel(AttnParams P) {
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) o[db] = mfma_pv(vop[db][tt], pb[tt], o[db]);
 
-    if (tn >= 0) store_tile(buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
-    t = tn;
-    mt = mtn;
+  };
+
+  // Pipeline: tile i is computed from LDS buffer i&1 while tiles i+1 and
+  // i+2 are in flight in the two register sets; after the step the set
+  // holding tile i+1 is written to the other buffer and reloaded with i+3.
+  u32x4 kra[STG], vra[STG], krb[STG], vrb[STG];
+  bool mt = false, ma = false, mb = false;
+  int t = cur.next(mt);
+  if (t >= 0) {
+    load_tile(t, kra, vra);
+    store_tile(0, kra, vra);
   }
+  int ta = cur.next(ma);
+  if (ta >= 0) load_tile(ta, kra, vra);
+  int tb2 = cur.next(mb);
+  if (tb2 >= 0) load_tile(tb2, krb, vrb);
+  __syncthreads();
+  // Q is complete here; re-define it so no later wait is attributed to its loads.
+#pragma unroll
+  for (int kk = 0; kk < NKS; ++kk) asm volatile("" : "+v"(qb[kk]));
+
+  while (t >= 0) {
+    step(lds, t, mt);
+    if (ta < 0) break;
+    store_tile(1, kra, vra);
+    t = ta;
+    mt = ma;
+    ta = cur.next(ma);
+    if (ta >= 0) load_tile(ta, kra, vra);
+    __syncthreads();
+
+    step(lds + TILE_BYTES, t, mt);
+    if (tb2 < 0) break;
+    store_tile(0, krb, vrb);
+    t = tb2;
+    mt = mb;
+    tb2 = cur.next(mb);
+    if (tb2 >= 0) load_tile(tb2, krb, vrb);
+    __syncthreads();
+  }
+  __syncthreads();
 
   // ---- merge the two key halves of each row half; kh == 0 writes the rows
-  l += __shfl_xor(l, 32, 64);
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
   float* mo = reinterpret_cast<float*>(lds);  // [rh][NDB][16][64]
   float* mm = mo + 2 * NDB * 16 * 64;         // [rh][64]
   float* ml = mm + 2 * 64;                    // [rh][64]

@@ -96,7 +96,8 @@ _LIB_LOCK = threading.Lock()
 
 
 def library_path() -> str:
-    return os.environ.get("MINFERENCE_MSA_LIB", LIB_PATH)
+    """libmsa.so next to the package, or the build named by MINFERENCE_MSA_LIB."""
+    return os.environ.get("MINFERENCE_MSA_LIB") or LIB_PATH
 
 
 def load_library() -> ctypes.CDLL:
