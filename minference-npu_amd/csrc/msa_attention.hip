@@ -13,19 +13,21 @@
 // Rows with no visible key produce 0 (the reference's nan_to_num).
 //
 // CDNA4 mapping (one workgroup = 4 wave64 = one 64-row query block):
-//   wave w = (row half rh, key half kh) owns query rows [32rh, 32rh+32) and
-//   keys [32kh, 32kh+32) of every tile, with a private online-softmax state;
-//   the two key halves of a row half merge once at the end.
-//   S^T = K.Q^T on v_mfma_f32_32x32x16_{bf16,f16} (A = K tile from LDS,
-//   B = Q from registers), so the accumulator layout (one query row per lane)
-//   is directly the B operand of O^T = V^T.P^T on v_mfma_f32_32x32x16_f16.
-//   P is rounded to fp16 (11-bit mantissa) for the PV product.
-//   V is staged once per layer as fp16 V^T with keys permuted inside each
-//   16-key group so every PV A operand is one 16-byte LDS read.
-//   K and V^T tiles are double-buffered in LDS (XOR-swizzled 16-byte slots,
-//   no bank conflicts) and the next tile is prefetched by buffer loads.
+//   wave w owns all 64 query rows and the 16-key chunk [16w, 16w+16) of every
+//   tile, with a private online-softmax state; the four chunk partials of a
+//   row merge once at the end.  The main loop touches no LDS and has no
+//   barrier: K and V operands go from L2 straight into registers.
+//   S^T = K.Q^T on v_mfma_f32_16x16x32_{bf16,f16}: A = K chunk (native
+//   [S][D] rows), B = Q (registers for the whole item), one 16-row group per
+//   accumulator.  One v_permlane16_swap per register pair turns two 16-row
+//   accumulators (rounded to fp16) into the B operand of
+//   O^T = V^T.P^T on v_mfma_f32_32x32x16_f16, whose A operand comes from V
+//   staged once per layer as fp16 in exact operand order (one 1 KB load per
+//   32 dims).
 //   The running max moves only when a row max grows by more than 2^8, so the
-//   O rescale is rare; the row max needs one lane^32 exchange per tile.
+//   O rescale is rare.  Row maxima and sums reduce over the four lanes of a
+//   row with two permlane swaps; the 64 row values of a wave then sit one
+//   per lane.
 //   Tiles that need no mask run first; boundary tiles (diagonal, band start,
 //   partial sink, S_k end) run last with the elementwise mask.
 
@@ -40,21 +42,17 @@ constexpr int KIND_DENSE = 0;
 constexpr int KIND_STREAM = 1;
 constexpr int KIND_BLOCK = 2;
 
-// Position of key p inside its 16-key group in the staged V^T rows: quads 1
-// and 2 are swapped (an involution, so it also maps position -> key).
-__device__ inline int vt_perm(int p) {
-  const int q = (p >> 2) & 3;
-  const int qs = ((q & 1) << 1) | (q >> 1);
-  return (p & ~12) | (qs << 2);
-}
-
 // ---------------------------------------------------------------------------
-// V [B][Hkv][S][D] (bf16/fp16) -> V^T [B*Hkv][D][s_pad] fp16, keys permuted,
-// zero padded to s_pad = 64 * n_kb.
+// V [B][Hkv][S][D] (bf16/fp16) -> fp16 PV operands, zero padded to
+// s_pad = 64 * n_kb keys:
+//   Vop[B*Hkv][chunk = key/16][D/32][lane 0..63][8]
+//   lane l of 32-dim block db holds V[16 chunk + 8 (l >> 5) + e][32 db + (l & 31)], e = 0..7
+// so a wave reads the A operand of one 32x32x16 MFMA as one contiguous 1 KB.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(256) void vt_kernel(VtParams P) {
   constexpr int KCH = D / 8;
+  constexpr int NDB = D / 32;
   constexpr int LP = D + 8;  // padded LDS row (halves)
   __shared__ __align__(16) uint16_t tile[kBlock * LP];
   const int j0 = blockIdx.x * kBlock;
@@ -78,18 +76,22 @@ __global__ __launch_bounds__(256) void vt_kernel(VtParams P) {
     store16(&tile[r * LP + c * 8], out);
   }
   __syncthreads();
-  uint16_t* dst = P.vt + int64_t(bk) * D * P.s_pad;
-  for (int ci = threadIdx.x; ci < D * 8; ci += 256) {
-    const int d = ci >> 3, c = ci & 7;
+  // the tile's 4 chunks are 64*D consecutive halves starting at key j0
+  uint16_t* dst = P.vt + (int64_t(bk) * P.s_pad + j0) * D;
+  for (int ci = threadIdx.x; ci < 4 * NDB * 64; ci += 256) {
+    const int l = ci & 63;
+    const int cd = ci >> 6;  // chunk * NDB + db
+    const int c = cd / NDB, db = cd - c * NDB;
+    const int key0 = 16 * c + 8 * (l >> 5);
+    const int d = 32 * db + (l & 31);
     u32x4 out;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int p0 = c * 8 + 2 * e;
-      const uint16_t lo = tile[vt_perm(p0) * LP + d];
-      const uint16_t hi = tile[vt_perm(p0 + 1) * LP + d];
+      const uint16_t lo = tile[(key0 + 2 * e) * LP + d];
+      const uint16_t hi = tile[(key0 + 2 * e + 1) * LP + d];
       out[e] = uint32_t(lo) | (uint32_t(hi) << 16);
     }
-    store16(dst + int64_t(d) * P.s_pad + j0 + c * 8, out);
+    store16(dst + ci * 8, out);
   }
 }
 
@@ -114,18 +116,20 @@ hipError_t launch_vt(const VtParams& p, int dtype, int D, hipStream_t st) {
 // ---------------------------------------------------------------------------
 // attention
 // ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <typename T>
-__device__ inline f32x16 mfma_qk(u32x4 a, u32x4 b, f32x16 c);
+__device__ inline f32x4 mfma_qk(u32x4 a, u32x4 b, f32x4 c);
 
 template <>
-__device__ inline f32x16 mfma_qk<Bf16>(u32x4 a, u32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+__device__ inline f32x4 mfma_qk<Bf16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
 template <>
-__device__ inline f32x16 mfma_qk<F16>(u32x4 a, u32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+__device__ inline f32x4 mfma_qk<F16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
@@ -134,37 +138,110 @@ __device__ inline f32x16 mfma_pv(u32x4 a, u32x4 b, f32x16 c) {
                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// LDS slot swizzles (16-byte granules) that keep the MFMA operand reads free
-// of bank conflicts for 8- and 16-lane LDS phases.
-__device__ inline int k_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
-__device__ inline int v_swz(int d) { return (d ^ (d >> 3)) & 7; }
+// Lane-row exchanges (a lane row = 16 consecutive lanes, R0..R3).
+//   swap16(x, y): x <- [x.R0, y.R0, x.R2, y.R2], y <- [x.R1, y.R1, x.R3, y.R3]
+//   swap32(x, y): x <- [x.R0, x.R1, y.R0, y.R1], y <- [x.R2, x.R3, y.R2, y.R3]
+__device__ inline void swap16(uint32_t& x, uint32_t& y) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+  x = r[0];
+  y = r[1];
+}
+__device__ inline void swap16(float& x, float& y) {
+  uint32_t a = __float_as_uint(x), b = __float_as_uint(y);
+  swap16(a, b);
+  x = __uint_as_float(a);
+  y = __uint_as_float(b);
+}
+__device__ inline void swap32(float& x, float& y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  x = __uint_as_float(r[0]);
+  y = __uint_as_float(r[1]);
+}
 
-// Tile sequence of one work item as up to five segments: the first `nfull`
-// segments hold tiles that need no mask, the rest hold the boundary tiles.
-// For block_sparse heads the segments index the id list, otherwise they are
-// tile numbers.  Segment bounds are wave-uniform (scalar registers).
-struct Cursor {
-  int lo0, hi0, lo1, hi1, lo2, hi2, lo3, hi3, lo4, hi4;
-  int nfull;
-  int seg, i, hi;
+// Row layouts of a wave's 64 query rows.  In the QK accumulator of row group
+// g (rows 16g..16g+15) lane l holds 4 keys of row 16g + (l & 15); the 4 lane
+// rows hold different keys of the same 16 rows ("group layout", one register
+// per group).  A reduced row value lives one per lane in the "lane layout":
+// lane l holds row 16 * rho(l >> 4) + (l & 15), rho = (0, 2, 1, 3).  The PV
+// accumulator of row block rb holds row 32 rb + (l & 31) ("block layout").
+struct RowMax {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct RowSum {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+
+// group layout partials (4 groups) -> lane layout totals
+template <typename Op>
+__device__ inline float reduce_rows(float v0, float v1, float v2, float v3, Op op) {
+  swap32(v0, v1);
+  swap32(v2, v3);
+  float a = op(v0, v1), b = op(v2, v3);
+  swap16(a, b);
+  return op(a, b);
+}
+
+// lane layout -> group layout (each group's value in all 4 lane rows)
+__device__ inline void lanes_to_groups(float u, float (&g)[4]) {
+  float x = u, y = u;
+  swap16(x, y);  // x = [g0, g0, g1, g1], y = [g2, g2, g3, g3]
+  float x2 = x, y2 = y;
+  swap32(x, x2);
+  swap32(y, y2);
+  g[0] = x;
+  g[1] = x2;
+  g[2] = y;
+  g[3] = y2;
+}
+
+// lane layout -> block layout of row blocks 0 and 1
+__device__ inline void lanes_to_blocks(float u, float (&r)[2]) {
+  float x = u, y = u;
+  swap32(x, y);  // x = [g0, g2, g0, g2], y = [g1, g3, g1, g3]
+  swap16(x, y);
+  r[0] = x;
+  r[1] = y;
+}
+
+// Tile sequence of one work item: up to five segments [lo_k, hi_k) laid end
+// to end; positions before `mpos` hold tiles that need no mask, the rest the
+// boundary tiles.  For block_sparse heads the segments index the id list,
+// otherwise they are tile numbers.  Everything is wave-uniform (scalar
+// registers) and position -> tile is branch-free, so the main loop is a plain
+// counted loop.
+struct TileSeq {
+  int lo0, lo1, lo2, lo3, lo4;
+  int c1, c2, c3, c4, total;  // start position of segments 1..4, end of segment 4
+  int mpos;
   int n_kb;
   const int32_t* list;
 
-  __device__ void bounds(int k, int& lo, int& hi_) const {
-    lo = k == 0 ? lo0 : k == 1 ? lo1 : k == 2 ? lo2 : k == 3 ? lo3 : lo4;
-    hi_ = k == 0 ? hi0 : k == 1 ? hi1 : k == 2 ? hi2 : k == 3 ? hi3 : hi4;
-  }
-  // next tile (clamped into [0, n_kb) for memory safety) or -1
-  __device__ int next(bool& masked) {
-    while (i >= hi) {
-      if (++seg >= 5) return -1;
-      bounds(seg, i, hi);
+  __device__ void set(const int (&lo)[5], const int (&hi)[5], int nfull) {
+    int c = 0;
+    int cs[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+      cs[k] = c;
+      c += max(hi[k] - lo[k], 0);
     }
-    masked = seg >= nfull;
+    lo0 = lo[0]; lo1 = lo[1]; lo2 = lo[2]; lo3 = lo[3]; lo4 = lo[4];
+    c1 = cs[1]; c2 = cs[2]; c3 = cs[3]; c4 = cs[4];
+    total = c;
+    mpos = nfull == 1 ? c1 : c2;
+  }
+  // tile at position q, clamped into [0, n_kb) for memory safety; positions
+  // past the end repeat the last tile (loads that are never consumed)
+  __device__ int tile(int q) const {
+    q = max(min(q, total - 1), 0);
+    int i = lo4 + (q - c4);
+    i = q < c4 ? lo3 + (q - c3) : i;
+    i = q < c3 ? lo2 + (q - c2) : i;
+    i = q < c2 ? lo1 + (q - c1) : i;
+    i = q < c1 ? lo0 + q : i;
     const int t = list ? list[i] : i;
-    ++i;
     return min(max(t, 0), n_kb - 1);
   }
+  __device__ bool masked(int q) const { return q >= mpos; }
 };
 
 template <typename TO>
@@ -183,26 +260,28 @@ __device__ inline void store_out4_16(uint16_t* dst, float a, float b, float c, f
   *reinterpret_cast<uint2*>(dst) = v;
 }
 
+template <int D>
+struct AttnShape {
+  static constexpr int NKS = D / 32;              // QK k-steps of 32 dims (= K loads per chunk)
+  static constexpr int NDB = D / 32;              // PV output blocks of 32 dims (= V loads)
+  static constexpr int CHUNK_BYTES = 16 * D * 2;  // one staged 16-key V chunk
+  static constexpr int NO = NDB * 2 * 16;         // O accumulator floats per lane
+  static constexpr int SLOT = (NO + 4) * 64;      // merge slot of one wave (floats)
+};
+
 template <typename T, bool OUT_F32, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D > 96 ? 1 : 2)))
 void attn_kernel(AttnParams P) {
-  constexpr int KCH = D / 8;   // 16-byte chunks per K row
-  constexpr int NKS = D / 16;  // QK^T k-steps (16 dims each)
-  constexpr int NDB = D / 32;  // PV output blocks of 32 dims
-  constexpr int STG = D / 32;  // staged chunks per thread for K and for V^T
-  constexpr int K_BYTES = kBlock * D * 2;         // K tile
-  constexpr int TILE_BYTES = 2 * K_BYTES;         // K tile + V^T tile
-  constexpr int MERGE_BYTES = (2 * NDB * 16 * 64 + 4 * 64) * 4;
-  constexpr int LDS_BYTES = 2 * TILE_BYTES > MERGE_BYTES ? 2 * TILE_BYTES : MERGE_BYTES;
-  __shared__ __align__(16) unsigned char lds[LDS_BYTES];
+  using S = AttnShape<D>;
+  constexpr int NKS = S::NKS;
+  constexpr int NDB = S::NDB;
+  __shared__ __align__(16) float lds[3 * S::SLOT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int n = lane & 31;
-  const int g = lane >> 5;
-  const int w = tid >> 6;
-  const int rh = w >> 1;  // query rows 32rh .. 32rh+31
-  const int kh = w & 1;   // keys 32kh .. 32kh+31 of every tile
+  const int lr = lane >> 4;  // lane row
+  const int lc = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // keys 16w .. 16w+15 of every tile
 
   // ---- work item.  Workgroups are dispatched round-robin over the 8 XCDs;
   // each XCD walks its own heads one at a time (query blocks longest-first),
@@ -235,13 +314,9 @@ void attn_kernel(AttnParams P) {
   // tile t needs no mask for the causal / S_k bounds iff t < F
   const int Fe = min(min((a0 + 1) >> 6, P.s_k >> 6), last_tile + 1);
 
-  Cursor cur;
-  cur.lo0 = cur.hi0 = cur.lo1 = cur.hi1 = cur.lo2 = cur.hi2 = 0;
-  cur.lo3 = cur.hi3 = cur.lo4 = cur.hi4 = 0;
-  cur.seg = -1;
-  cur.i = cur.hi = 0;
-  cur.n_kb = P.n_kb;
-  cur.list = nullptr;
+  TileSeq seq;
+  seq.n_kb = P.n_kb;
+  seq.list = nullptr;
   if (kind == KIND_BLOCK) {
     // canonical list: ascending causal ids, so the boundary ids come last
     const int64_t base = (int64_t(b) * P.idx_slots + hd.slot) * P.n_qb + bq;
@@ -249,11 +324,8 @@ void attn_kernel(AttnParams P) {
     const int32_t* list = P.idx + base * P.topk_max;
     int nf = cnt;
     while (nf > 0 && list[nf - 1] >= Fe) --nf;
-    cur.list = list;
-    cur.hi0 = nf;
-    cur.lo1 = nf;
-    cur.hi1 = cnt;
-    cur.nfull = 1;
+    seq.list = list;
+    seq.set({0, nf, 0, 0, 0}, {nf, cnt, 0, 0, 0}, 1);
   } else if (kind == KIND_STREAM) {
     const int lo = min(max(a0 - n_local + 1, 0) >> 6, last_tile + 1);
     const int nsink = min((min(max(n_init, 0), P.s_k) + 63) >> 6, lo);
@@ -262,263 +334,253 @@ void attn_kernel(AttnParams P) {
     bf0 = bf0 <= 0 ? 0 : (bf0 + 63) >> 6;
     bf0 = min(max(bf0, lo), last_tile + 1);
     const int fb_hi = max(bf0, Fe);
-    cur.hi0 = sf;                       // full sink
-    cur.lo1 = bf0; cur.hi1 = fb_hi;     // full band
-    cur.lo2 = sf; cur.hi2 = nsink;      // partial sink
-    cur.lo3 = lo; cur.hi3 = bf0;        // band tiles cut by the window start
-    cur.lo4 = fb_hi; cur.hi4 = last_tile + 1;  // diagonal / S_k boundary
-    cur.nfull = 2;
+    // full sink, full band | partial sink, band tiles cut by the window
+    // start, diagonal / S_k boundary
+    seq.set({0, bf0, sf, lo, fb_hi}, {sf, fb_hi, nsink, bf0, last_tile + 1}, 2);
   } else {
-    cur.hi0 = Fe;
-    cur.lo1 = Fe; cur.hi1 = last_tile + 1;
-    cur.nfull = 1;
+    seq.set({0, Fe, 0, 0, 0}, {Fe, last_tile + 1, 0, 0, 0}, 1);
   }
 
   const unsigned char* kbytes = reinterpret_cast<const unsigned char*>(P.k) +
                                 2 * (b * P.k_sb + int64_t(kvh) * P.k_sh);
-  const unsigned char* vtbytes = reinterpret_cast<const unsigned char*>(P.vt) +
-                                 2 * ((int64_t(b) * (P.heads / P.kv_group) + kvh) * D * int64_t(P.s_pad));
   const int64_t kss2 = 2 * P.k_ss;
+  const int64_t bk = int64_t(b) * (P.heads / P.kv_group) + kvh;
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.vt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
 
-  // ---- Q rows 32rh.. as the B operand: lane (n, g) holds Q[row][16ks + 8g .. +7]
-  u32x4 qb[NKS];
+  // ---- Q as the B operand: lane (lc, lr) of group g, k-step ks holds
+  // Q[q0 + 16g + lc][32ks + 8lr .. +7]
+  u32x4 qb[4][NKS];
   {
     const uint16_t* qbase =
         reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + int64_t(h) * P.q_sh;
-    const int row = q0 + 32 * rh + n;
 #pragma unroll
-    for (int kk = 0; kk < NKS; ++kk)
-      qb[kk] = row < P.s_q ? load16(qbase + int64_t(row) * P.q_ss + 16 * kk + 8 * g)
-                           : zero_u32x4();
+    for (int g = 0; g < 4; ++g) {
+      const int row = q0 + 16 * g + lc;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        qb[g][ks] = row < P.s_q ? load16(qbase + int64_t(row) * P.q_ss + 32 * ks + 8 * lr)
+                                : zero_u32x4();
+    }
   }
 
-  // ---- loop-invariant staging offsets (global bytes within a tile, LDS bytes)
-  uint32_t koff[STG], voff[STG], kslot[STG], vslot[STG];
-#pragma unroll
-  for (int u = 0; u < STG; ++u) {
-    const int ci = tid + 256 * u;
-    const int r = ci / KCH, c = ci - r * KCH;
-    koff[u] = uint32_t(r) * uint32_t(kss2) + 16u * c;
-    kslot[u] = 16u * (r * KCH + (c ^ k_swz(r)));
-    const int d = ci >> 3, c2 = ci & 7;
-    voff[u] = uint32_t(d) * uint32_t(2 * P.s_pad) + 16u * c2;
-    vslot[u] = K_BYTES + 16u * (d * 8 + (c2 ^ v_swz(d)));
-  }
-  // MFMA A-operand LDS offsets: K rows of this lane, V^T rows 32db + n
-  const int krow = 32 * kh + n;
-  const uint32_t ka0 = 16u * (krow * KCH + (g ^ k_swz(krow)));
-  const uint32_t ka1 = 16u * (krow * KCH + ((2 + g) ^ k_swz(krow)));
-  uint32_t va[NDB][2];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    const int d = 32 * db + n;
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-      va[db][tt] = K_BYTES + 16u * (d * 8 + ((4 * kh + 2 * tt + g) ^ v_swz(d)));
-  }
-
-  // Tile staging through buffer loads: the descriptor is rebased on each tile
-  // (scalar work) and bounded so that K rows at or past S_k read as zero.
-  // Two register sets alternate so each tile is loaded two tiles ahead.
-  auto load_tile = [&](int t, u32x4 (&kr)[STG], u32x4 (&vr)[STG]) {
+  // K chunk operand: lane (lc, lr) reads K[j0 + 16w + lc][32ks + 8lr .. +7].
+  // The descriptor is rebased on each tile and bounded so that rows at or
+  // past S_k read as zero.
+  const uint32_t krow_off = uint32_t(16 * w + lc) * uint32_t(kss2) + 16u * lr;
+  auto load_k = [&](int t, u32x4 (&kr)[NKS]) {
     const int j0 = t * kBlock;
     const int rows = min(kBlock, P.s_k - j0);
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<unsigned char*>(kbytes + int64_t(j0) * kss2), short(0),
-        int(rows * kss2), 0x00020000);
-    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<unsigned char*>(vtbytes + 2 * int64_t(j0)), short(0),
-        int(D * 2 * P.s_pad - 2 * j0), 0x00020000);
+        const_cast<unsigned char*>(kbytes + int64_t(j0) * kss2), short(0), int(rows * kss2),
+        0x00020000);
 #pragma unroll
-    for (int u = 0; u < STG; ++u) {
-      kr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff[u], 0, 0));
-      vr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[u], 0, 0));
-    }
+    for (int ks = 0; ks < NKS; ++ks)
+      kr[ks] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, krow_off + 64u * ks, 0, 0));
   };
-  auto store_tile = [&](int buf, const u32x4 (&kr)[STG], const u32x4 (&vr)[STG]) {
-    unsigned char* base = lds + buf * TILE_BYTES;
+  auto load_v = [&](int t, u32x4 (&vr)[NDB]) {
+    const int soff = (4 * t + w) * S::CHUNK_BYTES;
 #pragma unroll
-    for (int u = 0; u < STG; ++u) {
-      *reinterpret_cast<u32x4*>(base + kslot[u]) = kr[u];
-      *reinterpret_cast<u32x4*>(base + vslot[u]) = vr[u];
-    }
+    for (int db = 0; db < NDB; ++db)
+      vr[db] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, 16u * lane + 1024u * db, soff, 0));
   };
 
-  f32x16 o[NDB];
+  f32x16 o[NDB][2];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
-  // m is the running max in scaled log2 units; it only moves when the row
-  // max exceeds it by more than 8, so P stays <= 2^8 between rescales.
-  float m = -1e30f;
-  float l = 0.0f;
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[db][rb][i] = 0.0f;
+  // Running max in scaled log2 units (lane layout m_u, group layout m_g); it
+  // only moves when a row max exceeds it by more than 8, so P <= 2^8.
+  float m_u = -1e30f;
+  float m_g[4] = {-1e30f, -1e30f, -1e30f, -1e30f};
+  float l_g[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // per-lane partial row sums, group layout
   const float c_log2 = hd.scale_log2;
-  const int arow = a0 + 32 * rh + n;  // absolute position of this lane's query row
-  // per-lane mask bounds: causal and S_k end; the stream band start and sinks
-  const int key_hi = min(arow, P.s_k - 1);
-  const int band_lo = kind == KIND_STREAM ? arow - n_local + 1 : 0;
-  const int sink_hi = kind == KIND_STREAM ? n_init : 0;
+  const int arow0 = a0 + lc;  // absolute position of this lane's row in group 0
+  const int skm1 = P.s_k - 1;
+  const bool is_stream = kind == KIND_STREAM;
+  const int sink_hi = is_stream ? n_init : 0;
 
-  // one tile: QK^T, mask (boundary tiles only), online softmax, PV
-  auto step = [&](const unsigned char* tb, int t, bool mt) {
+  auto qk = [&](const u32x4 (&kr)[NKS], f32x4 (&s)[4]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) s[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) s[g] = mfma_qk<T>(kr[ks], qb[g][ks], s[g]);
+  };
 
-    // S^T[key][row]: 32 keys (this wave's half) x 32 rows
-    u32x4 ka[NKS];
-#pragma unroll
-    for (int kk = 0; kk < NKS; ++kk)
-      ka[kk] = *reinterpret_cast<const u32x4*>(tb + ((kk & 1) ? ka1 : ka0) + 64u * (kk >> 1));
-    f32x16 s;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.0f;
-#pragma unroll
-    for (int kk = 0; kk < NKS; ++kk) s = mfma_qk<T>(ka[kk], qb[kk], s);
-    // V^T operands do not depend on P: read them now, under the softmax
-    u32x4 vop[NDB][2];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) vop[db][tt] = *reinterpret_cast<const u32x4*>(tb + va[db][tt]);
-    __builtin_amdgcn_sched_barrier(0);
-
+  // mask (boundary tiles only), online softmax, PV for one chunk
+  auto softmax_pv = [&](f32x4 (&s)[4], const u32x4 (&vr)[NDB], int t, bool mt) {
     if (mt) {  // visible iff j <= key_hi and (j >= band_lo or j < sink_hi)
-      const int jb = t * kBlock + 32 * kh + 4 * g;
+      const int jb = t * kBlock + 16 * w + 4 * lr;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int j = jb + 8 * (i >> 2) + (i & 3);
-        const bool vis = (j <= key_hi) & ((j >= band_lo) | (j < sink_hi));
-        s[i] = vis ? s[i] : -__builtin_inff();
+      for (int g = 0; g < 4; ++g) {
+        const int ar = arow0 + 16 * g;
+        const int key_hi = min(ar, skm1);
+        const int band_lo = is_stream ? ar - n_local + 1 : 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = jb + i;
+          const bool vis = (j <= key_hi) & ((j >= band_lo) | (j < sink_hi));
+          s[g][i] = vis ? s[g][i] : -__builtin_inff();
+        }
       }
     }
-    // row max of the raw scores; lanes n and n+32 hold the two 16-key halves
-    // of row n and exchange them with one permlane32 swap
-    float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+    float mloc[4];
 #pragma unroll
-    for (int i = 3; i < 15; i += 2) mx = fmaxf(fmaxf(mx, s[i]), s[i + 1]);
-    mx = fmaxf(mx, s[15]);
-    {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
-                                                       false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c_log2;
-    }
-    if (__ballot(mx > m + 8.0f)) {  // wave-uniform: some row grew past the slack
-      const float mnew = fmaxf(m, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-      m = mnew;
-      l *= alpha;
+    for (int g = 0; g < 4; ++g) mloc[g] = fmaxf(fmaxf(fmaxf(s[g][0], s[g][1]), s[g][2]), s[g][3]);
+    const float mx = reduce_rows(mloc[0], mloc[1], mloc[2], mloc[3], RowMax()) * c_log2;
+    if (__ballot(mx > m_u + 8.0f)) {  // wave-uniform: some row grew past the slack
+      const float mnew = fmaxf(m_u, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_u - mnew);
+      m_u = mnew;
+      lanes_to_groups(m_u, m_g);
+      float a_g[4], a_b[2];
+      lanes_to_groups(alpha, a_g);
+      lanes_to_blocks(alpha, a_b);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) l_g[g] *= a_g[g];
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-    }
-    // P = 2^(s*c - m) rounded to fp16; the row sum uses fp32 P
-    u32x4 pb[2];
-    float psum = 0.0f;
+        for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c_log2, -m));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i + 1], c_log2, -m));
-      psum += p0 + p1;
-      typedef float f2 __attribute__((ext_vector_type(2)));
-      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-      pb[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{p0, p1}, h2));
+          for (int i = 0; i < 16; ++i) o[db][rb][i] *= a_b[rb];
     }
-    l += psum;
-    __builtin_amdgcn_sched_barrier(0);
+    // P = 2^(s*c - m) rounded to fp16; the row sums use fp32 P
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    uint32_t pk[4][2];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][i], c_log2, -m_g[g]));
+      l_g[g] += (p[0] + p[1]) + (p[2] + p[3]);
+      pk[g][0] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{p[0], p[1]}, h2));
+      pk[g][1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{p[2], p[3]}, h2));
+    }
+    // groups 2rb, 2rb+1 -> B operand of row block rb (keys 8(l>>5) .. +7 of row 32rb + (l&31))
+    u32x4 pb[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      uint32_t x0 = pk[2 * rb][0], y0 = pk[2 * rb + 1][0];
+      uint32_t x1 = pk[2 * rb][1], y1 = pk[2 * rb + 1][1];
+      swap16(x0, y0);
+      swap16(x1, y1);
+      pb[rb] = u32x4{x0, x1, y0, y1};
+    }
     // O^T[d][row] += V^T[d][key] . P^T[key][row]
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) o[db] = mfma_pv(vop[db][tt], pb[tt], o[db]);
-
+      for (int rb = 0; rb < 2; ++rb) o[db][rb] = mfma_pv(vr[db], pb[rb], o[db][rb]);
   };
 
-  // Pipeline: tile i is computed from LDS buffer i&1 while tiles i+1 and
-  // i+2 are in flight in the two register sets; after the step the set
-  // holding tile i+1 is written to the other buffer and reloaded with i+3.
-  u32x4 kra[STG], vra[STG], krb[STG], vrb[STG];
-  bool mt = false, ma = false, mb = false;
-  int t = cur.next(mt);
-  if (t >= 0) {
-    load_tile(t, kra, vra);
-    store_tile(0, kra, vra);
+  // Pipeline over positions p: two register sets alternate (A: even p, B:
+  // odd p).  The K operands of position p+2 are requested as soon as QK of p
+  // has consumed the set, the V operands once PV has.  Loads are issued
+  // unconditionally (past the end they repeat the last tile), so every path
+  // through the loop has the same loads in flight and the waits stay exact.
+  // The tile number of p+3 is looked up one step before its loads.  The loop
+  // runs whole (A, B) pairs and an odd last position runs after it, so the
+  // loop has no exit between the two halves.
+  const int total = seq.total;
+  u32x4 kA[NKS], vA[NDB], kB[NKS], vB[NDB];
+  int tA = seq.tile(0), tB = seq.tile(1);
+  load_k(tA, kA);
+  load_v(tA, vA);
+  load_k(tB, kB);
+  load_v(tB, vB);
+  int tn = seq.tile(2);
+  auto step = [&](u32x4 (&kr)[NKS], u32x4 (&vr)[NDB], int& tcur, int p) {
+    f32x4 s[4];
+    qk(kr, s);
+    load_k(tn, kr);
+    const int tnn = seq.tile(p + 3);
+    softmax_pv(s, vr, tcur, seq.masked(p));
+    load_v(tn, vr);
+    tcur = tn;
+    tn = tnn;
+  };
+  int p = 0;
+  for (; p + 1 < total; p += 2) {
+    step(kA, vA, tA, p);
+    step(kB, vB, tB, p + 1);
   }
-  int ta = cur.next(ma);
-  if (ta >= 0) load_tile(ta, kra, vra);
-  int tb2 = cur.next(mb);
-  if (tb2 >= 0) load_tile(tb2, krb, vrb);
-  __syncthreads();
-  // Q is complete here; re-define it so no later wait is attributed to its loads.
-#pragma unroll
-  for (int kk = 0; kk < NKS; ++kk) asm volatile("" : "+v"(qb[kk]));
+  if (p < total) step(kA, vA, tA, p);
 
-  while (t >= 0) {
-    step(lds, t, mt);
-    if (ta < 0) break;
-    store_tile(1, kra, vra);
-    t = ta;
-    mt = ma;
-    ta = cur.next(ma);
-    if (ta >= 0) load_tile(ta, kra, vra);
-    __syncthreads();
-
-    step(lds + TILE_BYTES, t, mt);
-    if (tb2 < 0) break;
-    store_tile(0, krb, vrb);
-    t = tb2;
-    mt = mb;
-    tb2 = cur.next(mb);
-    if (tb2 >= 0) load_tile(tb2, krb, vrb);
-    __syncthreads();
-  }
-  __syncthreads();
-
-  // ---- merge the two key halves of each row half; kh == 0 writes the rows
-  {
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
-    l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-  }
-  float* mo = reinterpret_cast<float*>(lds);  // [rh][NDB][16][64]
-  float* mm = mo + 2 * NDB * 16 * 64;         // [rh][64]
-  float* ml = mm + 2 * 64;                    // [rh][64]
-  if (kh == 1) {
+  // ---- merge the four chunk partials of each row; wave 0 writes the rows
+  float m_b[2], l_b[2];
+  lanes_to_blocks(m_u, m_b);
+  lanes_to_blocks(reduce_rows(l_g[0], l_g[1], l_g[2], l_g[3], RowSum()), l_b);
+  if (w > 0) {
+    float* slot = lds + (w - 1) * S::SLOT;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mo[((rh * NDB + db) * 16 + i) * 64 + lane] = o[db][i];
-    mm[rh * 64 + lane] = m;
-    ml[rh * 64 + lane] = l;
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) slot[((db * 2 + rb) * 16 + i) * 64 + lane] = o[db][rb][i];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      slot[(S::NO + rb) * 64 + lane] = m_b[rb];
+      slot[(S::NO + 2 + rb) * 64 + lane] = l_b[rb];
+    }
   }
   __syncthreads();
-  if (kh == 1) return;
+  if (w > 0) return;
 
-  const float m_oth = mm[rh * 64 + lane];
-  const float l_oth = ml[rh * 64 + lane];
-  const float mt2 = fmaxf(m, m_oth);
-  const float f0 = __builtin_amdgcn_exp2f(m - mt2);
-  const float f1 = __builtin_amdgcn_exp2f(m_oth - mt2);
-  const float lt = l * f0 + l_oth * f1;
-  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  const float s0 = f0 * inv, s1 = f1 * inv;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    float mw[4], lw[4];
+    mw[0] = m_b[rb];
+    lw[0] = l_b[rb];
+#pragma unroll
+    for (int v = 1; v < 4; ++v) {
+      mw[v] = lds[(v - 1) * S::SLOT + (S::NO + rb) * 64 + lane];
+      lw[v] = lds[(v - 1) * S::SLOT + (S::NO + 2 + rb) * 64 + lane];
+    }
+    const float mt = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+    float f[4];
+    float lt = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      f[v] = __builtin_amdgcn_exp2f(mw[v] - mt);
+      lt += lw[v] * f[v];
+    }
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) f[v] *= inv;
 
-  const int row = q0 + 32 * rh + n;
-  if (row < P.s_q) {
-    const int64_t obase = b * P.o_sb + int64_t(h) * P.o_sh + int64_t(row) * P.o_ss;
+    const int row = q0 + 32 * rb + (lane & 31);
+    if (row < P.s_q) {
+      const int64_t obase = b * P.o_sb + int64_t(h) * P.o_sh + int64_t(row) * P.o_ss;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
+      for (int db = 0; db < NDB; ++db) {
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        float v4[4];
+        for (int qd = 0; qd < 4; ++qd) {
+          float v4[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * qd + e;
-          v4[e] = o[db][i] * s0 + mo[((rh * NDB + db) * 16 + i) * 64 + lane] * s1;
-        }
-        const int d = 32 * db + 8 * qd + 4 * g;
-        if constexpr (OUT_F32) {
-          store_out4<float>(reinterpret_cast<float*>(P.o) + obase + d, v4[0], v4[1], v4[2], v4[3]);
-        } else {
-          store_out4_16<T>(reinterpret_cast<uint16_t*>(P.o) + obase + d, v4[0], v4[1], v4[2], v4[3]);
+          for (int e = 0; e < 4; ++e) {
+            const int i = 4 * qd + e;
+            const int r = (db * 2 + rb) * 16 + i;
+            float acc = o[db][rb][i] * f[0];
+#pragma unroll
+            for (int v = 1; v < 4; ++v) acc += lds[(v - 1) * S::SLOT + r * 64 + lane] * f[v];
+            v4[e] = acc;
+          }
+          const int d = 32 * db + 8 * qd + 4 * (lane >> 5);
+          if constexpr (OUT_F32) {
+            store_out4<float>(reinterpret_cast<float*>(P.o) + obase + d, v4[0], v4[1], v4[2], v4[3]);
+          } else {
+            store_out4_16<T>(reinterpret_cast<uint16_t*>(P.o) + obase + d, v4[0], v4[1], v4[2], v4[3]);
+          }
         }
       }
     }

@@ -42,7 +42,7 @@ struct HeadArg {
 struct AttnParams {
   const void* q;
   const void* k;
-  const uint16_t* vt;  // [batch*kv_heads][D][s_pad] fp16, keys permuted within 16
+  const uint16_t* vt;  // [batch*kv_heads][s_pad/16][D/32][64][8] fp16 PV operands (vt_kernel)
   void* o;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
