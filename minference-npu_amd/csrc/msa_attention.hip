@@ -38,6 +38,8 @@
 
 namespace msa {
 
+#define INLINE __attribute__((always_inline))
+
 constexpr int KIND_DENSE = 0;
 constexpr int KIND_STREAM = 1;
 constexpr int KIND_BLOCK = 2;
@@ -368,7 +370,7 @@ void attn_kernel(AttnParams P) {
   // The descriptor is rebased on each tile and bounded so that rows at or
   // past S_k read as zero.
   const uint32_t krow_off = uint32_t(16 * w + lc) * uint32_t(kss2) + 16u * lr;
-  auto load_k = [&](int t, u32x4 (&kr)[NKS]) {
+  auto load_k = [&](int t, u32x4 (&kr)[NKS]) INLINE {
     const int j0 = t * kBlock;
     const int rows = min(kBlock, P.s_k - j0);
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
@@ -377,14 +379,15 @@ void attn_kernel(AttnParams P) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
       kr[ks] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, krow_off + 64u * ks, 0, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, krow_off, 64 * ks, 0));
   };
-  auto load_v = [&](int t, u32x4 (&vr)[NDB]) {
+  const uint32_t vlane_off = 16u * lane;
+  auto load_v = [&](int t, u32x4 (&vr)[NDB]) INLINE {
     const int soff = (4 * t + w) * S::CHUNK_BYTES;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
       vr[db] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, 16u * lane + 1024u * db, soff, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vlane_off, soff + 1024 * db, 0));
   };
 
   f32x16 o[NDB][2];
@@ -394,9 +397,9 @@ void attn_kernel(AttnParams P) {
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[db][rb][i] = 0.0f;
-  // Running max in scaled log2 units (lane layout m_u, group layout m_g); it
-  // only moves when a row max exceeds it by more than 8, so P <= 2^8.
-  float m_u = -1e30f;
+  // Running max per row in scaled log2 units, group layout (each group's
+  // value in all 4 lane rows).  It only moves when some P would exceed 2^8,
+  // so the O rescale is rare.
   float m_g[4] = {-1e30f, -1e30f, -1e30f, -1e30f};
   float l_g[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // per-lane partial row sums, group layout
   const float c_log2 = hd.scale_log2;
@@ -405,81 +408,95 @@ void attn_kernel(AttnParams P) {
   const bool is_stream = kind == KIND_STREAM;
   const int sink_hi = is_stream ? n_init : 0;
 
-  auto qk = [&](const u32x4 (&kr)[NKS], f32x4 (&s)[4]) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) s[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // A step works on two 32-row halves h (groups 2h, 2h+1 = PV row block h) so
+  // that the softmax of one half overlaps the MFMAs of the other.
+  auto qk_half = [&](const u32x4 (&kr)[NKS], int hf, f32x4 (&s)[2]) INLINE {
+    s[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    s[1] = s[0];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) s[g] = mfma_qk<T>(kr[ks], qb[g][ks], s[g]);
+      for (int gg = 0; gg < 2; ++gg) s[gg] = mfma_qk<T>(kr[ks], qb[2 * hf + gg][ks], s[gg]);
   };
-
-  // mask (boundary tiles only), online softmax, PV for one chunk
-  auto softmax_pv = [&](f32x4 (&s)[4], const u32x4 (&vr)[NDB], int t, bool mt) {
-    if (mt) {  // visible iff j <= key_hi and (j >= band_lo or j < sink_hi)
-      const int jb = t * kBlock + 16 * w + 4 * lr;
+  // visible iff j <= key_hi and (j >= band_lo or j < sink_hi)
+  auto mask_half = [&](f32x4 (&s)[2], int hf, int t) INLINE {
+    const int jb = t * kBlock + 16 * w + 4 * lr;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int ar = arow0 + 16 * g;
-        const int key_hi = min(ar, skm1);
-        const int band_lo = is_stream ? ar - n_local + 1 : 0;
+    for (int gg = 0; gg < 2; ++gg) {
+      const int ar = arow0 + 16 * (2 * hf + gg);
+      const int key_hi = min(ar, skm1);
+      const int band_lo = is_stream ? ar - n_local + 1 : 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = jb + i;
-          const bool vis = (j <= key_hi) & ((j >= band_lo) | (j < sink_hi));
-          s[g][i] = vis ? s[g][i] : -__builtin_inff();
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int j = jb + i;
+        const bool vis = (j <= key_hi) & ((j >= band_lo) | (j < sink_hi));
+        s[gg][i] = vis ? s[gg][i] : -__builtin_inff();
       }
     }
-    float mloc[4];
+  };
+  // P = 2^(s*c - m) in place, with the current running max.  Returns true
+  // when some P exceeds 2^8 (P >= 0, so the float bits order like integers).
+  auto exp_half = [&](f32x4 (&s)[2], int hf) INLINE -> bool {
+    uint32_t mx = 0;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) mloc[g] = fmaxf(fmaxf(fmaxf(s[g][0], s[g][1]), s[g][2]), s[g][3]);
-    const float mx = reduce_rows(mloc[0], mloc[1], mloc[2], mloc[3], RowMax()) * c_log2;
-    if (__ballot(mx > m_u + 8.0f)) {  // wave-uniform: some row grew past the slack
-      const float mnew = fmaxf(m_u, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m_u - mnew);
-      m_u = mnew;
-      lanes_to_groups(m_u, m_g);
-      float a_g[4], a_b[2];
-      lanes_to_groups(alpha, a_g);
-      lanes_to_blocks(alpha, a_b);
+    for (int gg = 0; gg < 2; ++gg)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) l_g[g] *= a_g[g];
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) o[db][rb][i] *= a_b[rb];
-    }
-    // P = 2^(s*c - m) rounded to fp16; the row sums use fp32 P
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    uint32_t pk[4][2];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      float p[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][i], c_log2, -m_g[g]));
-      l_g[g] += (p[0] + p[1]) + (p[2] + p[3]);
-      pk[g][0] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{p[0], p[1]}, h2));
-      pk[g][1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{p[2], p[3]}, h2));
-    }
-    // groups 2rb, 2rb+1 -> B operand of row block rb (keys 8(l>>5) .. +7 of row 32rb + (l&31))
-    u32x4 pb[2];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      uint32_t x0 = pk[2 * rb][0], y0 = pk[2 * rb + 1][0];
-      uint32_t x1 = pk[2 * rb][1], y1 = pk[2 * rb + 1][1];
-      swap16(x0, y0);
-      swap16(x1, y1);
-      pb[rb] = u32x4{x0, x1, y0, y1};
-    }
-    // O^T[d][row] += V^T[d][key] . P^T[key][row]
+      for (int i = 0; i < 4; ++i) {
+        s[gg][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[gg][i], c_log2, -m_g[2 * hf + gg]));
+        mx = max(mx, __float_as_uint(s[gg][i]));
+      }
+    return __ballot(mx > 0x43800000u) != 0;  // 256.0f
+  };
+  // Rare path: recompute the half's scores, raise the running max to the
+  // row max, rescale the half's O and row sums, and redo the exponentials.
+  auto rescale_half = [&](const u32x4 (&kr)[NKS], f32x4 (&s)[2], int hf, int t, bool mt) INLINE {
+    qk_half(kr, hf, s);
+    if (mt) mask_half(s, hf, t);
+    float m0 = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+    float m1 = fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3]));
+    swap32(m0, m1);  // lane rows (R0, R2) and (R1, R3) of each group
+    float a = fmaxf(m0, m1), bb = a;
+    swap16(a, bb);
+    float g0 = fmaxf(a, bb), g1 = g0;  // [group 2h, 2h, 2h+1, 2h+1] by lane row
+    swap32(g0, g1);                    // g0: group 2h in every lane row, g1: group 2h+1
+    const float n0 = fmaxf(m_g[2 * hf], g0 * c_log2);
+    const float n1 = fmaxf(m_g[2 * hf + 1], g1 * c_log2);
+    const float al0 = __builtin_amdgcn_exp2f(m_g[2 * hf] - n0);
+    const float al1 = __builtin_amdgcn_exp2f(m_g[2 * hf + 1] - n1);
+    m_g[2 * hf] = n0;
+    m_g[2 * hf + 1] = n1;
+    l_g[2 * hf] *= al0;
+    l_g[2 * hf + 1] *= al1;
+    const float ab = (lr & 1) ? al1 : al0;  // block layout: lane rows 1, 3 hold group 2h+1
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) o[db][rb] = mfma_pv(vr[db], pb[rb], o[db][rb]);
+      for (int i = 0; i < 16; ++i) o[db][hf][i] *= ab;
+    exp_half(s, hf);
+  };
+  // P rounded to fp16, row sums of the rounded P, and PV of the half:
+  // groups 2h, 2h+1 -> B operand of row block h (keys 8(l>>5) .. +7 of row
+  // 32h + (l&31)) with one lane-row swap per register pair.
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  auto pv_half = [&](const f32x4 (&s)[2], int hf, const u32x4 (&vr)[NDB]) INLINE {
+    uint32_t pk[2][2];
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      pk[gg][0] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{s[gg][0], s[gg][1]}, h2));
+      pk[gg][1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{s[gg][2], s[gg][3]}, h2));
+      l_g[2 * hf + gg] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk[gg][0]), h2{1, 1},
+                                                l_g[2 * hf + gg], false);
+      l_g[2 * hf + gg] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk[gg][1]), h2{1, 1},
+                                                l_g[2 * hf + gg], false);
+    }
+    uint32_t x0 = pk[0][0], y0 = pk[1][0], x1 = pk[0][1], y1 = pk[1][1];
+    swap16(x0, y0);
+    swap16(x1, y1);
+    const u32x4 pb = u32x4{x0, x1, y0, y1};
+    // O^T[d][row] += V^T[d][key] . P^T[key][row]
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db][hf] = mfma_pv(vr[db], pb, o[db][hf]);
   };
 
   // Pipeline over positions p: two register sets alternate (A: even p, B:
@@ -487,10 +504,13 @@ void attn_kernel(AttnParams P) {
   // has consumed the set, the V operands once PV has.  Loads are issued
   // unconditionally (past the end they repeat the last tile), so every path
   // through the loop has the same loads in flight and the waits stay exact.
-  // The tile number of p+3 is looked up one step before its loads.  The loop
-  // runs whole (A, B) pairs and an odd last position runs after it, so the
-  // loop has no exit between the two halves.
+  // The tile number of p+3 is looked up one step before its loads.  Tiles
+  // that need no mask and boundary tiles run as two separate loops (the mask
+  // is a compile-time switch, so no branch splits a step's instruction
+  // stream); each loop runs whole (A, B) pairs, with a single step before or
+  // after it when its range starts or ends on the other set.
   const int total = seq.total;
+  const int mpos = min(seq.mpos, total);
   u32x4 kA[NKS], vA[NDB], kB[NKS], vB[NDB];
   int tA = seq.tile(0), tB = seq.tile(1);
   load_k(tA, kA);
@@ -498,26 +518,42 @@ void attn_kernel(AttnParams P) {
   load_k(tB, kB);
   load_v(tB, vB);
   int tn = seq.tile(2);
-  auto step = [&](u32x4 (&kr)[NKS], u32x4 (&vr)[NDB], int& tcur, int p) {
-    f32x4 s[4];
-    qk(kr, s);
-    load_k(tn, kr);
+  // one step: QK of both halves; half 0's softmax under half 1's QK, half
+  // 1's softmax under half 0's PV; K is reloaded once the rare path can no
+  // longer need it
+  auto step = [&](auto masked, u32x4 (&kr)[NKS], u32x4 (&vr)[NDB], int& tcur, int p) INLINE {
+    constexpr bool MT = decltype(masked)::value;
     const int tnn = seq.tile(p + 3);
-    softmax_pv(s, vr, tcur, seq.masked(p));
+    f32x4 sa[2], sb[2];
+    qk_half(kr, 0, sa);
+    qk_half(kr, 1, sb);
+    if constexpr (MT) mask_half(sa, 0, tcur);
+    if (exp_half(sa, 0)) rescale_half(kr, sa, 0, tcur, MT);
+    pv_half(sa, 0, vr);
+    if constexpr (MT) mask_half(sb, 1, tcur);
+    if (exp_half(sb, 1)) rescale_half(kr, sb, 1, tcur, MT);
+    load_k(tn, kr);
+    pv_half(sb, 1, vr);
     load_v(tn, vr);
     tcur = tn;
     tn = tnn;
   };
-  int p = 0;
-  for (; p + 1 < total; p += 2) {
-    step(kA, vA, tA, p);
-    step(kB, vB, tB, p + 1);
-  }
-  if (p < total) step(kA, vA, tA, p);
+  auto run = [&](auto masked, int p0, int p1) INLINE {
+    int p = p0;
+    if ((p & 1) && p < p1) step(masked, kB, vB, tB, p++);
+    for (; p + 1 < p1; p += 2) {
+      step(masked, kA, vA, tA, p);
+      step(masked, kB, vB, tB, p + 1);
+    }
+    if (p < p1) step(masked, kA, vA, tA, p);
+  };
+  run(std::integral_constant<bool, false>(), 0, mpos);
+  run(std::integral_constant<bool, true>(), mpos, total);
 
   // ---- merge the four chunk partials of each row; wave 0 writes the rows
   float m_b[2], l_b[2];
-  lanes_to_blocks(m_u, m_b);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) m_b[rb] = (lr & 1) ? m_g[2 * rb + 1] : m_g[2 * rb];
   lanes_to_blocks(reduce_rows(l_g[0], l_g[1], l_g[2], l_g[3], RowSum()), l_b);
   if (w > 0) {
     float* slot = lds + (w - 1) * S::SLOT;
