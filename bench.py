@@ -233,7 +233,7 @@ def main():
                                 s_sparse, idx, cnt, ws_est)
 
     def launch_stage():
-        _abi.stage_v(v, ws_att)
+        _abi.stage_kv(k, v, ws_att)
 
     def launch_attn():
         _abi.layer_attention(q, k, v, out, plan.heads, idx=idx if n_slots else None,
@@ -303,7 +303,7 @@ def main():
         "ms_per_layer": round(ms_step, 4),
         "pct_mfma_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
         "algorithmic_flop": flop,
-        "kernels_ms": {"estimator": round(t_est, 4), "stage_v": round(t_stage, 4),
+        "kernels_ms": {"estimator": round(t_est, 4), "stage_kv": round(t_stage, 4),
                        "attention": round(t_attn, 4)},
         "estimator_gbps": round(est_bytes / (t_est * 1e-3) / 1e9, 1) if n_slots else None,
         "roofline": {

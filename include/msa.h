@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MSA_ABI_VERSION 1
+#define MSA_ABI_VERSION 2
 
 /* status codes (negative: validation, nothing launched) */
 #define MSA_OK 0
@@ -113,7 +113,8 @@ int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k,
                        void* workspace, size_t workspace_bytes,
                        msa_stream_t stream);
 
-/* Bytes of workspace msa_layer_attention needs (V^T staged as fp16). */
+/* Bytes of workspace msa_layer_attention needs: K and V staged once per
+ * layer in MFMA operand order (V as fp16). */
 size_t msa_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t s_k,
                                      int32_t head_dim);
 
@@ -136,15 +137,17 @@ int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k,
                         msa_stream_t stream);
 
 /* The two launches msa_layer_attention makes, callable separately (so a
- * caller can time the attention kernel alone, or reuse one staged V^T):
- *   msa_stage_v: V [B][H_kv][S_k][D] -> fp16 V^T in the workspace
- *                (msa_attention_workspace_bytes bytes);
+ * caller can time the attention kernel alone, or reuse one staging):
+ *   msa_stage_kv: K and V [B][H_kv][S_k][D] -> MFMA operand order in the
+ *                workspace (msa_attention_workspace_bytes bytes); k and v
+ *                have the same shape and dtype;
  *   msa_layer_attention_staged: same arguments and checks as
- *                msa_layer_attention, reads V^T staged by msa_stage_v from
- *                the same workspace on the same stream (v gives shapes only).
+ *                msa_layer_attention, reads K and V staged by msa_stage_kv
+ *                from the same workspace on the same stream (k and v give
+ *                shapes only).
  * Same reference counterpart as msa_layer_attention. */
-int msa_stage_v(const msa_tensor4* v, void* workspace, size_t workspace_bytes,
-                msa_stream_t stream);
+int msa_stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
+                 size_t workspace_bytes, msa_stream_t stream);
 int msa_layer_attention_staged(const msa_tensor4* q, const msa_tensor4* k,
                                const msa_tensor4* v, const msa_tensor4* o,
                                const msa_head_desc* heads, int32_t n_heads,

@@ -153,18 +153,28 @@ int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t
 size_t msa_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t s_k,
                                      int32_t head_dim) {
   if (batch <= 0 || kv_heads <= 0 || s_k <= 0 || head_dim <= 0) return 0;
-  const int64_t bytes = batch * kv_heads * head_dim * cdiv(s_k, MSA_BLOCK) * MSA_BLOCK * 2;
+  // staged V operands (fp16), then staged K operands (input dtype)
+  const int64_t bytes = 2 * batch * kv_heads * head_dim * cdiv(s_k, MSA_BLOCK) * MSA_BLOCK * 2;
   return size_t((bytes + 255) / 256 * 256);
 }
 
-static int stage_v(const msa_tensor4* v, void* workspace, size_t workspace_bytes,
-                   hipStream_t hs) {
-  if (!v || !v->data) return MSA_E_NULL;
-  for (int i = 0; i < 4; ++i)
+// K and V halves of the attention workspace
+static uint16_t* staged_v(void* workspace) { return static_cast<uint16_t*>(workspace); }
+static uint16_t* staged_k(void* workspace, int64_t B, int64_t Hkv, int64_t Sk, int D) {
+  return staged_v(workspace) + B * Hkv * D * cdiv(Sk, MSA_BLOCK) * MSA_BLOCK;
+}
+
+static int stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
+                    size_t workspace_bytes, hipStream_t hs) {
+  if (!k || !v || !k->data || !v->data) return MSA_E_NULL;
+  for (int i = 0; i < 4; ++i) {
     if (v->size[i] <= 0) return MSA_E_RANK;
+    if (k->size[i] != v->size[i]) return MSA_E_RANK;
+  }
   if (v->dtype != MSA_DTYPE_BF16 && v->dtype != MSA_DTYPE_FP16) return MSA_E_DTYPE;
+  if (k->dtype != v->dtype) return MSA_E_DTYPE;
   if (!head_dim_ok(v->size[3])) return MSA_E_HEAD_DIM;
-  if (!aligned(v)) return MSA_E_ALIGN;
+  if (!aligned(v) || !aligned(k)) return MSA_E_ALIGN;
   if (v->size[2] > kMaxSeq) return MSA_E_SEQ;
   const int64_t B = v->size[0], Hkv = v->size[1], Sk = v->size[2];
   const int D = int(v->size[3]);
@@ -172,21 +182,24 @@ static int stage_v(const msa_tensor4* v, void* workspace, size_t workspace_bytes
   const size_t need = msa_attention_workspace_bytes(B, Hkv, Sk, D);
   if (!workspace || workspace_bytes < need) return MSA_E_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
-  VtParams vp;
-  vp.v = v->data;
-  vp.v_sb = v->stride[0]; vp.v_sh = v->stride[1]; vp.v_ss = v->stride[2];
-  vp.vt = static_cast<uint16_t*>(workspace);
-  vp.batch = int(B);
-  vp.kv_heads = int(Hkv);
-  vp.s_k = int(Sk);
-  vp.s_pad = int(cdiv(Sk, MSA_BLOCK) * MSA_BLOCK);
-  const hipError_t e = launch_vt(vp, v->dtype, D, hs);
+  StageParams sp;
+  sp.k = k->data;
+  sp.v = v->data;
+  sp.k_sb = k->stride[0]; sp.k_sh = k->stride[1]; sp.k_ss = k->stride[2];
+  sp.v_sb = v->stride[0]; sp.v_sh = v->stride[1]; sp.v_ss = v->stride[2];
+  sp.vt = staged_v(workspace);
+  sp.kt = staged_k(workspace, B, Hkv, Sk, D);
+  sp.batch = int(B);
+  sp.kv_heads = int(Hkv);
+  sp.s_k = int(Sk);
+  sp.s_pad = int(cdiv(Sk, MSA_BLOCK) * MSA_BLOCK);
+  const hipError_t e = launch_stage(sp, v->dtype, D, hs);
   return e == hipSuccess ? MSA_OK : int(e);
 }
 
-int msa_stage_v(const msa_tensor4* v, void* workspace, size_t workspace_bytes,
-                msa_stream_t stream) {
-  return stage_v(v, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+int msa_stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
+                 size_t workspace_bytes, msa_stream_t stream) {
+  return stage_kv(k, v, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
@@ -230,9 +243,8 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   if (B * Hkv > 65535) return MSA_E_HEADS;
 
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
-  uint16_t* vt = static_cast<uint16_t*>(workspace);
   if (stage) {
-    st = stage_v(v, workspace, workspace_bytes, hs);
+    st = stage_kv(k, v, workspace, workspace_bytes, hs);
     if (st != MSA_OK) return st;
   }
 
@@ -240,7 +252,8 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   memset(&ap, 0, sizeof(ap));
   ap.q = q->data;
   ap.k = k->data;
-  ap.vt = vt;
+  ap.vt = staged_v(workspace);
+  ap.kt = staged_k(workspace, B, Hkv, Sk, D);
   ap.o = o->data;
   ap.q_sb = q->stride[0]; ap.q_sh = q->stride[1]; ap.q_ss = q->stride[2];
   ap.k_sb = k->stride[0]; ap.k_sh = k->stride[1]; ap.k_ss = k->stride[2];

@@ -17,17 +17,17 @@
 //   tile, with a private online-softmax state; the four chunk partials of a
 //   row merge once at the end.  The main loop touches no LDS and has no
 //   barrier: K and V operands go from L2 straight into registers.
-//   S^T = K.Q^T on v_mfma_f32_16x16x32_{bf16,f16}: A = K chunk (native
-//   [S][D] rows), B = Q (registers for the whole item), one 16-row group per
-//   accumulator.  One v_permlane16_swap per register pair turns two 16-row
-//   accumulators (rounded to fp16) into the B operand of
-//   O^T = V^T.P^T on v_mfma_f32_32x32x16_f16, whose A operand comes from V
-//   staged once per layer as fp16 in exact operand order (one 1 KB load per
-//   32 dims).
-//   The running max moves only when a row max grows by more than 2^8, so the
-//   O rescale is rare.  Row maxima and sums reduce over the four lanes of a
-//   row with two permlane swaps; the 64 row values of a wave then sit one
-//   per lane.
+//   S^T = K.Q^T on v_mfma_f32_16x16x32_{bf16,f16}: A = K chunk, B = Q
+//   (registers for the whole item), one 16-row group per accumulator.  One
+//   v_permlane16_swap per register pair turns two 16-row accumulators
+//   (rounded to fp16) into the B operand of O^T = V^T.P^T on
+//   v_mfma_f32_32x32x16_f16.  K and V are staged once per layer in exact
+//   operand order (V as fp16), so every operand is one contiguous 1 KB load.
+//   The exponentials are taken with each row's running max straight off
+//   QK; only when some P exceeds 2^8 (the row max grew by more than 8 in
+//   log2 units) does a rare path recompute the half's scores, reduce the row
+//   maxima over the four lanes of each row with permlane swaps and rescale
+//   O.  Row sums accumulate per lane and reduce once at the end.
 //   Tiles that need no mask run first; boundary tiles (diagonal, band start,
 //   partial sink, S_k end) run last with the elementwise mask.
 
@@ -45,14 +45,18 @@ constexpr int KIND_STREAM = 1;
 constexpr int KIND_BLOCK = 2;
 
 // ---------------------------------------------------------------------------
-// V [B][Hkv][S][D] (bf16/fp16) -> fp16 PV operands, zero padded to
-// s_pad = 64 * n_kb keys:
-//   Vop[B*Hkv][chunk = key/16][D/32][lane 0..63][8]
-//   lane l of 32-dim block db holds V[16 chunk + 8 (l >> 5) + e][32 db + (l & 31)], e = 0..7
-// so a wave reads the A operand of one 32x32x16 MFMA as one contiguous 1 KB.
+// Per-layer staging of K and V into MFMA operand order, zero padded to
+// s_pad = 64 * n_kb keys (chunk = 16 keys; 32-dim k-steps ks / blocks db):
+//   Kop[B*Hkv][chunk][ks][lane 0..63][8], input dtype: lane l holds
+//     K[16 chunk + (l & 15)][32 ks + 8 (l >> 4) + e]      (QK A operand, 16x16x32)
+//   Vop[B*Hkv][chunk][db][lane 0..63][8], fp16: lane l holds
+//     V[16 chunk + 8 (l >> 5) + e][32 db + (l & 31)]     (PV A operand, 32x32x16)
+// so a wave reads every operand as one contiguous 1 KB.  blockIdx.z = 1
+// stages K (a permutation of 16-byte granules), 0 stages V (a transpose
+// through LDS, converted to fp16 with saturation).
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ __launch_bounds__(256) void vt_kernel(VtParams P) {
+__global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
   constexpr int KCH = D / 8;
   constexpr int NDB = D / 32;
   constexpr int LP = D + 8;  // padded LDS row (halves)
@@ -60,6 +64,21 @@ __global__ __launch_bounds__(256) void vt_kernel(VtParams P) {
   const int j0 = blockIdx.x * kBlock;
   const int bk = blockIdx.y;  // b * kv_heads + kvh
   const int b = bk / P.kv_heads, kvh = bk - b * P.kv_heads;
+  // the tile's 4 chunks are 64*D consecutive halves starting at key j0
+  const int64_t dst0 = (int64_t(bk) * P.s_pad + j0) * D;
+  if (blockIdx.z == 1) {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + kvh * P.k_sh;
+    for (int gi = threadIdx.x; gi < 4 * NDB * 64; gi += 256) {
+      const int l = gi & 63;
+      const int cks = gi >> 6;  // chunk * NDB + ks
+      const int c = cks / NDB, ks = cks - c * NDB;
+      const int j = j0 + 16 * c + (l & 15);
+      const u32x4 x = j < P.s_k ? load16(src + int64_t(j) * P.k_ss + 32 * ks + 8 * (l >> 4))
+                                : zero_u32x4();
+      store16(P.kt + dst0 + gi * 8, x);
+    }
+    return;
+  }
   const uint16_t* src = reinterpret_cast<const uint16_t*>(P.v) + b * P.v_sb + kvh * P.v_sh;
   for (int ci = threadIdx.x; ci < kBlock * KCH; ci += 256) {
     const int r = ci / KCH, c = ci - r * KCH;
@@ -78,8 +97,6 @@ __global__ __launch_bounds__(256) void vt_kernel(VtParams P) {
     store16(&tile[r * LP + c * 8], out);
   }
   __syncthreads();
-  // the tile's 4 chunks are 64*D consecutive halves starting at key j0
-  uint16_t* dst = P.vt + (int64_t(bk) * P.s_pad + j0) * D;
   for (int ci = threadIdx.x; ci < 4 * NDB * 64; ci += 256) {
     const int l = ci & 63;
     const int cd = ci >> 6;  // chunk * NDB + db
@@ -93,26 +110,26 @@ __global__ __launch_bounds__(256) void vt_kernel(VtParams P) {
       const uint16_t hi = tile[(key0 + 2 * e + 1) * LP + d];
       out[e] = uint32_t(lo) | (uint32_t(hi) << 16);
     }
-    store16(dst + ci * 8, out);
+    store16(P.vt + dst0 + ci * 8, out);
   }
 }
 
 template <typename T, int D>
-static hipError_t launch_vt_t(const VtParams& p, hipStream_t st) {
-  dim3 grid(p.s_pad / kBlock, p.batch * p.kv_heads);
-  hipLaunchKernelGGL((vt_kernel<T, D>), grid, dim3(256), 0, st, p);
+static hipError_t launch_stage_t(const StageParams& p, hipStream_t st) {
+  dim3 grid(p.s_pad / kBlock, p.batch * p.kv_heads, 2);
+  hipLaunchKernelGGL((stage_kernel<T, D>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
-hipError_t launch_vt(const VtParams& p, int dtype, int D, hipStream_t st) {
+hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st) {
   if (dtype == Bf16::id) {
-    if (D == 64) return launch_vt_t<Bf16, 64>(p, st);
-    if (D == 96) return launch_vt_t<Bf16, 96>(p, st);
-    return launch_vt_t<Bf16, 128>(p, st);
+    if (D == 64) return launch_stage_t<Bf16, 64>(p, st);
+    if (D == 96) return launch_stage_t<Bf16, 96>(p, st);
+    return launch_stage_t<Bf16, 128>(p, st);
   }
-  if (D == 64) return launch_vt_t<F16, 64>(p, st);
-  if (D == 96) return launch_vt_t<F16, 96>(p, st);
-  return launch_vt_t<F16, 128>(p, st);
+  if (D == 64) return launch_stage_t<F16, 64>(p, st);
+  if (D == 96) return launch_stage_t<F16, 96>(p, st);
+  return launch_stage_t<F16, 128>(p, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -166,9 +183,6 @@ __device__ inline void swap32(float& x, float& y) {
 // per group).  A reduced row value lives one per lane in the "lane layout":
 // lane l holds row 16 * rho(l >> 4) + (l & 15), rho = (0, 2, 1, 3).  The PV
 // accumulator of row block rb holds row 32 rb + (l & 31) ("block layout").
-struct RowMax {
-  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
-};
 struct RowSum {
   __device__ float operator()(float a, float b) const { return a + b; }
 };
@@ -181,19 +195,6 @@ __device__ inline float reduce_rows(float v0, float v1, float v2, float v3, Op o
   float a = op(v0, v1), b = op(v2, v3);
   swap16(a, b);
   return op(a, b);
-}
-
-// lane layout -> group layout (each group's value in all 4 lane rows)
-__device__ inline void lanes_to_groups(float u, float (&g)[4]) {
-  float x = u, y = u;
-  swap16(x, y);  // x = [g0, g0, g1, g1], y = [g2, g2, g3, g3]
-  float x2 = x, y2 = y;
-  swap32(x, x2);
-  swap32(y, y2);
-  g[0] = x;
-  g[1] = x2;
-  g[2] = y;
-  g[3] = y2;
 }
 
 // lane layout -> block layout of row blocks 0 and 1
@@ -217,6 +218,7 @@ struct TileSeq {
   int mpos;
   int n_kb;
   const int32_t* list;
+  const int32_t* any;  // any readable int32 (the query tensor)
 
   __device__ void set(const int (&lo)[5], const int (&hi)[5], int nfull) {
     int c = 0;
@@ -240,7 +242,10 @@ struct TileSeq {
     i = q < c3 ? lo2 + (q - c2) : i;
     i = q < c2 ? lo1 + (q - c1) : i;
     i = q < c1 ? lo0 + q : i;
-    const int t = list ? list[i] : i;
+    // the load is unconditional (element 0 of `any` when there is no list)
+    // so that no branch splits the caller's instruction stream
+    const int32_t v = (list ? list : any)[list ? i : 0];
+    const int t = list ? v : i;
     return min(max(t, 0), n_kb - 1);
   }
   __device__ bool masked(int q) const { return q >= mpos; }
@@ -319,6 +324,7 @@ void attn_kernel(AttnParams P) {
   TileSeq seq;
   seq.n_kb = P.n_kb;
   seq.list = nullptr;
+  seq.any = reinterpret_cast<const int32_t*>(P.q);
   if (kind == KIND_BLOCK) {
     // canonical list: ascending causal ids, so the boundary ids come last
     const int64_t base = (int64_t(b) * P.idx_slots + hd.slot) * P.n_qb + bq;
@@ -343,10 +349,9 @@ void attn_kernel(AttnParams P) {
     seq.set({0, Fe, 0, 0, 0}, {Fe, last_tile + 1, 0, 0, 0}, 1);
   }
 
-  const unsigned char* kbytes = reinterpret_cast<const unsigned char*>(P.k) +
-                                2 * (b * P.k_sb + int64_t(kvh) * P.k_sh);
-  const int64_t kss2 = 2 * P.k_ss;
   const int64_t bk = int64_t(b) * (P.heads / P.kv_group) + kvh;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.kt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(P.vt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
 
@@ -366,28 +371,22 @@ void attn_kernel(AttnParams P) {
     }
   }
 
-  // K chunk operand: lane (lc, lr) reads K[j0 + 16w + lc][32ks + 8lr .. +7].
-  // The descriptor is rebased on each tile and bounded so that rows at or
-  // past S_k read as zero.
-  const uint32_t krow_off = uint32_t(16 * w + lc) * uint32_t(kss2) + 16u * lr;
+  // K and V chunk operands of tile t: wave w reads chunk 4t + w of the staged
+  // operands, each MFMA operand as one contiguous 1 KB (lane l: 16 bytes).
+  const uint32_t lane_off = 16u * lane;
   auto load_k = [&](int t, u32x4 (&kr)[NKS]) INLINE {
-    const int j0 = t * kBlock;
-    const int rows = min(kBlock, P.s_k - j0);
-    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<unsigned char*>(kbytes + int64_t(j0) * kss2), short(0), int(rows * kss2),
-        0x00020000);
+    const int soff = (4 * t + w) * S::CHUNK_BYTES;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
       kr[ks] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, krow_off, 64 * ks, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, lane_off, soff + 1024 * ks, 0));
   };
-  const uint32_t vlane_off = 16u * lane;
   auto load_v = [&](int t, u32x4 (&vr)[NDB]) INLINE {
     const int soff = (4 * t + w) * S::CHUNK_BYTES;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
       vr[db] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vlane_off, soff + 1024 * db, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, lane_off, soff + 1024 * db, 0));
   };
 
   f32x16 o[NDB][2];

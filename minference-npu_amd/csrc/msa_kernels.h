@@ -42,7 +42,8 @@ struct HeadArg {
 struct AttnParams {
   const void* q;
   const void* k;
-  const uint16_t* vt;  // [batch*kv_heads][s_pad/16][D/32][64][8] fp16 PV operands (vt_kernel)
+  const uint16_t* kt;  // staged K operands (stage_kernel)
+  const uint16_t* vt;  // staged V operands (stage_kernel)
   void* o;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
@@ -56,10 +57,13 @@ struct AttnParams {
   HeadArg hd[kMaxHeads];
 };
 
-struct VtParams {
+struct StageParams {
+  const void* k;
   const void* v;
+  int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
-  uint16_t* vt;
+  uint16_t* kt;  // [batch*kv_heads][s_pad/16][D/32][64][8] QK A operands (input dtype)
+  uint16_t* vt;  // [batch*kv_heads][s_pad/16][D/32][64][8] PV A operands (fp16)
   int batch, kv_heads, s_k, s_pad;
 };
 
@@ -67,7 +71,7 @@ hipError_t launch_pool(const PoolParams& p, int dtype, int D, hipStream_t st);
 hipError_t launch_score(const ScoreParams& p, int D, hipStream_t st);
 int score_rows_for(int n_kb);
 size_t score_smem_bytes(int R, int D, int n_kb);
-hipError_t launch_vt(const VtParams& p, int dtype, int D, hipStream_t st);
+hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st);
 hipError_t launch_attention(const AttnParams& p, int dtype, int out_dtype, int D,
                             hipStream_t st);
 

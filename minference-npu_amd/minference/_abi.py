@@ -41,7 +41,7 @@ MSA_KIND_BLOCK = 2
 
 MSA_MAX_HEADS = 128
 MSA_BLOCK = 64
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _DTYPE_CODE = {
     torch.bfloat16: MSA_DTYPE_BF16,
@@ -57,7 +57,7 @@ EXPORTED_SYMBOLS = (
     "msa_block_estimate",
     "msa_attention_workspace_bytes",
     "msa_layer_attention",
-    "msa_stage_v",
+    "msa_stage_kv",
     "msa_layer_attention_staged",
 )
 
@@ -145,9 +145,10 @@ def load_library() -> ctypes.CDLL:
                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                 ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
             ]
-        lib.msa_stage_v.restype = ctypes.c_int
-        lib.msa_stage_v.argtypes = [
-            ctypes.POINTER(MsaTensor4), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        lib.msa_stage_kv.restype = ctypes.c_int
+        lib.msa_stage_kv.argtypes = [
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
         ver = lib.msa_abi_version()
         if ver != ABI_VERSION:
@@ -259,11 +260,12 @@ def head_descs(heads: Sequence[tuple]):
     return arr
 
 
-def stage_v(v: torch.Tensor, ws: torch.Tensor) -> None:
-    """Launch msa_stage_v (V -> fp16 V^T in ``ws``) on the current stream."""
-    vd = tensor4(v)
-    check(load_library().msa_stage_v(ctypes.byref(vd), ws.data_ptr(), ws.numel(),
-                                     current_stream_handle(v.device)))
+def stage_kv(k: torch.Tensor, v: torch.Tensor, ws: torch.Tensor) -> None:
+    """Launch msa_stage_kv (K, V -> MFMA operand order in ``ws``) on the
+    current stream."""
+    kd, vd = tensor4(k), tensor4(v)
+    check(load_library().msa_stage_kv(ctypes.byref(kd), ctypes.byref(vd), ws.data_ptr(),
+                                      ws.numel(), current_stream_handle(v.device)))
 
 
 def layer_attention(
@@ -280,14 +282,14 @@ def layer_attention(
     staged: bool = False,
 ) -> None:
     """Launch msa_layer_attention (or, with ``staged=True``,
-    msa_layer_attention_staged reading the V^T already in ``ws``).
+    msa_layer_attention_staged reading the K and V already staged in ``ws``).
     ``heads`` = [(kind, p1, p2, slot, scale)] * H."""
     lib = load_library()
     n = len(heads)
     arr = head_descs(heads)
     need = attention_workspace_bytes(k.shape[0], k.shape[1], k.shape[2], k.shape[3])
     if staged and (ws is None or ws.numel() < need):
-        raise ValueError("staged attention needs the workspace filled by stage_v")
+        raise ValueError("staged attention needs the workspace filled by stage_kv")
     if ws is None or ws.numel() < need:
         ws = workspace(need, q.device)
     qd, kd, vd, od = tensor4(q), tensor4(k), tensor4(v), tensor4(out)

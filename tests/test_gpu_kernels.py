@@ -182,6 +182,37 @@ def test_dense_vs_oracle(gpu_device, s_q, s_k, D, dtype):
     assert_close_f32(out32, ref, what="dense")
 
 
+@pytest.mark.parametrize("factor", [4.0, 12.0, 40.0])
+@pytest.mark.parametrize("kind", ["dense", "stream", "block"])
+def test_late_outlier_keys(gpu_device, kind, factor):
+    """Keys scaled by `factor` in the middle of the sequence make a row's max
+    logit jump after its first tiles: by a few units (no rescale), past the
+    lazy slack (rescale from the tracked maxima) or far enough that P would
+    overflow fp16 (the work item is redone)."""
+    from minference import block_sparse_attention, dense_attention, streaming_forward
+
+    S, H, D = 2048, 2, 96
+    q, k, v = make_qkv(1, H, S, S, D, torch.bfloat16, seed=int(factor))
+    k = k.float()
+    for j in (1500, 1501, 1777):
+        k[:, :, j] *= factor
+    k = k.to(torch.bfloat16)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    qn, kn, vn = np32(q), np32(k), np32(v)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    if kind == "dense":
+        dense_attention(dq, dk, dv, out=out32)
+        ref = O.dense_causal(qn, kn, vn)
+    elif kind == "stream":
+        streaming_forward(dq, dk, dv, 64, 1024, out=out32)
+        ref = O.streaming_attention(qn, kn, vn, 64, 1024)
+    else:
+        block_sparse_attention(dq, dk, dv, 6, out=out32)
+        idx, _ = O.select_block_sparse_topk_indices(qn, kn, 6, "bf16")
+        ref = O.block_sparse_from_indices(qn, kn, vn, idx)
+    assert_close_f32(out32, ref, what=f"{kind} x{factor}")
+
+
 # ---------------------------------------------------------------------------
 # one mixed layer through the dispatcher plan; strided (HF-like) views; GQA
 # ---------------------------------------------------------------------------
