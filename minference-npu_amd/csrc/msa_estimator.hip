@@ -12,6 +12,8 @@
 // correctly rounded value whatever the summation order; the CPU oracle uses
 // the same rule and the two agree bit for bit.  Ties break to the lower id.
 
+#include <type_traits>
+
 #include "msa_common.h"
 #include "msa_kernels.h"
 
@@ -192,19 +194,48 @@ __global__ __launch_bounds__(256) void score_topk_kernel(ScoreParams P) {
   }
   __syncthreads();
 
+  // Each thread scores NC columns (stride 256) at once, NC chosen from the
+  // candidate count: the pooled-K loads of a d-chunk are issued together and
+  // every pooled-Q value read from LDS serves all NC columns.  Per (row,
+  // column) the fp64 FMAs run in d order.
   const float* kT = P.k_poolT + int64_t(sb) * D * P.n_kb;
-  for (int c = t; c < ncand; c += 256) {
-    double acc[R];
+  auto score = [&](auto nc) {
+    constexpr int NC = decltype(nc)::value, DC = 8;
+    for (int cb = 0; cb < ncand; cb += 256 * NC) {
+      double acc[NC][R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0;
-    for (int d = 0; d < D; ++d) {
-      const double kv = double(kT[int64_t(d) * P.n_kb + c]);
+      for (int j = 0; j < NC; ++j)
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = fma(qp[r * D + d], kv, acc[r]);
+        for (int r = 0; r < R; ++r) acc[j][r] = 0.0;
+      for (int d0 = 0; d0 < D; d0 += DC) {
+        float kv[NC][DC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          const int c = min(cb + t + 256 * j, ncand - 1);
+#pragma unroll
+          for (int u = 0; u < DC; ++u) kv[j][u] = kT[int64_t(d0 + u) * P.n_kb + c];
+        }
+#pragma unroll
+        for (int u = 0; u < DC; ++u)
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const double qv = qp[r * D + d0 + u];
+#pragma unroll
+            for (int j = 0; j < NC; ++j) acc[j][r] = fma(qv, double(kv[j][u]), acc[j][r]);
+          }
+      }
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int c = cb + t + 256 * j;
+        if (c < ncand)
+#pragma unroll
+          for (int r = 0; r < R; ++r) sc[r * ncand + c] = float(acc[j][r]) * P.scale;
+      }
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r) sc[r * ncand + c] = float(acc[r]) * P.scale;
-  }
+  };
+  if (ncand > 512) score(std::integral_constant<int, 4>());
+  else if (ncand > 256) score(std::integral_constant<int, 2>());
+  else score(std::integral_constant<int, 1>());
   __syncthreads();
 
   const int topk = P.slot_topk[sb % P.n_slots];
