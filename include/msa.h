@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MSA_ABI_VERSION 2
+#define MSA_ABI_VERSION 3
 
 /* status codes (negative: validation, nothing launched) */
 #define MSA_OK 0
@@ -154,6 +154,20 @@ int msa_layer_attention_staged(const msa_tensor4* q, const msa_tensor4* k,
                                const int32_t* idx, const int32_t* cnt,
                                int32_t idx_slots, int32_t topk_max, void* workspace,
                                size_t workspace_bytes, msa_stream_t stream);
+
+
+/* Decode: one query row per head (q [B][H][1][D]) against the whole cache
+ * (k, v [B][H_kv][S_k][D], any strides with D contiguous and 16-byte rows),
+ * every key visible.  Replaces decode_dense,
+ * minference/backend_npu/attention.py:274-314, which the patched forward
+ * calls for q_len == 1 (minference/modules/minference_forward.py:488-490).
+ * scale is the softmax scale (the reference default is 1/sqrt(D)).  o may be
+ * q's dtype or fp32.  Two launches (split-K partials, then their merge); the
+ * workspace holds the partials (msa_decode_workspace_bytes). */
+size_t msa_decode_workspace_bytes(int64_t batch, int64_t heads, int64_t s_k, int32_t head_dim);
+int msa_decode_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
+                         const msa_tensor4* o, float scale, void* workspace,
+                         size_t workspace_bytes, msa_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -2,6 +2,8 @@
 // Nothing here allocates device memory or synchronises the stream.
 
 #include <math.h>
+
+#include <algorithm>
 #include <string.h>
 
 #include "../../include/msa.h"
@@ -345,6 +347,73 @@ int msa_layer_attention_staged(const msa_tensor4* q, const msa_tensor4* k, const
                                msa_stream_t stream) {
   return layer_attention_impl(q, k, v, o, heads, n_heads, idx, cnt, idx_slots, topk_max,
                               workspace, workspace_bytes, stream, false);
+}
+
+
+// ---------------------------------------------------------------------------
+// decode
+// ---------------------------------------------------------------------------
+// Key splits of one decode call: about 2048 workgroups in all, at least 64
+// keys each.
+static void decode_split(int64_t bh, int64_t s_k, int& n_split, int& chunk) {
+  int64_t ns = (2048 + bh - 1) / bh;
+  ns = std::max<int64_t>(1, std::min<int64_t>(ns, cdiv(s_k, 64)));
+  int64_t ch = cdiv(s_k, ns);
+  ch = cdiv(ch, 64) * 64;
+  n_split = int(cdiv(s_k, ch));
+  chunk = int(ch);
+}
+
+size_t msa_decode_workspace_bytes(int64_t batch, int64_t heads, int64_t s_k, int32_t head_dim) {
+  if (batch <= 0 || heads <= 0 || s_k <= 0 || head_dim <= 0) return 0;
+  int ns, ch;
+  decode_split(batch * heads, s_k, ns, ch);
+  const int64_t bytes = batch * heads * ns * (int64_t(head_dim) + 2) * 4;
+  return size_t((bytes + 255) / 256 * 256);
+}
+
+int msa_decode_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
+                         const msa_tensor4* o, float scale, void* workspace,
+                         size_t workspace_bytes, msa_stream_t stream) {
+  int st = check_qk(q, k);
+  if (st != MSA_OK) return st;
+  if (!v || !o || !v->data || !o->data) return MSA_E_NULL;
+  for (int i = 0; i < 4; ++i) {
+    if (v->size[i] != k->size[i]) return MSA_E_RANK;
+    if (o->size[i] != q->size[i]) return MSA_E_RANK;
+  }
+  if (q->size[2] != 1) return MSA_E_SEQ;
+  if (v->dtype != q->dtype) return MSA_E_DTYPE;
+  if (o->dtype != q->dtype && o->dtype != MSA_DTYPE_FP32) return MSA_E_DTYPE;
+  if (!aligned(v) || !aligned(o)) return MSA_E_ALIGN;
+  if (!(scale > 0.0f) || !isfinite(scale)) return MSA_E_HEADS;
+  const int64_t B = q->size[0], H = q->size[1], Hkv = k->size[1], Sk = k->size[2];
+  const int D = int(q->size[3]);
+  // buffer descriptors cover one head's cache: < 2 GiB of rows
+  if ((Sk + 64) * k->stride[2] * 2 >= (int64_t(1) << 31) ||
+      (Sk + 64) * v->stride[2] * 2 >= (int64_t(1) << 31))
+    return MSA_E_SEQ;
+  if (B * H > 65535) return MSA_E_HEADS;
+  const size_t need = msa_decode_workspace_bytes(B, H, Sk, D);
+  if (!workspace || workspace_bytes < need) return MSA_E_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
+
+  DecodeParams dp;
+  memset(&dp, 0, sizeof(dp));
+  dp.q = q->data; dp.k = k->data; dp.v = v->data; dp.o = o->data;
+  dp.q_sb = q->stride[0]; dp.q_sh = q->stride[1];
+  dp.k_sb = k->stride[0]; dp.k_sh = k->stride[1]; dp.k_ss = k->stride[2];
+  dp.v_sb = v->stride[0]; dp.v_sh = v->stride[1]; dp.v_ss = v->stride[2];
+  dp.o_sb = o->stride[0]; dp.o_sh = o->stride[1];
+  dp.batch = int(B);
+  dp.heads = int(H);
+  dp.kv_group = int(H / Hkv);
+  dp.s_k = int(Sk);
+  decode_split(B * H, Sk, dp.n_split, dp.chunk);
+  dp.scale_log2 = float(double(scale) * 1.4426950408889634);
+  dp.part = static_cast<float*>(workspace);
+  const hipError_t e = launch_decode(dp, q->dtype, o->dtype, D, reinterpret_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSA_OK : int(e);
 }
 
 }  // extern "C"

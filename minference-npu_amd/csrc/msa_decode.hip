@@ -1,0 +1,262 @@
+// Decode attention: one query row per head against the whole KV cache.
+//
+// Reference semantics: decode_dense, MInference-NPU/minference/backend_npu/attention.py:274-314
+// (q [B,H,1,D], k/v cache [B,H_kv,S,D], scale default 1/sqrt(D), every key
+// visible), dispatched for q_len == 1 by
+// MInference-NPU/minference/modules/minference_forward.py:488-490.
+//
+// The work is a GEMV pair per head and is bound by HBM (K and V are read
+// once, 4*D bytes per key); MFMA would waste 15 of 16 rows, so it runs on
+// the VALU in fp32.
+//
+// Split-K: the grid is (n_split, B*H); workgroup (s, b*H+h) walks keys
+// [s*chunk, min((s+1)*chunk, S)) of head h in 16-key blocks, wave w taking
+// blocks w, w+4, ...  A block of K is 16 rows of D elements; with rows
+// contiguous it is 16*D*2 bytes read as D/32 one-kilobyte loads per wave
+// (lane l, load i: elements f = 8l + 512i .. +7 of the block, always inside
+// row f / D).  Each lane forms the partial dot products of its 8-element
+// pieces, the 16 key dot products reduce through wave-private LDS, the
+// online softmax runs on 16 lanes, and P is read back per piece for the PV
+// update of the same pieces of V.  Rows with another stride use the same
+// pieces, addressed row by row.
+//
+// Each workgroup leaves (m, l, O[D]) for its key range in the workspace; the
+// combine kernel merges the splits of a head and writes the output row.
+
+#include "msa_common.h"
+#include "msa_kernels.h"
+
+namespace msa {
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void decode_kernel(DecodeParams P) {
+  constexpr int NL = D / 32;   // 1 KB loads per 16-key block of K (and of V)
+  constexpr int NPC = D / 8;   // 8-element pieces per key row
+  __shared__ float part[4][16][NPC + 1];  // per-wave partial dot products
+  __shared__ float pw[4][16];             // per-wave P of the block
+  __shared__ float om[4][64 * NL * 8 + 2];  // merge: per-wave O pieces, m, l
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int split = blockIdx.x;
+  const int bh = blockIdx.y;  // b * heads + h
+  const int b = bh / P.heads;
+  const int h = bh - b * P.heads;
+  const int kvh = h / P.kv_group;
+
+  const int j_begin = split * P.chunk;
+  const int j_end = min(j_begin + P.chunk, P.s_k);
+
+  // this lane's pieces: key row kr_i of the block, first element d0_i
+  int key_i[NL], d0_i[NL];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int f = 8 * lane + 512 * i;
+    key_i[i] = f / D;
+    d0_i[i] = f - key_i[i] * D;
+  }
+  // q pieces in fp32
+  float qv[NL][8];
+  {
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + int64_t(h) * P.q_sh;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const u32x4 x = load16(qrow + d0_i[i]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qv[i][2 * e] = T::to_float(uint16_t(x[e] & 0xffffu));
+        qv[i][2 * e + 1] = T::to_float(uint16_t(x[e] >> 16));
+      }
+    }
+  }
+
+  // Buffer descriptors bounded at row S, so pieces of rows >= S read 0.
+  const unsigned char* kbase = reinterpret_cast<const unsigned char*>(P.k) +
+                               2 * (b * P.k_sb + int64_t(kvh) * P.k_sh);
+  const unsigned char* vbase = reinterpret_cast<const unsigned char*>(P.v) +
+                               2 * (b * P.v_sb + int64_t(kvh) * P.v_sh);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<unsigned char*>(kbase), short(0), int(int64_t(P.s_k) * P.k_ss * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<unsigned char*>(vbase), short(0), int(int64_t(P.s_k) * P.v_ss * 2), 0x00020000);
+  uint32_t koff[NL], voff[NL];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    koff[i] = uint32_t(key_i[i]) * uint32_t(P.k_ss) * 2u + 2u * d0_i[i];
+    voff[i] = uint32_t(key_i[i]) * uint32_t(P.v_ss) * 2u + 2u * d0_i[i];
+  }
+  auto load_block = [&](int j0, u32x4 (&kr)[NL], u32x4 (&vr)[NL]) {
+    const int ks = j0 * int(P.k_ss) * 2, vs = j0 * int(P.v_ss) * 2;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff[i], ks, 0));
+      vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i], vs, 0));
+    }
+  };
+
+  float o[NL][8];
+#pragma unroll
+  for (int i = 0; i < NL; ++i)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) o[i][u] = 0.0f;
+  float m = -__builtin_inff();  // running max (scaled, log2 units), wave-uniform
+  float l = 0.0f;               // running sum (lanes 0..15 hold partial sums)
+  const float c = P.scale_log2;
+
+  const int first = j_begin + 16 * w;
+  u32x4 kc[NL], vc[NL], kn[NL], vn[NL];
+  // loads are unconditional (past the range they repeat the current block;
+  // rows at or past S read 0), so the waits stay exact
+  load_block(first, kc, vc);
+  for (int j0 = first; j0 < j_end; j0 += 64) {
+    const int jn = j0 + 64;
+    load_block(jn < j_end ? jn : j0, kn, vn);
+    // partial dot products of this lane's pieces
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc = __builtin_fmaf(qv[i][2 * e], T::to_float(uint16_t(kc[i][e] & 0xffffu)), acc);
+        acc = __builtin_fmaf(qv[i][2 * e + 1], T::to_float(uint16_t(kc[i][e] >> 16)), acc);
+      }
+      part[w][key_i[i]][d0_i[i] / 8] = acc;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    // lanes 0..15: the block's 16 scores
+    float s = -__builtin_inff();
+    if (lane < 16) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int p = 0; p < NPC; ++p) acc += part[w][lane][p];
+      s = (j0 + lane < j_end) ? acc * c : -__builtin_inff();
+    }
+    float bm = s;
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
+    bm = __shfl(bm, 0, 64);
+    const float mn = fmaxf(m, bm);
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);  // m = -inf at first: exp2(-inf) = 0
+    m = mn;
+    const float p = lane < 16 ? __builtin_amdgcn_exp2f(s - m) : 0.0f;
+    l = l * alpha + p;
+    if (lane < 16) pw[w][lane] = p;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const float pi = pw[w][key_i[i]];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[i][2 * e] = __builtin_fmaf(pi, T::to_float(uint16_t(vc[i][e] & 0xffffu)), o[i][2 * e] * alpha);
+        o[i][2 * e + 1] = __builtin_fmaf(pi, T::to_float(uint16_t(vc[i][e] >> 16)), o[i][2 * e + 1] * alpha);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      kc[i] = kn[i];
+      vc[i] = vn[i];
+    }
+  }
+
+  // ---- merge the 4 waves and the 16 key positions of every piece
+  // wave sum of l over lanes 0..15
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
+  float* mine = om[w];
+#pragma unroll
+  for (int i = 0; i < NL; ++i)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mine[(64 * i + lane) * 8 + u] = o[i][u];
+  if (lane == 0) {
+    mine[64 * NL * 8] = m;
+    mine[64 * NL * 8 + 1] = l;
+  }
+  __syncthreads();
+  // thread t < D: element d = t of O, summing every (wave, piece) whose
+  // piece covers d, each wave scaled by exp2(m_w - M)
+  if (tid < D) {
+    float mw[4], M = -__builtin_inff();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      mw[v] = om[v][64 * NL * 8];
+      M = fmaxf(M, mw[v]);
+    }
+    float L = 0.0f, acc = 0.0f;
+    const int d = tid, dp = d & ~7, du = d & 7;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float f = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mw[v] - M);
+      L += f * om[v][64 * NL * 8 + 1];
+      float sv = 0.0f;
+      for (int r = 0; r < 16; ++r) {  // piece of key row r covering d
+        const int fl = r * D + dp;    // flat element of that piece in the block
+        const int i = fl / 512, ln = (fl - 512 * i) / 8;
+        sv += om[v][(64 * i + ln) * 8 + du];
+      }
+      acc += f * sv;
+    }
+    float* dst = P.part + (int64_t(bh) * P.n_split + split) * (D + 2);
+    dst[d] = acc;
+    if (d == 0) {
+      dst[D] = M;
+      dst[D + 1] = L;
+    }
+  }
+}
+
+// Merge the splits of one head: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+template <typename T, bool OUT_F32, int D>
+__global__ __launch_bounds__(128) void decode_combine_kernel(DecodeParams P) {
+  const int bh = blockIdx.x;
+  const int b = bh / P.heads, h = bh - b * P.heads;
+  const float* src = P.part + int64_t(bh) * P.n_split * (D + 2);
+  const int d = threadIdx.x;
+  float M = -__builtin_inff();
+  for (int s = 0; s < P.n_split; ++s) M = fmaxf(M, src[s * (D + 2) + D]);
+  float L = 0.0f, acc = 0.0f;
+  for (int s = 0; s < P.n_split; ++s) {
+    const float ms = src[s * (D + 2) + D];
+    const float f = ms == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+    L += f * src[s * (D + 2) + D + 1];
+    if (d < D) acc += f * src[s * (D + 2) + d];
+  }
+  if (d < D) {
+    const float r = L > 0.0f ? acc / L : 0.0f;
+    const int64_t off = b * P.o_sb + int64_t(h) * P.o_sh + d;
+    if constexpr (OUT_F32) {
+      reinterpret_cast<float*>(P.o)[off] = r;
+    } else {
+      reinterpret_cast<uint16_t*>(P.o)[off] = T::from_float(r);
+    }
+  }
+}
+
+template <typename T, bool OUT_F32, int D>
+static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t st) {
+  hipLaunchKernelGGL((decode_kernel<T, D>), dim3(p.n_split, p.batch * p.heads), dim3(256), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((decode_combine_kernel<T, OUT_F32, D>), dim3(p.batch * p.heads), dim3(128), 0,
+                     st, p);
+  return hipGetLastError();
+}
+
+template <typename T, bool OUT_F32>
+static hipError_t launch_decode_d(const DecodeParams& p, int D, hipStream_t st) {
+  if (D == 64) return launch_decode_t<T, OUT_F32, 64>(p, st);
+  if (D == 96) return launch_decode_t<T, OUT_F32, 96>(p, st);
+  return launch_decode_t<T, OUT_F32, 128>(p, st);
+}
+
+hipError_t launch_decode(const DecodeParams& p, int dtype, int out_dtype, int D, hipStream_t st) {
+  const bool f32 = out_dtype == 3;
+  if (dtype == Bf16::id)
+    return f32 ? launch_decode_d<Bf16, true>(p, D, st) : launch_decode_d<Bf16, false>(p, D, st);
+  return f32 ? launch_decode_d<F16, true>(p, D, st) : launch_decode_d<F16, false>(p, D, st);
+}
+
+}  // namespace msa

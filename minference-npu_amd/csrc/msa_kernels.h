@@ -67,11 +67,27 @@ struct StageParams {
   int batch, kv_heads, s_k, s_pad;
 };
 
+struct DecodeParams {
+  const void* q;  // [batch][heads][1][D]
+  const void* k;  // [batch][kv_heads][s_k][D]
+  const void* v;
+  void* o;        // [batch][heads][1][D]
+  int64_t q_sb, q_sh;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh;
+  int batch, heads, kv_group, s_k;
+  int n_split, chunk;  // key range of split s: [s*chunk, min((s+1)*chunk, s_k))
+  float scale_log2;    // softmax scale * log2(e)
+  float* part;         // workspace [batch*heads][n_split][D+2]: O, m, l per split
+};
+
 hipError_t launch_pool(const PoolParams& p, int dtype, int D, hipStream_t st);
 hipError_t launch_score(const ScoreParams& p, int D, hipStream_t st);
 int score_rows_for(int n_kb);
 size_t score_smem_bytes(int R, int D, int n_kb);
 hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st);
+hipError_t launch_decode(const DecodeParams& p, int dtype, int out_dtype, int D, hipStream_t st);
 hipError_t launch_attention(const AttnParams& p, int dtype, int out_dtype, int D,
                             hipStream_t st);
 

@@ -41,7 +41,7 @@ MSA_KIND_BLOCK = 2
 
 MSA_MAX_HEADS = 128
 MSA_BLOCK = 64
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _DTYPE_CODE = {
     torch.bfloat16: MSA_DTYPE_BF16,
@@ -59,6 +59,8 @@ EXPORTED_SYMBOLS = (
     "msa_layer_attention",
     "msa_stage_kv",
     "msa_layer_attention_staged",
+    "msa_decode_workspace_bytes",
+    "msa_decode_attention",
 )
 
 
@@ -150,6 +152,16 @@ def load_library() -> ctypes.CDLL:
             ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
+        lib.msa_decode_workspace_bytes.restype = ctypes.c_size_t
+        lib.msa_decode_workspace_bytes.argtypes = [
+            ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+        ]
+        lib.msa_decode_attention.restype = ctypes.c_int
+        lib.msa_decode_attention.argtypes = [
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
         ver = lib.msa_abi_version()
         if ver != ABI_VERSION:
             raise ImportError(f"libmsa ABI version {ver} != expected {ABI_VERSION}")
@@ -209,6 +221,23 @@ def estimate_workspace_bytes(batch: int, n_slots: int, s_q: int, s_k: int, head_
 
 def attention_workspace_bytes(batch: int, kv_heads: int, s_k: int, head_dim: int) -> int:
     return int(load_library().msa_attention_workspace_bytes(batch, kv_heads, s_k, head_dim))
+
+
+def decode_workspace_bytes(batch: int, heads: int, s_k: int, head_dim: int) -> int:
+    return int(load_library().msa_decode_workspace_bytes(batch, heads, s_k, head_dim))
+
+
+def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                     scale: float, ws: Optional[torch.Tensor] = None) -> None:
+    """Launch msa_decode_attention (q [B,H,1,D] against the cache k/v) on the
+    current stream."""
+    need = decode_workspace_bytes(q.shape[0], q.shape[1], k.shape[2], q.shape[3])
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, q.device)
+    qd, kd, vd, od = tensor4(q), tensor4(k), tensor4(v), tensor4(out)
+    check(load_library().msa_decode_attention(
+        ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ctypes.byref(od), float(scale),
+        ws.data_ptr(), ws.numel(), current_stream_handle(q.device)))
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:

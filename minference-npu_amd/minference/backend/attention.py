@@ -1,8 +1,9 @@
-"""Dense causal attention on MI355X.
+"""Dense attention on MI355X.
 
-Drop-in for ``dense_attention`` / ``prefill_dense`` of
-MInference-NPU/minference/backend_npu/attention.py:192-271.  It runs the same
-tile-list kernel as the sparse kinds with every causal tile listed.
+Drop-in for ``dense_attention`` / ``prefill_dense`` / ``decode_dense`` of
+MInference-NPU/minference/backend_npu/attention.py:192-314.  Prefill runs the
+same tile-list kernel as the sparse kinds with every causal tile listed;
+decode (one query row) runs a split-K kernel that reads the cache in place.
 """
 
 from __future__ import annotations
@@ -14,7 +15,7 @@ import torch
 from .. import _abi
 from ..ops.common import check_bnsd, check_supported, dense_scale, head_chunks, kernel_view, make_out
 
-__all__ = ["dense_attention", "prefill_dense"]
+__all__ = ["dense_attention", "prefill_dense", "decode_dense"]
 
 
 def dense_attention(
@@ -30,11 +31,12 @@ def dense_attention(
 
     Query i sees key j iff j <= i + (S_k - S_q).  ``scale`` defaults to
     1/sqrt(D) of the unpadded head_dim (reference :210-211).  Only the causal
-    prefill form is implemented (``causal=False`` belongs to decode, which is
-    outside this build).
+    prefill form is implemented; the non-causal one-row form is
+    ``decode_dense``.
     """
     if not causal:
-        raise NotImplementedError("dense_attention(causal=False) is not part of the MI355X prefill path")
+        raise NotImplementedError("dense_attention(causal=False) is not part of the MI355X prefill "
+                                  "path; use decode_dense for one query row")
     check_bnsd(q, k, v)
     check_supported(q, k, v)
     q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
@@ -49,3 +51,36 @@ def dense_attention(
 def prefill_dense(q, k, v, *, scale: Optional[float] = None, causal: bool = True):
     """Same as dense_attention (reference :258-271)."""
     return dense_attention(q, k, v, scale=scale, causal=causal)
+
+
+def decode_dense(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    *,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """One query row per head against the whole cache (reference :274-314).
+
+    q ``[B, H, 1, D]``; k_cache / v_cache ``[B, H_kv, S_kv, D]`` with
+    ``H % H_kv == 0`` (the reference passes ``H_kv == H``); every key is
+    visible; ``scale`` defaults to 1/sqrt(D).  Returns ``[B, H, 1, D]`` in q's
+    dtype (or writes ``out``, q's dtype or fp32).
+    """
+    assert q.dim() == 4 and k_cache.dim() == 4, "q and the caches must be 4-D [B,H,S,D]"
+    assert v_cache.shape == k_cache.shape, (
+        f"v_cache shape {tuple(v_cache.shape)} != k_cache shape {tuple(k_cache.shape)}")
+    assert q.shape[0] == k_cache.shape[0] and q.shape[-1] == k_cache.shape[-1], (
+        f"q/k_cache B/D mismatch; q={tuple(q.shape)} k={tuple(k_cache.shape)}")
+    if q.shape[1] % k_cache.shape[1] != 0:
+        raise ValueError(f"q heads {q.shape[1]} not a multiple of cache heads {k_cache.shape[1]}")
+    if q.shape[2] != 1:
+        raise NotImplementedError("decode_dense takes one query row; use dense_attention for "
+                                  "q_len > 1")
+    check_supported(q, k_cache, v_cache)
+    q, k_cache, v_cache = kernel_view(q), kernel_view(k_cache), kernel_view(v_cache)
+    result = make_out(q, out)
+    s = dense_scale(q.shape[-1]) if scale is None else float(scale)
+    _abi.decode_attention(q, k_cache, v_cache, result, s)
+    return result

@@ -152,6 +152,15 @@ def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan:
     return out
 
 
+def run_decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                         scale: float) -> torch.Tensor:
+    """Decode launch: q [B, H, 1, D] against the whole cache k/v [B, H_kv, S_k, D]
+    (the reference's decode_dense, backend_npu/attention.py:274-314)."""
+    _abi.require_device(q, k, v)
+    _abi.decode_attention(q, k, v, out, scale)
+    return out
+
+
 def init_minference_parameters(self) -> None:
     """Per-layer one-time setup (reference :175-213): reads starting_layer,
     is_search, config_path and the attn type injected by the patch, and loads
@@ -236,12 +245,14 @@ def minference_forward():
                                device=query.device)
         out = out_bshd.transpose(1, 2)
         if q_len == 1:
-            plan = dense_plan(n_heads, hd)  # decode: one query row sees every key
-        elif self._minference_attn_type == "dense" or self.layer_idx < self.starting_layer:
-            plan = dense_plan(n_heads, hd)
+            # decode: one query row sees the whole cache (reference :488-490)
+            run_decode_attention(query, key, value, out, dense_scale(hd))
         else:
-            plan = _layer_plan(self, n_heads, hd, key.shape[2])
-        run_layer_attention(query, key, value, plan, out)
+            if self._minference_attn_type == "dense" or self.layer_idx < self.starting_layer:
+                plan = dense_plan(n_heads, hd)
+            else:
+                plan = _layer_plan(self, n_heads, hd, key.shape[2])
+            run_layer_attention(query, key, value, plan, out)
 
         attn_output = out_bshd.reshape(bsz, q_len, n_heads * hd)
         attn_output = self.o_proj(attn_output)

@@ -158,6 +158,48 @@ def test_estimator_validation(kw, expected):
     assert est(t4(SHAPE), t4(SHAPE), hl, tl, tm, **args) == expected
 
 
+def dec(q, k, v, o, scale=0.1, ws=FAKE, wsb=1 << 40):
+    lib = _abi.load_library()
+    return lib.msa_decode_attention(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v),
+                                    ctypes.byref(o), scale, ws, wsb, None)
+
+
+QD, KD = [2, 8, 1, 96], [2, 2, 4096, 96]
+
+
+@pytest.mark.parametrize(
+    "mutate,expected",
+    [
+        (lambda a: a.__setitem__("q", t4([2, 8, 2, 96])) or a.__setitem__("o", t4([2, 8, 2, 96])), _abi.MSA_E_SEQ),
+        (lambda a: a.__setitem__("k", t4([2, 3, 4096, 96])) or a.__setitem__("v", t4([2, 3, 4096, 96])), _abi.MSA_E_RANK),
+        (lambda a: a.__setitem__("v", t4([2, 2, 4000, 96])), _abi.MSA_E_RANK),
+        (lambda a: a.__setitem__("o", t4([2, 8, 1, 64])), _abi.MSA_E_RANK),
+        (lambda a: a.__setitem__("v", t4(KD, _abi.MSA_DTYPE_FP16)), _abi.MSA_E_DTYPE),
+        (lambda a: a.__setitem__("o", t4(QD, _abi.MSA_DTYPE_FP16)), _abi.MSA_E_DTYPE),
+        (lambda a: a.__setitem__("k", t4(KD, data=FAKE + 8)), _abi.MSA_E_ALIGN),
+        (lambda a: a.__setitem__("scale", 0.0), _abi.MSA_E_HEADS),
+        (lambda a: a.__setitem__("scale", float("nan")), _abi.MSA_E_HEADS),
+        (lambda a: a.__setitem__("k", t4([1, 1, 1 << 20, 128], strides=[0, 0, 2048, 1]))
+         or a.__setitem__("q", t4([1, 1, 1, 128])) or a.__setitem__("o", t4([1, 1, 1, 128]))
+         or a.__setitem__("v", t4([1, 1, 1 << 20, 128], strides=[0, 0, 2048, 1])), _abi.MSA_E_SEQ),
+        (lambda a: a.__setitem__("wsb", 100), _abi.MSA_E_WORKSPACE),
+        (lambda a: a.__setitem__("v", t4(KD, data=0)), _abi.MSA_E_NULL),
+    ],
+)
+def test_decode_validation(mutate, expected):
+    a = {"q": t4(QD), "k": t4(KD), "v": t4(KD), "o": t4(QD), "scale": 0.1, "wsb": 1 << 40}
+    mutate(a)
+    assert dec(a["q"], a["k"], a["v"], a["o"], a["scale"], wsb=a["wsb"]) == expected
+
+
+def test_decode_workspace_sizes():
+    # about 2048 split workgroups in all, >= 64 keys each; (D + 2) fp32 per split
+    assert _abi.decode_workspace_bytes(1, 32, 65536, 96) == 32 * 64 * 98 * 4
+    assert _abi.decode_workspace_bytes(1, 32, 100, 96) == (32 * 2 * 98 * 4 + 255) // 256 * 256
+    assert _abi.decode_workspace_bytes(4, 128, 8192, 128) == 512 * 4 * 130 * 4
+    assert _abi.decode_workspace_bytes(1, 1, 0, 96) == 0
+
+
 def test_python_ops_refuse_cpu_tensors():
     import torch
 
@@ -172,3 +214,9 @@ def test_python_ops_refuse_cpu_tensors():
         dense_attention(q, q, q)
     with pytest.raises(AssertionError):
         streaming_forward(q[0], q, q, 64, 128)
+    from minference.backend.attention import decode_dense
+
+    with pytest.raises(RuntimeError, match="GPU only"):
+        decode_dense(q[:, :, :1], q, q)
+    with pytest.raises(NotImplementedError):
+        decode_dense(q, q, q)

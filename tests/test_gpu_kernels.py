@@ -214,6 +214,61 @@ def test_late_outlier_keys(gpu_device, kind, factor):
 
 
 # ---------------------------------------------------------------------------
+# decode: one query row against the whole cache
+# ---------------------------------------------------------------------------
+DECODE_CASES = [
+    # (B, H, H_kv, S_k, D, dtype)
+    (1, 4, 4, 1, 96, torch.bfloat16),
+    (1, 4, 4, 63, 96, torch.bfloat16),
+    (2, 3, 3, 1000, 96, torch.bfloat16),
+    (1, 8, 2, 4096 + 17, 96, torch.bfloat16),
+    (1, 4, 4, 2048, 64, torch.float16),
+    (1, 2, 2, 3000, 128, torch.bfloat16),
+    (1, 2, 2, 70000, 96, torch.bfloat16),
+]
+
+
+def _decode_inputs(B, H, Hkv, S, D, dtype, seed):
+    q, _, _ = make_qkv(B, H, 1, S, D, dtype, seed=seed)             # RoPE at position S-1
+    _, k, v = make_qkv(B, Hkv, S, S, D, dtype, seed=seed + 1, sink_scale=8.0)
+    return q, k, v
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=[str(c[:5]) + dtype_tag(c[5]) for c in DECODE_CASES])
+def test_decode_vs_oracle(gpu_device, case):
+    from minference.backend.attention import decode_dense
+
+    B, H, Hkv, S, D, dtype = case
+    q, k, v = _decode_inputs(B, H, Hkv, S, D, dtype, seed=S)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    ref = O.dense_causal(np32(q), np32(k), np32(v))  # the single row sees every key
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    decode_dense(dq, dk, dv, out=out32)
+    assert_close_f32(out32, ref, what=f"decode {case}")
+    out = decode_dense(dq, dk, dv, scale=0.05)
+    assert out.dtype == dtype
+    assert_close_lowp(out, O.dense_causal(np32(q), np32(k), np32(v), scale=0.05), what=f"decode lowp {case}")
+
+
+def test_decode_strided_cache_view(gpu_device):
+    """The cache as a slice of a preallocated [B, S_max, H, D] buffer."""
+    from minference.backend.attention import decode_dense
+
+    B, H, S, S_max, D = 2, 4, 777, 1024, 96
+    q, k, v = _decode_inputs(B, H, H, S, D, torch.bfloat16, seed=5)
+    kbuf = torch.zeros(B, S_max, H, D, dtype=torch.bfloat16)
+    vbuf = torch.zeros(B, S_max, H, D, dtype=torch.bfloat16)
+    kbuf[:, :S] = k.transpose(1, 2)
+    vbuf[:, :S] = v.transpose(1, 2)
+    dkb, dvb = to_dev(gpu_device, kbuf, vbuf)
+    dk, dv = dkb.transpose(1, 2)[:, :, :S], dvb.transpose(1, 2)[:, :, :S]
+    assert dk.stride(2) == H * D
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    decode_dense(q.to(gpu_device), dk, dv, out=out32)
+    assert_close_f32(out32, O.dense_causal(np32(q), np32(k), np32(v)), what="decode strided")
+
+
+# ---------------------------------------------------------------------------
 # one mixed layer through the dispatcher plan; strided (HF-like) views; GQA
 # ---------------------------------------------------------------------------
 def _mixed_patterns(H):

@@ -124,9 +124,22 @@ def _tiny_phi3(n_heads=2, n_kv=2, layers=2, seed=0):
     return Phi3ForCausalLM(cfg).eval()
 
 
+def _oracle_decode(q, k, v, out, scale):
+    """CPU stand-in for run_decode_attention: the last query row sees every key."""
+    qn = q.detach().float().numpy()
+    kn = k.detach().float().numpy()
+    vn = v.detach().float().numpy()
+    rep = qn.shape[1] // kn.shape[1]
+    kn, vn = np.repeat(kn, rep, 1), np.repeat(vn, rep, 1)
+    res = O.dense_causal(qn, kn, vn, scale=scale)
+    out.copy_(torch.from_numpy(res).to(out.dtype))
+    return out
+
+
 @pytest.fixture
 def cpu_launch(monkeypatch):
     monkeypatch.setattr(MF, "run_layer_attention", _oracle_launch)
+    monkeypatch.setattr(MF, "run_decode_attention", _oracle_decode)
 
 
 @pytest.mark.parametrize("n_kv", [2, 1])
