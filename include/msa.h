@@ -101,11 +101,16 @@ size_t msa_estimate_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_q,
  *   slot_topk[s]  (host array or NULL = all topk_max) = top-k of slot s,
  *                 1 <= slot_topk[s] <= topk_max <= n_kv_blocks (the caller
  *                 clamps topk_blocks to n_kv_blocks as the reference does)
- *   idx  [B][n_slots][n_qb][topk_max] int32 (device): the first cnt entries
- *        are the selected causal block ids ascending, entries cnt..topk-1 are
- *        the next future ids bq+1, bq+2, ... (never attended), entries
- *        topk..topk_max-1 are left untouched
- *   cnt  [B][n_slots][n_qb] int32 (device): min(topk, bq+1) */
+ *   idx  [B][n_slots][n_qb][topk_max] int32 (device): the first
+ *        c = min(topk, bq+1) entries are the selected block ids ascending,
+ *        entries c..topk-1 are the next ids bq+1, bq+2, ... (the reference's
+ *        -inf picks in the q-block frame), entries topk..topk_max-1 are left
+ *        untouched
+ *   cnt  [B][n_slots][n_qb] int32 (device): how many leading entries any row
+ *        of query block bq may attend under the absolute token-causal mask
+ *        (row i at S_k - S_q + i): c, plus the surplus ids at or before the
+ *        block's last row when S_q < S_k (reference
+ *        minference/ops/block_sparse_kernel_npu.py:279-314) */
 int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k,
                        const int32_t* slot_heads, const int32_t* slot_topk,
                        int32_t n_slots, int32_t block, int32_t topk_max,

@@ -146,6 +146,8 @@ int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t
   sp.topk_max = topk_max;
   sp.batch = int(q->size[0]);
   sp.n_slots = n_slots;
+  sp.s_q = int(q->size[2]);
+  sp.s_k = int(k->size[2]);
   sp.scale = score_scale;
   for (int s = 0; s < n_slots; ++s) sp.slot_topk[s] = int16_t(slot_topk ? slot_topk[s] : topk_max);
   e = launch_score(sp, D, hs);
@@ -356,7 +358,7 @@ int msa_layer_attention_staged(const msa_tensor4* q, const msa_tensor4* k, const
 // Key splits of one decode call: about 2048 workgroups in all, at least 64
 // keys each.
 static void decode_split(int64_t bh, int64_t s_k, int& n_split, int& chunk) {
-  int64_t ns = (2048 + bh - 1) / bh;
+  int64_t ns = (kDecodeMaxSplit + bh - 1) / bh;
   ns = std::max<int64_t>(1, std::min<int64_t>(ns, cdiv(s_k, 64)));
   int64_t ch = cdiv(s_k, ns);
   ch = cdiv(ch, 64) * 64;
@@ -412,6 +414,7 @@ int msa_decode_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_t
   decode_split(B * H, Sk, dp.n_split, dp.chunk);
   dp.scale_log2 = float(double(scale) * 1.4426950408889634);
   dp.part = static_cast<float*>(workspace);
+  dp.ml = dp.part + B * H * dp.n_split * D;
   const hipError_t e = launch_decode(dp, q->dtype, o->dtype, D, reinterpret_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSA_OK : int(e);
 }

@@ -20,8 +20,8 @@
 // update of the same pieces of V.  Rows with another stride use the same
 // pieces, addressed row by row.
 //
-// Each workgroup leaves (m, l, O[D]) for its key range in the workspace; the
-// combine kernel merges the splits of a head and writes the output row.
+// Each workgroup leaves O[D] and (m, l) for its key range in the workspace;
+// the combine kernel merges the splits of a head and writes the output row.
 
 #include "msa_common.h"
 #include "msa_kernels.h"
@@ -86,12 +86,14 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams P) {
     koff[i] = uint32_t(key_i[i]) * uint32_t(P.k_ss) * 2u + 2u * d0_i[i];
     voff[i] = uint32_t(key_i[i]) * uint32_t(P.v_ss) * 2u + 2u * d0_i[i];
   }
-  auto load_block = [&](int j0, u32x4 (&kr)[NL], u32x4 (&vr)[NL]) {
+  // K and V are read once per call: loads carry the non-temporal hint (cache
+  // policy bit 1) so the stream does not evict reused lines.
+  auto load_block = [&](int j0, u32x4 (&kr)[NL], u32x4 (&vr)[NL]) __attribute__((always_inline)) {
     const int ks = j0 * int(P.k_ss) * 2, vs = j0 * int(P.v_ss) * 2;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff[i], ks, 0));
-      vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i], vs, 0));
+      kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, koff[i], ks, 2));
+      vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i], vs, 2));
     }
   };
 
@@ -104,14 +106,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams P) {
   float l = 0.0f;               // running sum (lanes 0..15 hold partial sums)
   const float c = P.scale_log2;
 
-  const int first = j_begin + 16 * w;
-  u32x4 kc[NL], vc[NL], kn[NL], vn[NL];
-  // loads are unconditional (past the range they repeat the current block;
-  // rows at or past S read 0), so the waits stay exact
-  load_block(first, kc, vc);
-  for (int j0 = first; j0 < j_end; j0 += 64) {
-    const int jn = j0 + 64;
-    load_block(jn < j_end ? jn : j0, kn, vn);
+  // one 16-key block: scores, online softmax, O update
+  auto block = [&](int j0, const u32x4(&kc)[NL], const u32x4(&vc)[NL]) __attribute__((always_inline)) {
     // partial dot products of this lane's pieces
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -155,11 +151,28 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams P) {
       }
     }
     __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      kc[i] = kn[i];
-      vc[i] = vn[i];
-    }
+  };
+
+  // Wave w takes blocks first + 64 i, i < nblk, two blocks in flight ahead
+  // of the one being reduced, in three rotating register sets.  Loads past
+  // the wave's last block repeat that block, so every load is unconditional
+  // and in range.
+  const int first = j_begin + 16 * w;
+  const int nblk = j_end > first ? (j_end - first + 63) / 64 : 0;
+  const int last = first + 64 * max(nblk - 1, 0);
+  auto jb = [&](int i) { return min(first + 64 * i, last); };
+  u32x4 ka[NL], va[NL], kb[NL], vb[NL], kc[NL], vc[NL];
+  load_block(jb(0), ka, va);
+  load_block(jb(1), kb, vb);
+  for (int i = 0; i < nblk; i += 3) {
+    load_block(jb(i + 2), kc, vc);
+    block(first + 64 * i, ka, va);
+    if (i + 1 >= nblk) break;
+    load_block(jb(i + 3), ka, va);
+    block(first + 64 * (i + 1), kb, vb);
+    if (i + 2 >= nblk) break;
+    load_block(jb(i + 4), kb, vb);
+    block(first + 64 * (i + 2), kc, vc);
   }
 
   // ---- merge the 4 waves and the 16 key positions of every piece
@@ -199,34 +212,77 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams P) {
       }
       acc += f * sv;
     }
-    float* dst = P.part + (int64_t(bh) * P.n_split + split) * (D + 2);
-    dst[d] = acc;
+    const int64_t row = int64_t(bh) * P.n_split + split;
+    P.part[row * D + d] = acc;
     if (d == 0) {
-      dst[D] = M;
-      dst[D + 1] = L;
+      P.ml[2 * row] = M;
+      P.ml[2 * row + 1] = L;
     }
   }
 }
 
 // Merge the splits of one head: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+// Every load is independent: the (m, l) pairs are read once into LDS, then
+// G groups of D/4 threads each sum a stride of splits with 16-byte loads and
+// the groups reduce through LDS.
 template <typename T, bool OUT_F32, int D>
-__global__ __launch_bounds__(128) void decode_combine_kernel(DecodeParams P) {
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams P) {
+  constexpr int TPR = D / 4;    // threads per split row, 4 elements each
+  constexpr int G = 256 / TPR;  // split groups
+  __shared__ float fs[kDecodeMaxSplit];
+  __shared__ float red[8];
+  __shared__ __align__(16) float acc_g[G][D];
   const int bh = blockIdx.x;
   const int b = bh / P.heads, h = bh - b * P.heads;
-  const float* src = P.part + int64_t(bh) * P.n_split * (D + 2);
-  const int d = threadIdx.x;
-  float M = -__builtin_inff();
-  for (int s = 0; s < P.n_split; ++s) M = fmaxf(M, src[s * (D + 2) + D]);
-  float L = 0.0f, acc = 0.0f;
-  for (int s = 0; s < P.n_split; ++s) {
-    const float ms = src[s * (D + 2) + D];
-    const float f = ms == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-    L += f * src[s * (D + 2) + D + 1];
-    if (d < D) acc += f * src[s * (D + 2) + d];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int ns = P.n_split;
+  const float* ml = P.ml + int64_t(bh) * ns * 2;
+
+  float mx = -__builtin_inff();
+  for (int s = tid; s < ns; s += 256) {
+    const float ms = ml[2 * s];
+    fs[s] = ms;
+    mx = fmaxf(mx, ms);
   }
-  if (d < D) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) red[w] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float L = 0.0f;
+  for (int s = tid; s < ns; s += 256) {
+    const float f = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(fs[s] - M);
+    fs[s] = f;
+    L += f * ml[2 * s + 1];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
+  if (lane == 0) red[4 + w] = L;
+  __syncthreads();
+  L = (red[4] + red[5]) + (red[6] + red[7]);
+
+  const int g = tid / TPR, c = tid - g * TPR;
+  if (g < G) {
+    const float* src = P.part + int64_t(bh) * ns * D + 4 * c;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll 4
+    for (int s = g; s < ns; s += G) {
+      const float4 x = *reinterpret_cast<const float4*>(src + int64_t(s) * D);
+      const float f = fs[s];
+      a0 = __builtin_fmaf(f, x.x, a0);
+      a1 = __builtin_fmaf(f, x.y, a1);
+      a2 = __builtin_fmaf(f, x.z, a2);
+      a3 = __builtin_fmaf(f, x.w, a3);
+    }
+    *reinterpret_cast<float4*>(&acc_g[g][4 * c]) = float4{a0, a1, a2, a3};
+  }
+  __syncthreads();
+  if (tid < D) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < G; ++q) acc += acc_g[q][tid];
     const float r = L > 0.0f ? acc / L : 0.0f;
-    const int64_t off = b * P.o_sb + int64_t(h) * P.o_sh + d;
+    const int64_t off = b * P.o_sb + int64_t(h) * P.o_sh + tid;
     if constexpr (OUT_F32) {
       reinterpret_cast<float*>(P.o)[off] = r;
     } else {
@@ -240,7 +296,7 @@ static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t st) {
   hipLaunchKernelGGL((decode_kernel<T, D>), dim3(p.n_split, p.batch * p.heads), dim3(256), 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((decode_combine_kernel<T, OUT_F32, D>), dim3(p.batch * p.heads), dim3(128), 0,
+  hipLaunchKernelGGL((decode_combine_kernel<T, OUT_F32, D>), dim3(p.batch * p.heads), dim3(256), 0,
                      st, p);
   return hipGetLastError();
 }

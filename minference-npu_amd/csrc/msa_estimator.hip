@@ -249,9 +249,16 @@ __global__ __launch_bounds__(256) void score_topk_kernel(ScoreParams P) {
     } else {
       wave_topk(sc + r * ncand, n, topk, hist + w * 256, out, lane);
     }
-    // surplus slots: the next future ids, never attended (token-causal mask)
+    // Surplus slots (the reference's -inf picks, which torch.topk fills with
+    // q-frame future ids): the next ids bq+1, bq+2, ...  The token mask is
+    // in the absolute frame (row i at s_k - s_q + i), so with s_q < s_k some
+    // of them lie in the past of the block's rows and are attended; the
+    // count covers the selected ids plus those surplus ids whose first key
+    // is at or before the block's last absolute row.
     for (int p = cnt + lane; p < topk; p += 64) out[p] = bq + 1 + (p - cnt);
-    if (lane == 0) P.cnt[int64_t(sb) * P.n_qb + bq] = cnt;
+    const int a1 = P.s_k - P.s_q + min(64 * bq + 63, P.s_q - 1);
+    const int n_sur = max(0, min(topk - cnt, (a1 >> 6) - bq));
+    if (lane == 0) P.cnt[int64_t(sb) * P.n_qb + bq] = cnt + n_sur;
   }
 }
 

@@ -27,6 +27,7 @@ struct ScoreParams {
   int32_t* idx;  // [batch*n_slots][n_qb][topk_max]
   int32_t* cnt;  // [batch*n_slots][n_qb]
   int n_qb, n_kb, topk_max, batch, n_slots;
+  int s_q, s_k;  // row i of the query is absolute position s_k - s_q + i
   float scale;
   int16_t slot_topk[kMaxHeads];
 };
@@ -79,8 +80,12 @@ struct DecodeParams {
   int batch, heads, kv_group, s_k;
   int n_split, chunk;  // key range of split s: [s*chunk, min((s+1)*chunk, s_k))
   float scale_log2;    // softmax scale * log2(e)
-  float* part;         // workspace [batch*heads][n_split][D+2]: O, m, l per split
+  float* part;         // workspace [batch*heads][n_split][D]: unnormalised O per split
+  float* ml;           // workspace [batch*heads][n_split][2]: (m, l) per split
 };
+
+// Most splits a decode call uses (one head alone gets this many).
+constexpr int kDecodeMaxSplit = 2048;
 
 hipError_t launch_pool(const PoolParams& p, int dtype, int D, hipStream_t st);
 hipError_t launch_score(const ScoreParams& p, int D, hipStream_t st);

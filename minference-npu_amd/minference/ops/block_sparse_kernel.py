@@ -73,7 +73,9 @@ def select_block_sparse_topk_indices(
     with fewer causal blocks than ``topk``) hold the next future ids; the
     reference fills them with ``torch.topk``'s choice among ``-inf`` scores,
     and the token-level causal mask discards them in both implementations.
-    With ``return_counts=True`` also returns the per-row causal counts.
+    With ``return_counts=True`` also returns the per-row counts of leading ids
+    some row of the query block attends: min(topk, bq+1), plus, when
+    S_q < S_k, the surplus ids that lie before the block's last absolute row.
     """
     check_bnsd(q, k)
     check_supported(q, k)

@@ -46,6 +46,7 @@ __all__ = [
     "block_scores",
     "select_topk",
     "select_block_sparse_topk_indices",
+    "attend_count",
     "stream_visible",
     "streaming_attention",
     "block_token_visible",
@@ -189,6 +190,19 @@ def select_block_sparse_topk_indices(q: np.ndarray, k: np.ndarray, topk_blocks: 
     qp = pool_blocks(q, dtype, block)
     kp = pool_blocks(k, dtype, block)
     return select_topk(block_scores(qp, kp, scale), max(1, int(topk_blocks)))
+
+
+def attend_count(idx: np.ndarray, s_q: int, s_k: int, block: int = BLOCK) -> np.ndarray:
+    """Per id row [..., n_bq, topk] (ascending): how many ids some row of the
+    query block can attend under the absolute token-causal mask, row i at
+    s_k - s_q + i (block_sparse_kernel_npu.py:310-314).  An id counts when
+    its first key is at or before the block's last row; the counted ids are a
+    prefix of the row.  With s_q == s_k this is min(topk, bq + 1); with
+    s_q < s_k it includes surplus (q-frame future) ids in the rows' past."""
+    idx = np.asarray(idx)
+    n_bq = idx.shape[-2]
+    last = s_k - s_q + np.minimum(np.arange(n_bq) * block + block - 1, s_q - 1)
+    return (idx * block <= last[:, None]).sum(-1)
 
 
 # ---------------------------------------------------------------------------

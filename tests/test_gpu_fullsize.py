@@ -65,6 +65,7 @@ def test_cfg2_block_ids_bit_exact_and_rows(gpu_device):
     ridx, rcnt = O.select_block_sparse_topk_indices(qn, kn, topk, "bf16")
     gi = idx.cpu().numpy()
     assert np.array_equal(cnt.cpu().numpy(), rcnt)
+    assert np.array_equal(rcnt, O.attend_count(ridx, S, S))
     assert np.array_equal(gi, ridx), f"{(gi != ridx).sum()} block ids differ"
 
     print("[cfg2] attention", flush=True)

@@ -52,6 +52,8 @@ EST_CASES = [
     (1, 2, 2048, 2048, 128, 7, torch.float16, None),
     (1, 4, 640, 640, 96, 1, torch.float16, 8.0),
     (1, 2, 512, 1024, 96, 5, torch.bfloat16, None),
+    (1, 2, 100, 700, 96, 3, torch.bfloat16, None),     # chunk with S_k - S_q not a block multiple
+    (1, 2, 300, 2000, 96, 100, torch.bfloat16, 8.0),   # top-k clamped to n_kb
 ]
 
 
@@ -66,7 +68,7 @@ def test_estimator_bit_exact(gpu_device, case):
     got_i = idx.cpu().numpy()
     got_c = cnt.cpu().numpy()
     assert got_i.shape == ridx.shape
-    assert np.array_equal(got_c, rcnt)
+    assert np.array_equal(got_c, O.attend_count(ridx, S_q, S_k))
     assert np.array_equal(got_i, ridx), f"{(got_i != ridx).sum()} ids differ"
 
 
@@ -129,6 +131,27 @@ BLOCK_CASES = [
     (1, 2, 2048, 128, 8, torch.float16, 8.0),
     (1, 4, 4096, 96, 16, torch.bfloat16, 8.0),
 ]
+BLOCK_CHUNK_CASES = [
+    # (S_q, S_k, topk): chunked prefill, the q-frame -inf picks attended
+    (100, 700, 3),
+    (512, 1024, 5),
+    (300, 2000, 100),   # top-k clamped to n_kb: causal dense
+    (1000, 4113, 16),
+]
+
+
+@pytest.mark.parametrize("case", BLOCK_CHUNK_CASES, ids=[str(c) for c in BLOCK_CHUNK_CASES])
+def test_block_sparse_chunked_vs_oracle(gpu_device, case):
+    from minference import block_sparse_attention
+
+    s_q, s_k, topk = case
+    q, k, v = make_qkv(1, 3, s_q, s_k, 96, torch.bfloat16, seed=s_q + topk, sink_scale=8.0)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    block_sparse_attention(dq, dk, dv, topk, out=out32)
+    idx, _ = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, "bf16")
+    ref = O.block_sparse_from_indices(np32(q), np32(k), np32(v), idx)
+    assert_close_f32(out32, ref, what=f"block chunk {case}")
 
 
 @pytest.mark.parametrize("case", BLOCK_CASES, ids=[str(c[:5]) + dtype_tag(c[5]) for c in BLOCK_CASES])

@@ -94,3 +94,58 @@ def test_patched_dense_model_matches_hf(gpu_device, tmp_path):
     assert nxt.shape == (1, 103)
     rel = (got - ref).abs().max() / ref.abs().max()
     assert rel < 2e-2, rel
+
+
+def test_patched_chunked_prefill_and_decode_match_oracle(gpu_device, tmp_path, monkeypatch):
+    """Prefill in two chunks through a cache (the second with S_q < S_k), then
+    decode steps: every attention launch of the patched model is checked
+    against the oracle on the inputs it received."""
+    from transformers import DynamicCache
+
+    model = _tiny_phi3(gpu_device, n_kv=2)
+    recs = [P.record("stream_llm", 64, 256), P.record("block_sparse", 3), P.record("dense"),
+            P.record("block_sparse", 100)]
+    path = tmp_path / "mix.json"
+    P.write(str(path), [{str(h): recs[(h + layer) % 4] for h in range(8)} for layer in range(2)])
+    captured = []
+    real_l, real_d = MF.run_layer_attention, MF.run_decode_attention
+
+    def spy_l(q, k, v, plan, out):
+        res = real_l(q, k, v, plan, out)
+        captured.append(("layer", q.clone(), k.clone(), v.clone(), plan, res.float().clone()))
+        return res
+
+    def spy_d(q, k, v, out, scale):
+        res = real_d(q, k, v, out, scale)
+        captured.append(("decode", q.clone(), k.clone(), v.clone(), scale, res.float().clone()))
+        return res
+
+    monkeypatch.setattr(MF, "run_layer_attention", spy_l)
+    monkeypatch.setattr(MF, "run_decode_attention", spy_d)
+    patched = MInference(attn_type="minference", config_path=str(path))(model)
+    ids = torch.randint(3, 256, (1, 700), device=gpu_device,
+                        generator=torch.Generator(device=gpu_device).manual_seed(3))
+    cache = DynamicCache()
+    with torch.no_grad():
+        patched(ids[:, :600], past_key_values=cache, use_cache=True)
+        logits = patched(ids[:, 600:], past_key_values=cache, use_cache=True).logits
+        nxt = logits[:, -1:].argmax(-1)
+        for _ in range(3):
+            logits = patched(nxt, past_key_values=cache, use_cache=True).logits
+            assert torch.isfinite(logits).all()
+            nxt = logits[:, -1:].argmax(-1)
+    kinds = [c[0] for c in captured]
+    assert kinds == ["layer"] * 4 + ["decode"] * 6, kinds
+    assert captured[2][1].shape[2] == 100 and captured[2][2].shape[2] == 700
+    assert captured[-1][2].shape[2] == 703
+    for kind, q, k, v, plan_or_scale, got in captured:
+        if kind == "layer":
+            ref = _oracle_layer(q, k, v, plan_or_scale)
+        else:
+            qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+            rep = qn.shape[1] // kn.shape[1]
+            ref = O.dense_causal(qn, np.repeat(kn, rep, 1), np.repeat(vn, rep, 1),
+                                 scale=plan_or_scale)
+        g = got.cpu().numpy().astype(np.float64)
+        bound = 2e-3 + np.abs(ref) * 2.0 ** -8  # bf16 output of the model
+        assert (np.abs(g - ref) <= bound).all(), (kind, q.shape, np.abs(g - ref).max())

@@ -307,6 +307,38 @@ def test_block_full_topk_equals_dense(S):
     assert np.abs(a - b).max() < 1e-12
 
 
+@pytest.mark.parametrize("s_q,s_k", [(128, 512), (100, 700), (300, 2000)])
+def test_block_chunked_full_topk_equals_dense(s_q, s_k):
+    """Chunked prefill (S_q < S_k): with top-k = n_kb every id row holds all
+    blocks (the causal picks plus the q-frame -inf picks), so the token mask
+    reduces to the absolute causal mask and the output to causal dense."""
+    q, k, v = make_qkv(B=1, H=2, S_q=s_q, S_k=s_k, D=64, dtype=torch.float32, seed=s_q)
+    nb = -(-s_k // 64)
+    idx, cnt = O.select_block_sparse_topk_indices(np32(q), np32(k), nb, "fp32")
+    assert (np.sort(idx, -1) == np.arange(nb)).all()
+    s = O.sparse_scale(64)
+    a = O.block_sparse_from_indices(np32(q), np32(k), np32(v), idx, scale=s)
+    b = O.dense_causal(np32(q), np32(k), np32(v), scale=s)
+    assert np.abs(a - b).max() < 1e-12
+
+
+@pytest.mark.parametrize("s_q,s_k,topk", [(64, 64, 1), (256, 256, 3), (100, 700, 3), (128, 512, 5),
+                                          (70, 1000, 16), (300, 2000, 40)])
+def test_attend_count_bruteforce(s_q, s_k, topk):
+    """attend_count against the token mask itself: id b of block row bq counts
+    iff some (row of bq, key of b) pair is visible."""
+    q, k, _ = make_qkv(B=1, H=1, S_q=s_q, S_k=s_k, D=32, dtype=torch.float32, seed=topk)
+    idx, cnt = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, "fp32")
+    got = O.attend_count(idx, s_q, s_k)[0, 0]
+    for bq in range(idx.shape[2]):
+        vis = O.block_token_visible(idx[0, 0], s_q, s_k)[64 * bq:64 * bq + 64]
+        seen = [b for b in idx[0, 0, bq] if vis[:, 64 * b:64 * b + 64].any()]
+        assert got[bq] == len(seen)
+        assert list(idx[0, 0, bq, :got[bq]]) == seen  # a prefix of the row
+        if s_q == s_k:
+            assert got[bq] == cnt[0, 0, bq] == min(topk, bq + 1)
+
+
 def test_block_q0_closed_form_and_bruteforce():
     S, topk = 448, 3
     q, k, v = make_qkv(B=1, H=1, S_q=S, D=64, dtype=torch.bfloat16, seed=4)
