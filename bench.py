@@ -35,6 +35,7 @@ for _p in (ROOT, os.path.join(ROOT, "minference-npu_amd"), os.path.join(ROOT, "t
         sys.path.insert(0, _p)
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (no sparsity)
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 BLOCK = 64
 
 # workload -> profile summary holding the calibrated HBM traffic of the attention kernel
@@ -59,6 +60,7 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-dense", action="store_true", help="skip the same-GPU dense baselines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
     ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads of BASELINE config 1 timed on the CPU (scaled to 32)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -317,11 +319,47 @@ def main():
         },
     }
 
+    if not args.no_decode:
+        result["decode"] = decode_bench(k, v, S, H, D, args.seed)
     if not args.no_dense:
         result["dense"] = dense_baselines(q, k, v, S, H, D, ms_step)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_heads)
     print(json.dumps(result), flush=True)
+
+
+def decode_bench(k, v, S, H, D, seed, reps=20):
+    """One decode step of the layer (msa_decode_attention: q [1,H,1,D] against
+    the whole K/V cache of S keys), timed with HIP events on the launch
+    stream.  K and V (4*D bytes per key and head) are read once per step and
+    exceed the on-die cache at the headline length, so the step is bound by
+    HBM."""
+    import torch
+
+    from minference import _abi
+    from minference.ops.common import dense_scale
+
+    g = torch.Generator(device=k.device).manual_seed(seed + 7)
+    q1 = torch.randn((1, H, 1, D), generator=g, device=k.device).to(k.dtype)
+    out = torch.empty_like(q1)
+    ws = _abi.workspace(_abi.decode_workspace_bytes(1, H, S, D), k.device)
+    sc = dense_scale(D)
+    stream = torch.cuda.current_stream(k.device)
+    for _ in range(3):
+        _abi.decode_attention(q1, k, v, out, sc, ws)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reps)]
+    torch.cuda.synchronize()
+    for i in range(reps):
+        ev[2 * i].record(stream)
+        _abi.decode_attention(q1, k, v, out, sc, ws)
+        ev[2 * i + 1].record(stream)
+    torch.cuda.synchronize()
+    us = sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(reps)) / reps * 1e3
+    nbytes = 2 * H * S * D * k.element_size()
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"s_k": S, "heads": H, "us_per_layer": round(us, 2), "kv_bytes": nbytes,
+            "hbm_gbps": round(gbps, 1), "frac_hbm_peak": round(gbps / PEAK_HBM_GBPS, 4),
+            "kernels": "msa::decode_kernel + msa::decode_combine_kernel"}
 
 
 def dense_baselines(q, k, v, S, H, D, ms_sparse):
