@@ -47,6 +47,11 @@ __all__ = [
     "select_topk",
     "select_block_sparse_topk_indices",
     "attend_count",
+    "vs_sizes",
+    "vs_scores",
+    "vs_estimate",
+    "vs_token_visible",
+    "vertical_slash_from_indices",
     "stream_visible",
     "streaming_attention",
     "block_token_visible",
@@ -206,6 +211,84 @@ def attend_count(idx: np.ndarray, s_q: int, s_k: int, block: int = BLOCK) -> np.
 
 
 # ---------------------------------------------------------------------------
+# vertical_and_slash estimator (minference_forward.py:140-167)
+# ---------------------------------------------------------------------------
+LAST_Q = 64          # query rows the estimator looks at (minference_forward.py:43)
+VS_SINK_COLS = 30    # columns forced into the vertical set (:157)
+VS_LOCAL_DIAGS = 100  # nearest diagonals forced into the slash set (:163)
+
+
+def vs_sizes(s: int, vertical_size: int, slash_size: int):
+    """Clamped sizes of :146-147: min(S, max(v, 30)) and min(S, max(s, 50))."""
+    return min(s, max(int(vertical_size), 30)), min(s, max(int(slash_size), 50))
+
+
+def vs_scores(q: np.ndarray, k: np.ndarray, dtype: str):
+    """Column sums and anti-diagonal sums of the last-rows attention of one
+    head (:148-164).  q, k: [S, D] with S_q == S_k.
+
+    * scores: q[-n:] . k^T formed in fp64 (exact for 16-bit operands), rounded
+      to fp32 and to the input dtype (the reference's matmul output dtype),
+      then divided by fp32(sqrt(D)) and rounded to the input dtype again
+      (``/ math.sqrt(D)`` on a bf16/fp16 tensor);
+    * the last n columns get the causal mask of :150-151 (row r sees column
+      S - n + c iff c <= r);
+    * softmax in fp64 (the reference's fp32 softmax, here without its
+      rounding), then column sums and the sums along each diagonal
+      t = 0 .. S-1 (t indexes sum_all_diagonal_matrix's output, :124-137,
+      truncated at :161-162), each rounded once to fp32;
+    * the first 30 columns and the last 100 diagonals are set to +inf.
+
+    Returns (vertical [S] fp32, slash [S] fp32)."""
+    S, D = k.shape
+    n = min(LAST_Q, S)
+    ql = np.asarray(q[S - n:], dtype=np.float64)
+    dots = ql @ np.asarray(k, dtype=np.float64).T                    # [n, S]
+    a = round_to(dots.astype(np.float32), dtype)
+    x = round_to(a / np.float32(math.sqrt(D)), dtype).astype(np.float64)
+    r = np.arange(n)[:, None]
+    c = np.arange(S)[None, :] - (S - n)
+    x = np.where(c > r, -np.inf, x)
+    m = x.max(axis=1, keepdims=True)
+    e = np.exp(x - m)
+    p = e / e.sum(axis=1, keepdims=True)
+    vert = p.sum(axis=0).astype(np.float32)
+    slash = np.zeros(S)
+    for i in range(n):
+        lo = n - 1 - i                     # first diagonal that meets row i
+        slash[lo:] += p[i, : S - lo]       # column i + t + 1 - n for t = lo .. S-1
+    slash = slash.astype(np.float32)
+    vert[:VS_SINK_COLS] = np.inf
+    slash[max(0, S - VS_LOCAL_DIAGS):] = np.inf
+    return vert, slash
+
+
+def _topk_lower(vals: np.ndarray, k: int) -> np.ndarray:
+    """Indices of the k largest values, ties to the lower index."""
+    return np.argsort(-vals.astype(np.float64), kind="stable")[:k]
+
+
+def vs_estimate(q: np.ndarray, k: np.ndarray, vertical_size: int, slash_size: int,
+                dtype: str):
+    """Vertical and slash indices of every head (:140-165).  q [B, H, S, D],
+    k [B, H_kv, S, D].  Returns (v_idx [B, H, nv] ascending, s_idx [B, H, ns]
+    descending), nv/ns from vs_sizes; s = S - 1 - t for the selected
+    diagonals t.  Ties in the top-k go to the lower column / diagonal index
+    (torch.topk's choice among exact ties is unspecified)."""
+    B, H, S, D = q.shape
+    assert k.shape[2] == S, "vertical_and_slash needs S_q == S_k"
+    kvg = H // k.shape[1]
+    nv, ns = vs_sizes(S, vertical_size, slash_size)
+    v_idx = np.empty((B, H, nv), dtype=np.int64)
+    s_idx = np.empty((B, H, ns), dtype=np.int64)
+    for b, h in _heads(q):
+        vert, slash = vs_scores(q[b, h], k[b, h // kvg], dtype)
+        v_idx[b, h] = np.sort(_topk_lower(vert, nv))
+        s_idx[b, h] = np.sort(S - 1 - _topk_lower(slash, ns))[::-1]
+    return v_idx, s_idx
+
+
+# ---------------------------------------------------------------------------
 # token visibility
 # ---------------------------------------------------------------------------
 def stream_visible(s_q: int, s_k: int, n_init: int, n_local: int) -> np.ndarray:
@@ -230,6 +313,31 @@ def block_token_visible(idx_row: np.ndarray, s_q: int, s_k: int, block: int = BL
     a = np.arange(s_k - s_q, s_k)[:, None]
     j = np.arange(s_k)[None, :]
     return tok & (j <= a)
+
+
+def vs_token_visible(v_idx_row: np.ndarray, s_idx_row: np.ndarray, s_q: int, s_k: int,
+                     block: int = BLOCK) -> np.ndarray:
+    """Token mask of one vertical_and_slash head (vertical_slash_kernel_npu.py:
+    282-367, the reference's production path; True = visible).  Query block
+    bq (end_m = 64(bq+1)) sees, for every slash s < end_m, the 64 keys
+    [hi - 64, hi) with hi = clamp(end_m - s, 64, S_k); every row sees the
+    vertical columns (clamped into [0, S_k)); then the causal mask j <= i."""
+    assert s_q == s_k, "vertical_and_slash needs S_q == S_k"
+    n_rows = -(-s_k // block)
+    cov = np.zeros((n_rows, s_k), dtype=bool)
+    for bq in range(n_rows):
+        end_m = (bq + 1) * block
+        for s in np.asarray(s_idx_row).tolist():
+            if s < end_m:
+                hi = min(max(end_m - s, block), s_k)
+                lo = min(max(hi - block, 0), s_k)
+                cov[bq, lo:hi] = True
+    vert = np.zeros(s_k, dtype=bool)
+    vert[np.clip(np.asarray(v_idx_row), 0, s_k - 1)] = True
+    tok = np.repeat(cov | vert[None, :], block, axis=0)[:s_q]
+    i = np.arange(s_q)[:, None]
+    j = np.arange(s_k)[None, :]
+    return tok & (j <= i)
 
 
 # ---------------------------------------------------------------------------
@@ -295,6 +403,23 @@ def block_sparse_from_indices(q, k, v, idx, scale: float | None = None,
     out = np.zeros((B, H, s_q, D), dtype=acc)
     for b, h in _heads(q):
         vis = block_token_visible(np.asarray(idx[b, h]), s_q, s_k)
+        out[b, h] = masked_attention(q[b, h], k[b, h // kvg], v[b, h // kvg], vis, scale, acc)
+    return out
+
+
+def vertical_slash_from_indices(q, k, v, v_idx, s_idx, scale: float | None = None,
+                                acc=np.float64) -> np.ndarray:
+    """Vertical-slash attention for given indices v_idx [B, H, nv] and s_idx
+    [B, H, ns] (_vertical_slash_pytorch_ref, vertical_slash_kernel_npu.py:375-407;
+    scale (padded D)**-0.5 after the pad at :581-587)."""
+    if scale is None:
+        scale = sparse_scale(q.shape[-1])
+    B, H, s_q, D = q.shape
+    s_k = k.shape[2]
+    kvg = H // k.shape[1]
+    out = np.zeros((B, H, s_q, D), dtype=acc)
+    for b, h in _heads(q):
+        vis = vs_token_visible(v_idx[b, h], s_idx[b, h], s_q, s_k)
         out[b, h] = masked_attention(q[b, h], k[b, h // kvg], v[b, h // kvg], vis, scale, acc)
     return out
 
