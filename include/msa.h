@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MSA_ABI_VERSION 3
+#define MSA_ABI_VERSION 4
 
 /* status codes (negative: validation, nothing launched) */
 #define MSA_OK 0
@@ -43,7 +43,7 @@ extern "C" {
 #define MSA_E_HEADS (-8)       /* bad head count / head index / kind */
 #define MSA_E_WORKSPACE (-9)   /* workspace missing or too small */
 #define MSA_E_SEQ (-10)        /* S_q > S_k, S_q == 0, or too long */
-#define MSA_E_SLOTS (-11)      /* block-sparse head without an index slot */
+#define MSA_E_SLOTS (-11)      /* sparse head without an index slot, or bad index lists */
 
 /* element types */
 #define MSA_DTYPE_BF16 1
@@ -54,6 +54,9 @@ extern "C" {
 #define MSA_KIND_DENSE 0  /* "dense"        */
 #define MSA_KIND_STREAM 1 /* "stream_llm"   */
 #define MSA_KIND_BLOCK 2  /* "block_sparse" */
+#define MSA_KIND_VS 3     /* "vertical_and_slash" */
+
+#define MSA_VS_MAX_SEQ 131072 /* longest S of a vertical_and_slash head */
 
 #define MSA_MAX_HEADS 128 /* head descriptors per msa_layer_attention call */
 #define MSA_BLOCK 64      /* the only supported block size */
@@ -160,6 +163,52 @@ int msa_layer_attention_staged(const msa_tensor4* q, const msa_tensor4* k,
                                int32_t idx_slots, int32_t topk_max, void* workspace,
                                size_t workspace_bytes, msa_stream_t stream);
 
+
+/* vertical_and_slash index lists of a layer: one slot per vertical_and_slash
+ * head (msa_head_desc.slot).  Device arrays:
+ *   v_idx [B][n_slots][v_stride]: vertical columns, ascending, distinct, in
+ *         [0, S_k); the first v_cnt[b][slot] entries are used
+ *   s_idx [B][n_slots][s_stride]: slash offsets s (the diagonal key = row - s),
+ *         any order and range; the first s_cnt[b][slot] entries are used
+ * These are the v_idx / s_idx of the reference's
+ * vertical_slash_sparse_attention (minference/ops/vertical_slash_kernel_npu.py:
+ * 518-525), with per-row counts.  Every head sharing a slot must read the
+ * same kv head. */
+typedef struct msa_vs_lists {
+  const int32_t* v_idx;
+  const int32_t* v_cnt;
+  const int32_t* s_idx;
+  const int32_t* s_cnt;
+  int32_t n_slots;
+  int32_t v_stride;
+  int32_t s_stride;
+  int32_t reserved;
+} msa_vs_lists;
+
+/* Bytes of the vertical_and_slash workspace of msa_layer_attention_ex: the
+ * per-(slot, query block) tile lists with their key masks, and the vertical
+ * columns' K and V staged contiguously per slot. */
+size_t msa_vs_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_k, int32_t v_stride,
+                              int32_t head_dim);
+
+/* msa_layer_attention with vertical_and_slash heads (kind MSA_KIND_VS).
+ * Replaces, besides msa_layer_attention's counterparts, the
+ * vertical_and_slash group of minference/modules/minference_forward.py:421-436
+ * and vertical_slash_sparse_attention
+ * (minference/ops/vertical_slash_kernel_npu.py:518-599): visibility of
+ * _build_vs_mask_direct (:282-367) under the causal mask, as one tile-list
+ * build launch, one gather of the vertical columns and one attention launch
+ * for the vertical_and_slash heads (the other heads keep their own launch).
+ * vertical_and_slash heads need S_q == S_k <= MSA_VS_MAX_SEQ and
+ * B * H <= MSA_MAX_HEADS.  vs and vs_workspace may be NULL when no head is
+ * vertical_and_slash.  stage = 0 reads K/V staged by msa_stage_kv (as
+ * msa_layer_attention_staged), 1 stages them first. */
+int msa_layer_attention_ex(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
+                           const msa_tensor4* o, const msa_head_desc* heads, int32_t n_heads,
+                           const int32_t* idx, const int32_t* cnt, int32_t idx_slots,
+                           int32_t topk_max, const msa_vs_lists* vs, void* vs_workspace,
+                           size_t vs_workspace_bytes, void* workspace, size_t workspace_bytes,
+                           int32_t stage, msa_stream_t stream);
 
 /* Decode: one query row per head (q [B][H][1][D]) against the whole cache
  * (k, v [B][H_kv][S_k][D], any strides with D contiguous and 16-byte rows),

@@ -137,6 +137,7 @@ int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t
   if (e != hipSuccess) return int(e);
 
   ScoreParams sp;
+  memset(&sp, 0, sizeof(sp));
   sp.q_pool = q_pool;
   sp.k_poolT = k_poolT;
   sp.idx = idx;
@@ -187,6 +188,7 @@ static int stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
   if (!workspace || workspace_bytes < need) return MSA_E_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
   StageParams sp;
+  memset(&sp, 0, sizeof(sp));  // gather-mode fields stay null: plain staging
   sp.k = k->data;
   sp.v = v->data;
   sp.k_sb = k->stride[0]; sp.k_sh = k->stride[1]; sp.k_ss = k->stride[2];
@@ -206,11 +208,101 @@ int msa_stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
   return stage_kv(k, v, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
+// vertical_and_slash workspace: tile ids, key masks, counts per (slot,
+// query block); gathered vertical K and V per slot.
+struct VsLayout {
+  int64_t n_rows;
+  int cap, nv_pad;
+  size_t ids, masks, cnt, gk, gv, total;
+};
+
+static VsLayout vs_layout(int64_t B, int64_t n_slots, int64_t s_k, int64_t v_stride, int64_t D) {
+  VsLayout L;
+  const int64_t n_kb = cdiv(s_k, MSA_BLOCK);
+  L.nv_pad = int(cdiv(std::max<int64_t>(v_stride, 1), MSA_BLOCK) * MSA_BLOCK);
+  L.cap = int(n_kb + L.nv_pad / MSA_BLOCK);
+  L.n_rows = B * n_slots * n_kb;
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  size_t off = 0;
+  L.ids = off;
+  off = up(off + size_t(L.n_rows) * L.cap * 4);
+  L.masks = off;
+  off = up(off + size_t(L.n_rows) * L.cap * 8);
+  L.cnt = off;
+  off = up(off + size_t(L.n_rows) * 2 * 4);
+  L.gk = off;
+  off = up(off + size_t(B * n_slots) * L.nv_pad * D * 2);
+  L.gv = off;
+  off = up(off + size_t(B * n_slots) * L.nv_pad * D * 2);
+  L.total = off;
+  return L;
+}
+
+size_t msa_vs_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_k, int32_t v_stride,
+                              int32_t head_dim) {
+  if (batch <= 0 || n_slots <= 0 || s_k <= 0 || v_stride <= 0 || head_dim <= 0) return 0;
+  return vs_layout(batch, n_slots, s_k, v_stride, head_dim).total;
+}
+
+// Work estimate of one head in key tiles, for the XCD balance.
+static double head_cost(const msa_head_desc& hd, int n_kb, int topk_max, const msa_vs_lists* vs) {
+  const double nb = double(n_kb);
+  if (hd.kind == MSA_KIND_DENSE) return nb * (nb + 1) / 2;
+  if (hd.kind == MSA_KIND_STREAM) {
+    const double band = fmin(nb, double(hd.p2) / 64.0 + 1.0);
+    const double sink = fmin(nb, ceil(fmax(double(hd.p1), 0.0) / 64.0));
+    return nb * (band + sink);
+  }
+  if (hd.kind == MSA_KIND_VS) {
+    const double per = fmin(nb, 2.0 * vs->s_stride + 1.0 + vs->v_stride / 64.0);
+    return nb * per;
+  }
+  const double kk = fmin(nb, double(topk_max));
+  return nb * kk - kk * (kk - 1) / 2;
+}
+
+// (batch, head) pairs of one launch: with a multiple of 8 pairs, the 8 XCDs
+// (round-robin workgroup dispatch) each get a fixed subset so that its L2
+// serves those heads, balanced by estimated work (greedy
+// longest-processing-time); otherwise plain order.
+static void order_heads(AttnParams& ap, const int* pairs, const double* cost, int n) {
+  ap.n_bh = n;
+  if (n % 8 != 0) {
+    for (int i = 0; i < n; ++i) ap.head_order[i] = int16_t(pairs[i]);
+    ap.xcd_heads = 0;
+    return;
+  }
+  const int per = n / 8;
+  int order[kMaxHeads];
+  for (int i = 0; i < n; ++i) order[i] = i;
+  for (int i = 1; i < n; ++i) {  // insertion sort, descending cost
+    const int x = order[i];
+    int j = i - 1;
+    while (j >= 0 && cost[order[j]] < cost[x]) {
+      order[j + 1] = order[j];
+      --j;
+    }
+    order[j + 1] = x;
+  }
+  double load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int fill[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = 0; i < n; ++i) {
+    int best = -1;
+    for (int x = 0; x < 8; ++x)
+      if (fill[x] < per && (best < 0 || load[x] < load[best])) best = x;
+    ap.head_order[best * per + fill[best]] = int16_t(pairs[order[i]]);
+    ++fill[best];
+    load[best] += cost[order[i]];
+  }
+  ap.xcd_heads = per;
+}
+
 static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
                                 const msa_tensor4* o, const msa_head_desc* heads, int32_t n_heads,
                                 const int32_t* idx, const int32_t* cnt, int32_t idx_slots,
-                                int32_t topk_max, void* workspace, size_t workspace_bytes,
-                                msa_stream_t stream, bool stage) {
+                                int32_t topk_max, const msa_vs_lists* vs, void* vs_workspace,
+                                size_t vs_workspace_bytes, void* workspace,
+                                size_t workspace_bytes, msa_stream_t stream, bool stage) {
   int st = check_qk(q, k);
   if (st != MSA_OK) return st;
   if (!v || !o || !v->data || !o->data || !heads) return MSA_E_NULL;
@@ -228,18 +320,46 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   if (n_heads != H || H > kMaxHeads) return MSA_E_HEADS;
   const int n_qb = int(cdiv(Sq, MSA_BLOCK));
   const int n_kb = int(cdiv(Sk, MSA_BLOCK));
+  const int kv_group = int(H / Hkv);
   bool any_block = false;
+  int n_vs = 0;
   for (int h = 0; h < n_heads; ++h) {
     const msa_head_desc& hd = heads[h];
-    if (hd.kind != MSA_KIND_DENSE && hd.kind != MSA_KIND_STREAM && hd.kind != MSA_KIND_BLOCK)
+    if (hd.kind != MSA_KIND_DENSE && hd.kind != MSA_KIND_STREAM && hd.kind != MSA_KIND_BLOCK &&
+        hd.kind != MSA_KIND_VS)
       return MSA_E_HEADS;
     if (!(hd.scale > 0.0f) || !isfinite(hd.scale)) return MSA_E_HEADS;
     if (hd.kind == MSA_KIND_BLOCK) {
       any_block = true;
       if (hd.slot < 0 || hd.slot >= idx_slots) return MSA_E_SLOTS;
     }
+    if (hd.kind == MSA_KIND_VS) ++n_vs;
   }
   if (any_block && (!idx || !cnt || topk_max < 1)) return MSA_E_SLOTS;
+  VsLayout vl;
+  int16_t slot_kvh[kMaxHeads];
+  if (n_vs) {
+    if (!vs || !vs->v_idx || !vs->v_cnt || !vs->s_idx || !vs->s_cnt) return MSA_E_SLOTS;
+    if (vs->n_slots < 1 || vs->n_slots > kMaxHeads || vs->v_stride < 1 ||
+        vs->v_stride > kVsMaxSeq || vs->s_stride < 1)
+      return MSA_E_SLOTS;
+    if (Sq != Sk || Sk > kVsMaxSeq) return MSA_E_SEQ;
+    if (B * H > kMaxHeads) return MSA_E_HEADS;
+    for (int s = 0; s < vs->n_slots; ++s) slot_kvh[s] = -1;
+    for (int h = 0; h < n_heads; ++h) {
+      if (heads[h].kind != MSA_KIND_VS) continue;
+      const int s = heads[h].slot;
+      if (s < 0 || s >= vs->n_slots) return MSA_E_SLOTS;
+      const int kvh = h / kv_group;
+      if (slot_kvh[s] >= 0 && slot_kvh[s] != kvh) return MSA_E_SLOTS;
+      slot_kvh[s] = int16_t(kvh);
+    }
+    for (int s = 0; s < vs->n_slots; ++s)
+      if (slot_kvh[s] < 0) slot_kvh[s] = 0;  // unused slot: any kv head
+    vl = vs_layout(B, vs->n_slots, Sk, vs->v_stride, D);
+    if (!vs_workspace || vs_workspace_bytes < vl.total) return MSA_E_WORKSPACE;
+    if ((reinterpret_cast<uintptr_t>(vs_workspace) & 255u) != 0) return MSA_E_ALIGN;
+  }
   const size_t need = msa_attention_workspace_bytes(B, Hkv, Sk, D);
   if (!workspace || workspace_bytes < need) return MSA_E_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
@@ -264,7 +384,7 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   ap.o_sb = o->stride[0]; ap.o_sh = o->stride[1]; ap.o_ss = o->stride[2];
   ap.batch = int(B);
   ap.heads = int(H);
-  ap.kv_group = int(H / Hkv);
+  ap.kv_group = kv_group;
   ap.s_q = int(Sq);
   ap.s_k = int(Sk);
   ap.n_qb = n_qb;
@@ -276,60 +396,101 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   ap.topk_max = topk_max;
   const double log2e = 1.4426950408889634;
   for (int h = 0; h < n_heads; ++h) {
-    ap.hd[h].kind = int16_t(heads[h].kind);
-    ap.hd[h].slot = int16_t(heads[h].kind == MSA_KIND_BLOCK ? heads[h].slot : 0);
+    const int kd = heads[h].kind;
+    ap.hd[h].kind = int16_t(kd);
+    ap.hd[h].slot = int16_t(kd == MSA_KIND_BLOCK || kd == MSA_KIND_VS ? heads[h].slot : 0);
     ap.hd[h].p1 = heads[h].p1;
     ap.hd[h].p2 = heads[h].p2;
     ap.hd[h].scale_log2 = float(double(heads[h].scale) * log2e);
   }
 
-  // Spread (batch, head) pairs over the 8 XCDs (round-robin workgroup
-  // dispatch) so each XCD's L2 serves a fixed head subset and the estimated
-  // work per XCD is balanced (greedy longest-processing-time assignment).
   const int BH = int(B * H);
-  if (BH % 8 == 0 && BH <= kMaxHeads) {
-    const int per = BH / 8;
-    double cost[kMaxHeads];
-    for (int hh = 0; hh < BH; ++hh) {
-      const msa_head_desc& hd = heads[hh % H];
-      const double nb = double(n_kb);
-      if (hd.kind == MSA_KIND_DENSE) cost[hh] = nb * (nb + 1) / 2;
-      else if (hd.kind == MSA_KIND_STREAM) {
-        const double band = fmin(nb, double(hd.p2) / 64.0 + 1.0);
-        const double sink = fmin(nb, ceil(fmax(double(hd.p1), 0.0) / 64.0));
-        cost[hh] = nb * (band + sink);
-      } else {
-        const double kk = fmin(nb, double(topk_max));
-        cost[hh] = nb * kk - kk * (kk - 1) / 2;
+  if (n_vs == 0) {
+    if (BH % 8 == 0 && BH <= kMaxHeads) {
+      int pairs[kMaxHeads];
+      double cost[kMaxHeads];
+      for (int i = 0; i < BH; ++i) {
+        pairs[i] = i;
+        cost[i] = head_cost(heads[i % H], n_kb, topk_max, vs);
       }
+      order_heads(ap, pairs, cost, BH);
+    } else {
+      ap.n_bh = 0;  // every pair, plain order (also for B * H > kMaxHeads)
+      ap.xcd_heads = 0;
     }
-    int order[kMaxHeads];
-    for (int i = 0; i < BH; ++i) order[i] = i;
-    for (int i = 1; i < BH; ++i) {  // insertion sort, descending cost
-      const int x = order[i];
-      int j = i - 1;
-      while (j >= 0 && cost[order[j]] < cost[x]) {
-        order[j + 1] = order[j];
-        --j;
-      }
-      order[j + 1] = x;
-    }
-    double load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int fill[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int i = 0; i < BH; ++i) {
-      int best = -1;
-      for (int x = 0; x < 8; ++x)
-        if (fill[x] < per && (best < 0 || load[x] < load[best])) best = x;
-      ap.head_order[best * per + fill[best]] = int16_t(order[i]);
-      ++fill[best];
-      load[best] += cost[order[i]];
-    }
-    ap.xcd_heads = per;
-  } else {
-    ap.xcd_heads = 0;
+    const hipError_t e = launch_attention(ap, q->dtype, o->dtype, D, hs);
+    return e == hipSuccess ? MSA_OK : int(e);
   }
 
-  const hipError_t e = launch_attention(ap, q->dtype, o->dtype, D, hs);
+  // vertical_and_slash heads: tile lists, gathered vertical columns, launch
+  unsigned char* vw = static_cast<unsigned char*>(vs_workspace);
+  VsBuildParams bp;
+  memset(&bp, 0, sizeof(bp));
+  bp.v_idx = vs->v_idx;
+  bp.v_cnt = vs->v_cnt;
+  bp.s_idx = vs->s_idx;
+  bp.s_cnt = vs->s_cnt;
+  bp.ids = reinterpret_cast<int32_t*>(vw + vl.ids);
+  bp.masks = reinterpret_cast<uint64_t*>(vw + vl.masks);
+  bp.cnt = reinterpret_cast<int32_t*>(vw + vl.cnt);
+  bp.v_stride = vs->v_stride;
+  bp.s_stride = vs->s_stride;
+  bp.cap = vl.cap;
+  bp.n_qb = n_qb;
+  bp.n_kb = n_kb;
+  bp.s_k = int(Sk);
+  hipError_t e = launch_vs_build(bp, int(B) * vs->n_slots, hs);
+  if (e != hipSuccess) return int(e);
+
+  StageParams gp;
+  memset(&gp, 0, sizeof(gp));
+  gp.k = k->data;
+  gp.v = v->data;
+  gp.k_sb = k->stride[0]; gp.k_sh = k->stride[1]; gp.k_ss = k->stride[2];
+  gp.v_sb = v->stride[0]; gp.v_sh = v->stride[1]; gp.v_ss = v->stride[2];
+  gp.kt = reinterpret_cast<uint16_t*>(vw + vl.gk);
+  gp.vt = reinterpret_cast<uint16_t*>(vw + vl.gv);
+  gp.batch = int(B);
+  gp.kv_heads = int(Hkv);
+  gp.s_k = int(Sk);
+  gp.s_pad = vl.nv_pad;
+  gp.rows = vs->v_idx;
+  gp.rows_cnt = vs->v_cnt;
+  gp.rows_stride = vs->v_stride;
+  gp.n_slots = vs->n_slots;
+  for (int s = 0; s < vs->n_slots; ++s) gp.slot_kvh[s] = slot_kvh[s];
+  e = launch_stage(gp, q->dtype, D, hs);
+  if (e != hipSuccess) return int(e);
+
+  int vs_pairs[kMaxHeads], other[kMaxHeads];
+  double vs_cost[kMaxHeads], other_cost[kMaxHeads];
+  int n_v = 0, n_o = 0;
+  for (int i = 0; i < BH; ++i) {
+    const msa_head_desc& hd = heads[i % H];
+    if (hd.kind == MSA_KIND_VS) {
+      vs_pairs[n_v] = i;
+      vs_cost[n_v++] = head_cost(hd, n_kb, topk_max, vs);
+    } else {
+      other[n_o] = i;
+      other_cost[n_o++] = head_cost(hd, n_kb, topk_max, vs);
+    }
+  }
+  AttnParams vp = ap;
+  vp.vs_ids = bp.ids;
+  vp.vs_masks = bp.masks;
+  vp.vs_cnt = bp.cnt;
+  vp.gkt = gp.kt;
+  vp.gvt = gp.vt;
+  vp.vs_slots = vs->n_slots;
+  vp.vs_cap = vl.cap;
+  vp.nv_pad = vl.nv_pad;
+  order_heads(vp, vs_pairs, vs_cost, n_v);
+  e = launch_attention_vs(vp, q->dtype, o->dtype, D, hs);
+  if (e != hipSuccess) return int(e);
+  if (n_o) {
+    order_heads(ap, other, other_cost, n_o);
+    e = launch_attention(ap, q->dtype, o->dtype, D, hs);
+  }
   return e == hipSuccess ? MSA_OK : int(e);
 }
 
@@ -339,7 +500,7 @@ int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_te
                         int32_t topk_max, void* workspace, size_t workspace_bytes,
                         msa_stream_t stream) {
   return layer_attention_impl(q, k, v, o, heads, n_heads, idx, cnt, idx_slots, topk_max,
-                              workspace, workspace_bytes, stream, true);
+                              nullptr, nullptr, 0, workspace, workspace_bytes, stream, true);
 }
 
 int msa_layer_attention_staged(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
@@ -348,7 +509,18 @@ int msa_layer_attention_staged(const msa_tensor4* q, const msa_tensor4* k, const
                                int32_t topk_max, void* workspace, size_t workspace_bytes,
                                msa_stream_t stream) {
   return layer_attention_impl(q, k, v, o, heads, n_heads, idx, cnt, idx_slots, topk_max,
-                              workspace, workspace_bytes, stream, false);
+                              nullptr, nullptr, 0, workspace, workspace_bytes, stream, false);
+}
+
+int msa_layer_attention_ex(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
+                           const msa_tensor4* o, const msa_head_desc* heads, int32_t n_heads,
+                           const int32_t* idx, const int32_t* cnt, int32_t idx_slots,
+                           int32_t topk_max, const msa_vs_lists* vs, void* vs_workspace,
+                           size_t vs_workspace_bytes, void* workspace, size_t workspace_bytes,
+                           int32_t stage, msa_stream_t stream) {
+  return layer_attention_impl(q, k, v, o, heads, n_heads, idx, cnt, idx_slots, topk_max, vs,
+                              vs_workspace, vs_workspace_bytes, workspace, workspace_bytes,
+                              stream, stage != 0);
 }
 
 

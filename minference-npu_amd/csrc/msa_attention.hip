@@ -43,6 +43,7 @@ namespace msa {
 constexpr int KIND_DENSE = 0;
 constexpr int KIND_STREAM = 1;
 constexpr int KIND_BLOCK = 2;
+constexpr int KIND_VS = 3;
 
 // ---------------------------------------------------------------------------
 // Per-layer staging of K and V into MFMA operand order, zero padded to
@@ -53,7 +54,9 @@ constexpr int KIND_BLOCK = 2;
 //     V[16 chunk + 8 (l >> 5) + e][32 db + (l & 31)]     (PV A operand, 32x32x16)
 // so a wave reads every operand as one contiguous 1 KB.  blockIdx.z = 1
 // stages K (a permutation of 16-byte granules), 0 stages V (a transpose
-// through LDS, converted to fp16 with saturation).
+// through LDS, converted to fp16 with saturation).  In gather mode the keys
+// of a slot are the listed rows (the vertical columns of a
+// vertical_and_slash head) instead of 0 .. s_k-1.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
@@ -62,8 +65,23 @@ __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
   constexpr int LP = D + 8;  // padded LDS row (halves)
   __shared__ __align__(16) uint16_t tile[kBlock * LP];
   const int j0 = blockIdx.x * kBlock;
-  const int bk = blockIdx.y;  // b * kv_heads + kvh
-  const int b = bk / P.kv_heads, kvh = bk - b * P.kv_heads;
+  const int bk = blockIdx.y;  // b * kv_heads + kvh (gather mode: b * n_slots + slot)
+  int b, kvh, rcnt = 0;
+  const int32_t* rows = nullptr;
+  if (P.rows) {
+    b = bk / P.n_slots;
+    kvh = P.slot_kvh[bk - b * P.n_slots];
+    rows = P.rows + int64_t(bk) * P.rows_stride;
+    rcnt = min(max(P.rows_cnt[bk], 0), P.rows_stride);
+  } else {
+    b = bk / P.kv_heads;
+    kvh = bk - b * P.kv_heads;
+  }
+  // source row of staged key j, -1 for a zero key
+  auto src_row = [&](int j) -> int {
+    if (rows) return j < rcnt ? min(max(rows[j], 0), P.s_k - 1) : -1;
+    return j < P.s_k ? j : -1;
+  };
   // the tile's 4 chunks are 64*D consecutive halves starting at key j0
   const int64_t dst0 = (int64_t(bk) * P.s_pad + j0) * D;
   if (blockIdx.z == 1) {
@@ -72,9 +90,9 @@ __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
       const int l = gi & 63;
       const int cks = gi >> 6;  // chunk * NDB + ks
       const int c = cks / NDB, ks = cks - c * NDB;
-      const int j = j0 + 16 * c + (l & 15);
-      const u32x4 x = j < P.s_k ? load16(src + int64_t(j) * P.k_ss + 32 * ks + 8 * (l >> 4))
-                                : zero_u32x4();
+      const int j = src_row(j0 + 16 * c + (l & 15));
+      const u32x4 x = j >= 0 ? load16(src + int64_t(j) * P.k_ss + 32 * ks + 8 * (l >> 4))
+                             : zero_u32x4();
       store16(P.kt + dst0 + gi * 8, x);
     }
     return;
@@ -82,9 +100,9 @@ __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
   const uint16_t* src = reinterpret_cast<const uint16_t*>(P.v) + b * P.v_sb + kvh * P.v_sh;
   for (int ci = threadIdx.x; ci < kBlock * KCH; ci += 256) {
     const int r = ci / KCH, c = ci - r * KCH;
-    const int j = j0 + r;
+    const int j = src_row(j0 + r);
     u32x4 out = zero_u32x4();
-    if (j < P.s_k) {
+    if (j >= 0) {
       const u32x4 in = load16(src + int64_t(j) * P.v_ss + c * 8);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -116,7 +134,7 @@ __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
 
 template <typename T, int D>
 static hipError_t launch_stage_t(const StageParams& p, hipStream_t st) {
-  dim3 grid(p.s_pad / kBlock, p.batch * p.kv_heads, 2);
+  dim3 grid(p.s_pad / kBlock, p.batch * (p.rows ? p.n_slots : p.kv_heads), 2);
   hipLaunchKernelGGL((stage_kernel<T, D>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
@@ -276,7 +294,9 @@ struct AttnShape {
   static constexpr int SLOT = (NO + 4) * 64;      // merge slot of one wave (floats)
 };
 
-template <typename T, bool OUT_F32, int D>
+// VS = false: stream_llm / block_sparse / dense heads; VS = true: the
+// vertical_and_slash heads of a layer (tile lists from vs_build_kernel).
+template <typename T, bool OUT_F32, int D, bool VS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D > 96 ? 1 : 2)))
 void attn_kernel(AttnParams P) {
   using S = AttnShape<D>;
@@ -293,7 +313,7 @@ void attn_kernel(AttnParams P) {
   // ---- work item.  Workgroups are dispatched round-robin over the 8 XCDs;
   // each XCD walks its own heads one at a time (query blocks longest-first),
   // so the K/V of the 8 heads in flight stay resident in L2 / Infinity Cache.
-  const int BH = P.batch * P.heads;
+  const int BH = P.n_bh ? P.n_bh : P.batch * P.heads;
   const int item = blockIdx.x;
   int hh, bq;
   if (P.xcd_heads) {
@@ -302,7 +322,7 @@ void attn_kernel(AttnParams P) {
     hh = P.head_order[(item & 7) * P.xcd_heads + r / P.n_qb];
   } else {
     bq = P.n_qb - 1 - item / BH;
-    hh = item % BH;
+    hh = P.n_bh ? int(P.head_order[item % BH]) : item % BH;
   }
   const int b = hh / P.heads;
   const int h = hh - b * P.heads;
@@ -325,7 +345,18 @@ void attn_kernel(AttnParams P) {
   seq.n_kb = P.n_kb;
   seq.list = nullptr;
   seq.any = reinterpret_cast<const int32_t*>(P.q);
-  if (kind == KIND_BLOCK) {
+  int64_t vs_base = 0;  // list row of a vertical_and_slash item
+  if constexpr (VS) {
+    // full tiles (no mask), then partial tiles, then gathered vertical tiles
+    // (ids n_kb + g), every entry with its key mask
+    vs_base = ((int64_t(b) * P.vs_slots + hd.slot) * P.n_qb + bq);
+    const int nf = P.vs_cnt[2 * vs_base];
+    const int nt = P.vs_cnt[2 * vs_base + 1];
+    vs_base *= P.vs_cap;
+    seq.list = P.vs_ids + vs_base;
+    seq.n_kb = P.n_kb + P.nv_pad / kBlock;
+    seq.set({0, nf, 0, 0, 0}, {nf, nt, 0, 0, 0}, 1);
+  } else if (kind == KIND_BLOCK) {
     // canonical list: ascending causal ids, so the boundary ids come last
     const int64_t base = (int64_t(b) * P.idx_slots + hd.slot) * P.n_qb + bq;
     const int cnt = max(0, min(P.cnt[base], P.topk_max));
@@ -354,6 +385,15 @@ void attn_kernel(AttnParams P) {
       const_cast<uint16_t*>(P.kt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(P.vt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
+  // gathered vertical operands of a vertical_and_slash slot (tiles n_kb + g)
+  __amdgpu_buffer_rsrc_t gkrs = krs, gvrs = vrs;
+  if constexpr (VS) {
+    const int64_t gb = (int64_t(b) * P.vs_slots + hd.slot) * P.nv_pad * D;
+    gkrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.gkt + gb), short(0),
+                                             P.nv_pad * D * 2, 0x00020000);
+    gvrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.gvt + gb), short(0),
+                                             P.nv_pad * D * 2, 0x00020000);
+  }
 
   // ---- Q as the B operand: lane (lc, lr) of group g, k-step ks holds
   // Q[q0 + 16g + lc][32ks + 8lr .. +7]
@@ -375,18 +415,30 @@ void attn_kernel(AttnParams P) {
   // operands, each MFMA operand as one contiguous 1 KB (lane l: 16 bytes).
   const uint32_t lane_off = 16u * lane;
   auto load_k = [&](int t, u32x4 (&kr)[NKS]) INLINE {
+    __amdgpu_buffer_rsrc_t rs = krs;
+    if constexpr (VS) {
+      const bool gat = t >= P.n_kb;
+      rs = gat ? gkrs : krs;
+      t = gat ? t - P.n_kb : t;
+    }
     const int soff = (4 * t + w) * S::CHUNK_BYTES;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
       kr[ks] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, lane_off, soff + 1024 * ks, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, soff + 1024 * ks, 0));
   };
   auto load_v = [&](int t, u32x4 (&vr)[NDB]) INLINE {
+    __amdgpu_buffer_rsrc_t rs = vrs;
+    if constexpr (VS) {
+      const bool gat = t >= P.n_kb;
+      rs = gat ? gvrs : vrs;
+      t = gat ? t - P.n_kb : t;
+    }
     const int soff = (4 * t + w) * S::CHUNK_BYTES;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
       vr[db] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, lane_off, soff + 1024 * db, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, soff + 1024 * db, 0));
   };
 
   f32x16 o[NDB][2];
@@ -417,9 +469,18 @@ void attn_kernel(AttnParams P) {
 #pragma unroll
       for (int gg = 0; gg < 2; ++gg) s[gg] = mfma_qk<T>(kr[ks], qb[2 * hf + gg][ks], s[gg]);
   };
-  // visible iff j <= key_hi and (j >= band_lo or j < sink_hi)
-  auto mask_half = [&](f32x4 (&s)[2], int hf, int t) INLINE {
+  // visible iff j <= key_hi and (j >= band_lo or j < sink_hi); for a
+  // vertical_and_slash tile: iff the key's bit is set in the tile's mask and
+  // (gathered tile, all keys in every row's past, or j <= key_hi)
+  auto mask_half = [&](f32x4 (&s)[2], int hf, int t, int p) INLINE {
     const int jb = t * kBlock + 16 * w + 4 * lr;
+    uint32_t bits = 0xfu;
+    bool past = false;
+    if constexpr (VS) {
+      const uint64_t mk = P.vs_masks[vs_base + p];
+      bits = uint32_t(mk >> (16 * w + 4 * lr)) & 0xfu;
+      past = t >= P.n_kb;
+    }
 #pragma unroll
     for (int gg = 0; gg < 2; ++gg) {
       const int ar = arow0 + 16 * (2 * hf + gg);
@@ -428,7 +489,12 @@ void attn_kernel(AttnParams P) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = jb + i;
-        const bool vis = (j <= key_hi) & ((j >= band_lo) | (j < sink_hi));
+        bool vis;
+        if constexpr (VS) {
+          vis = ((bits >> i) & 1u) && (past || j <= key_hi);
+        } else {
+          vis = (j <= key_hi) & ((j >= band_lo) | (j < sink_hi));
+        }
         s[gg][i] = vis ? s[gg][i] : -__builtin_inff();
       }
     }
@@ -448,9 +514,10 @@ void attn_kernel(AttnParams P) {
   };
   // Rare path: recompute the half's scores, raise the running max to the
   // row max, rescale the half's O and row sums, and redo the exponentials.
-  auto rescale_half = [&](const u32x4 (&kr)[NKS], f32x4 (&s)[2], int hf, int t, bool mt) INLINE {
+  auto rescale_half = [&](const u32x4 (&kr)[NKS], f32x4 (&s)[2], int hf, int t, int p,
+                          bool mt) INLINE {
     qk_half(kr, hf, s);
-    if (mt) mask_half(s, hf, t);
+    if (mt) mask_half(s, hf, t, p);
     float m0 = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
     float m1 = fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3]));
     swap32(m0, m1);  // lane rows (R0, R2) and (R1, R3) of each group
@@ -526,11 +593,11 @@ void attn_kernel(AttnParams P) {
     f32x4 sa[2], sb[2];
     qk_half(kr, 0, sa);
     qk_half(kr, 1, sb);
-    if constexpr (MT) mask_half(sa, 0, tcur);
-    if (exp_half(sa, 0)) rescale_half(kr, sa, 0, tcur, MT);
+    if constexpr (MT) mask_half(sa, 0, tcur, p);
+    if (exp_half(sa, 0)) rescale_half(kr, sa, 0, tcur, p, MT);
     pv_half(sa, 0, vr);
-    if constexpr (MT) mask_half(sb, 1, tcur);
-    if (exp_half(sb, 1)) rescale_half(kr, sb, 1, tcur, MT);
+    if constexpr (MT) mask_half(sb, 1, tcur, p);
+    if (exp_half(sb, 1)) rescale_half(kr, sb, 1, tcur, p, MT);
     load_k(tn, kr);
     pv_half(sb, 1, vr);
     load_v(tn, vr);
@@ -622,26 +689,34 @@ void attn_kernel(AttnParams P) {
   }
 }
 
-template <typename T, bool OUT_F32, int D>
+template <typename T, bool OUT_F32, int D, bool VS>
 static hipError_t launch_attn_t(const AttnParams& p, hipStream_t st) {
-  const int64_t items = int64_t(p.n_qb) * p.batch * p.heads;
-  hipLaunchKernelGGL((attn_kernel<T, OUT_F32, D>), dim3(uint32_t(items)), dim3(256), 0, st, p);
+  const int64_t items = int64_t(p.n_qb) * (p.n_bh ? p.n_bh : p.batch * p.heads);
+  hipLaunchKernelGGL((attn_kernel<T, OUT_F32, D, VS>), dim3(uint32_t(items)), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
-template <typename T, bool OUT_F32>
+template <typename T, bool OUT_F32, bool VS>
 static hipError_t launch_attn_d(const AttnParams& p, int D, hipStream_t st) {
-  if (D == 64) return launch_attn_t<T, OUT_F32, 64>(p, st);
-  if (D == 96) return launch_attn_t<T, OUT_F32, 96>(p, st);
-  return launch_attn_t<T, OUT_F32, 128>(p, st);
+  if (D == 64) return launch_attn_t<T, OUT_F32, 64, VS>(p, st);
+  if (D == 96) return launch_attn_t<T, OUT_F32, 96, VS>(p, st);
+  return launch_attn_t<T, OUT_F32, 128, VS>(p, st);
 }
 
 hipError_t launch_attention(const AttnParams& p, int dtype, int out_dtype, int D,
                             hipStream_t st) {
   const bool f32 = out_dtype == 3;
   if (dtype == Bf16::id)
-    return f32 ? launch_attn_d<Bf16, true>(p, D, st) : launch_attn_d<Bf16, false>(p, D, st);
-  return f32 ? launch_attn_d<F16, true>(p, D, st) : launch_attn_d<F16, false>(p, D, st);
+    return f32 ? launch_attn_d<Bf16, true, false>(p, D, st) : launch_attn_d<Bf16, false, false>(p, D, st);
+  return f32 ? launch_attn_d<F16, true, false>(p, D, st) : launch_attn_d<F16, false, false>(p, D, st);
+}
+
+hipError_t launch_attention_vs(const AttnParams& p, int dtype, int out_dtype, int D,
+                               hipStream_t st) {
+  const bool f32 = out_dtype == 3;
+  if (dtype == Bf16::id)
+    return f32 ? launch_attn_d<Bf16, true, true>(p, D, st) : launch_attn_d<Bf16, false, true>(p, D, st);
+  return f32 ? launch_attn_d<F16, true, true>(p, D, st) : launch_attn_d<F16, false, true>(p, D, st);
 }
 
 }  // namespace msa

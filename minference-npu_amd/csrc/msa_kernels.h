@@ -53,10 +53,41 @@ struct AttnParams {
   const int32_t* idx;
   const int32_t* cnt;
   int idx_slots, topk_max;
-  int xcd_heads;  // 0: plain order; else heads per XCD (order taken from head_order)
-  int16_t head_order[kMaxHeads];  // batch*heads <= kMaxHeads when xcd_heads != 0
+  // (batch, head) pairs of this launch: n_bh > 0 lists them in head_order
+  // (b * heads + h); n_bh == 0 takes every pair in plain order.
+  // xcd_heads != 0: n_bh = 8 * xcd_heads and head_order holds each XCD's
+  // pairs consecutively.
+  int n_bh;
+  int xcd_heads;
+  // vertical_and_slash launch: per (b * vs_slots + slot, query block) a list
+  // of vs_cap tile ids (gathered vertical tiles as n_kb + g), one 64-bit key
+  // mask per entry, and (unmasked prefix, total) counts; gathered vertical
+  // operands per slot in stage_kernel's layout, nv_pad keys each.
+  const int32_t* vs_ids;
+  const uint64_t* vs_masks;
+  const int32_t* vs_cnt;
+  const uint16_t* gkt;
+  const uint16_t* gvt;
+  int vs_slots, vs_cap, nv_pad;
+  int16_t head_order[kMaxHeads];
   HeadArg hd[kMaxHeads];
 };
+
+// vertical_and_slash tile lists of one layer (vs_build_kernel).
+struct VsBuildParams {
+  const int32_t* v_idx;  // [batch*slots][v_stride]: vertical columns, ascending, distinct
+  const int32_t* v_cnt;  // [batch*slots]
+  const int32_t* s_idx;  // [batch*slots][s_stride]: slash offsets, any order
+  const int32_t* s_cnt;  // [batch*slots]
+  int32_t* ids;          // outputs in the AttnParams vs_* layout
+  uint64_t* masks;
+  int32_t* cnt;
+  int v_stride, s_stride, cap, n_qb, n_kb, s_k;
+};
+
+// Longest key axis of a vertical_and_slash head (the tile-list builder keeps
+// one 64-bit mask per key tile in LDS).
+constexpr int kVsMaxSeq = 131072;
 
 struct StageParams {
   const void* k;
@@ -66,6 +97,14 @@ struct StageParams {
   uint16_t* kt;  // [batch*kv_heads][s_pad/16][D/32][64][8] QK A operands (input dtype)
   uint16_t* vt;  // [batch*kv_heads][s_pad/16][D/32][64][8] PV A operands (fp16)
   int batch, kv_heads, s_k, s_pad;
+  // Gather mode (rows != nullptr): blockIdx.y = b * n_slots + slot; staged key
+  // j of that slot is row rows[(b * n_slots + slot) * rows_stride + j] of kv
+  // head slot_kvh[slot] for j < rows_cnt[b * n_slots + slot], zero after;
+  // s_pad keys per slot.
+  const int32_t* rows;
+  const int32_t* rows_cnt;
+  int rows_stride, n_slots;
+  int16_t slot_kvh[kMaxHeads];
 };
 
 struct DecodeParams {
@@ -95,5 +134,8 @@ hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st);
 hipError_t launch_decode(const DecodeParams& p, int dtype, int out_dtype, int D, hipStream_t st);
 hipError_t launch_attention(const AttnParams& p, int dtype, int out_dtype, int D,
                             hipStream_t st);
+hipError_t launch_attention_vs(const AttnParams& p, int dtype, int out_dtype, int D,
+                               hipStream_t st);
+hipError_t launch_vs_build(const VsBuildParams& p, int n_bs, hipStream_t st);
 
 }  // namespace msa

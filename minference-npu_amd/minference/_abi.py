@@ -38,10 +38,12 @@ MSA_DTYPE_FP32 = 3
 MSA_KIND_DENSE = 0
 MSA_KIND_STREAM = 1
 MSA_KIND_BLOCK = 2
+MSA_KIND_VS = 3
+MSA_VS_MAX_SEQ = 131072
 
 MSA_MAX_HEADS = 128
 MSA_BLOCK = 64
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _DTYPE_CODE = {
     torch.bfloat16: MSA_DTYPE_BF16,
@@ -61,6 +63,8 @@ EXPORTED_SYMBOLS = (
     "msa_layer_attention_staged",
     "msa_decode_workspace_bytes",
     "msa_decode_attention",
+    "msa_vs_workspace_bytes",
+    "msa_layer_attention_ex",
 )
 
 
@@ -81,6 +85,19 @@ class MsaHeadDesc(ctypes.Structure):
         ("p2", ctypes.c_int32),
         ("slot", ctypes.c_int32),
         ("scale", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class MsaVsLists(ctypes.Structure):
+    _fields_ = [
+        ("v_idx", ctypes.c_void_p),
+        ("v_cnt", ctypes.c_void_p),
+        ("s_idx", ctypes.c_void_p),
+        ("s_cnt", ctypes.c_void_p),
+        ("n_slots", ctypes.c_int32),
+        ("v_stride", ctypes.c_int32),
+        ("s_stride", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
     ]
 
@@ -161,6 +178,19 @@ def load_library() -> ctypes.CDLL:
             ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
             ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
             ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.msa_vs_workspace_bytes.restype = ctypes.c_size_t
+        lib.msa_vs_workspace_bytes.argtypes = [
+            ctypes.c_int64, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+        ]
+        lib.msa_layer_attention_ex.restype = ctypes.c_int
+        lib.msa_layer_attention_ex.argtypes = [
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.POINTER(MsaHeadDesc), ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+            ctypes.POINTER(MsaVsLists), ctypes.c_void_p, ctypes.c_size_t,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_void_p,
         ]
         ver = lib.msa_abi_version()
         if ver != ABI_VERSION:
@@ -297,6 +327,10 @@ def stage_kv(k: torch.Tensor, v: torch.Tensor, ws: torch.Tensor) -> None:
                                       ws.numel(), current_stream_handle(v.device)))
 
 
+def vs_workspace_bytes(batch: int, n_slots: int, s_k: int, v_stride: int, head_dim: int) -> int:
+    return int(load_library().msa_vs_workspace_bytes(batch, n_slots, s_k, v_stride, head_dim))
+
+
 def layer_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -309,10 +343,15 @@ def layer_attention(
     topk_max: int = 0,
     ws: Optional[torch.Tensor] = None,
     staged: bool = False,
+    vs: Optional[tuple] = None,
+    vs_ws: Optional[torch.Tensor] = None,
 ) -> None:
     """Launch msa_layer_attention (or, with ``staged=True``,
     msa_layer_attention_staged reading the K and V already staged in ``ws``).
-    ``heads`` = [(kind, p1, p2, slot, scale)] * H."""
+    ``heads`` = [(kind, p1, p2, slot, scale)] * H.  With vertical_and_slash
+    heads, ``vs`` = (v_idx [B,slots,nv], v_cnt [B,slots], s_idx [B,slots,ns],
+    s_cnt [B,slots]) int32 contiguous device tensors and the call goes to
+    msa_layer_attention_ex."""
     lib = load_library()
     n = len(heads)
     arr = head_descs(heads)
@@ -321,14 +360,37 @@ def layer_attention(
         raise ValueError("staged attention needs the workspace filled by stage_kv")
     if ws is None or ws.numel() < need:
         ws = workspace(need, q.device)
+    for t in (idx, cnt):
+        if t is not None and (t.dtype != torch.int32 or not t.is_contiguous()
+                              or t.device != q.device):
+            raise ValueError("block ids / counts must be contiguous int32 on q's device")
     qd, kd, vd, od = tensor4(q), tensor4(k), tensor4(v), tensor4(out)
+    idx_p = idx.data_ptr() if idx is not None else None
+    cnt_p = cnt.data_ptr() if cnt is not None else None
+    stream = current_stream_handle(q.device)
+    if vs is not None:
+        v_idx, v_cnt, s_idx, s_cnt = vs
+        for t in vs:
+            if t.dtype != torch.int32 or not t.is_contiguous() or t.device != q.device:
+                raise ValueError("vertical_and_slash lists must be contiguous int32 on q's device")
+        lists = MsaVsLists(v_idx.data_ptr(), v_cnt.data_ptr(), s_idx.data_ptr(), s_cnt.data_ptr(),
+                           int(v_idx.shape[1]), int(v_idx.shape[2]), int(s_idx.shape[2]), 0)
+        vneed = vs_workspace_bytes(q.shape[0], v_idx.shape[1], k.shape[2], v_idx.shape[2],
+                                   q.shape[3])
+        if vs_ws is None or vs_ws.numel() < vneed:
+            vs_ws = workspace(vneed, q.device)
+        st = lib.msa_layer_attention_ex(
+            ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ctypes.byref(od), arr, n,
+            idx_p, cnt_p, int(idx_slots), int(topk_max), ctypes.byref(lists),
+            vs_ws.data_ptr(), vs_ws.numel(), ws.data_ptr(), ws.numel(), 0 if staged else 1,
+            stream)
+        check(st)
+        return
     fn = lib.msa_layer_attention_staged if staged else lib.msa_layer_attention
     st = fn(
         ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ctypes.byref(od),
-        arr, n,
-        idx.data_ptr() if idx is not None else None,
-        cnt.data_ptr() if cnt is not None else None,
+        arr, n, idx_p, cnt_p,
         int(idx_slots), int(topk_max), ws.data_ptr(), ws.numel(),
-        current_stream_handle(q.device),
+        stream,
     )
     check(st)

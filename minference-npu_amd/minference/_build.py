@@ -18,7 +18,7 @@ CSRC_DIR = os.path.join(os.path.dirname(PKG_DIR), "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmsa.so")
 
-SOURCES = ("msa_abi.hip", "msa_estimator.hip", "msa_attention.hip", "msa_decode.hip")
+SOURCES = ("msa_abi.hip", "msa_estimator.hip", "msa_attention.hip", "msa_decode.hip", "msa_vs.hip")
 
 HIPCC_FLAGS = (
     "--offload-arch=gfx950",
