@@ -185,6 +185,34 @@ typedef struct msa_vs_lists {
   int32_t reserved;
 } msa_vs_lists;
 
+/* Bytes of workspace msa_vs_estimate needs (last-rows scores, row
+ * statistics, column and diagonal sums). */
+size_t msa_vs_estimate_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s,
+                                       int32_t head_dim);
+
+/* vertical_and_slash estimator for the vertical_and_slash heads of a layer
+ * (one call for all of them).  Replaces the index estimation of
+ * _vertical_and_slash_kernel, minference/modules/minference_forward.py:
+ * 140-165: scores of the last min(64, S) query rows in the input dtype,
+ * divided by sqrt(D) and rounded again, causal within the last rows, fp64
+ * softmax, column sums (first 30 forced) and diagonal sums (last 100
+ * forced), top-k with ties to the lower index.
+ *   slot_heads[s] (host) = head of q for slot s
+ *   slot_vsize[s], slot_ssize[s] (host) = vertical / slash counts, already
+ *     clamped as the reference does (min(S, max(v, 30)), min(S, max(s, 50)));
+ *     1 <= size <= v_stride / s_stride
+ *   v_idx [B][n_slots][v_stride], v_cnt [B][n_slots] (device): columns
+ *     ascending, count = slot_vsize
+ *   s_idx [B][n_slots][s_stride], s_cnt [B][n_slots] (device): slash offsets
+ *     S - 1 - t descending, count = slot_ssize
+ * These are exactly the msa_vs_lists msa_layer_attention_ex takes.  Needs
+ * S_q == S_k <= MSA_VS_MAX_SEQ. */
+int msa_vs_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t* slot_heads,
+                    const int32_t* slot_vsize, const int32_t* slot_ssize, int32_t n_slots,
+                    int32_t* v_idx, int32_t* v_cnt, int32_t v_stride, int32_t* s_idx,
+                    int32_t* s_cnt, int32_t s_stride, void* workspace, size_t workspace_bytes,
+                    msa_stream_t stream);
+
 /* Bytes of the vertical_and_slash workspace of msa_layer_attention_ex: the
  * per-(slot, query block) tile lists with their key masks, and the vertical
  * columns' K and V staged contiguously per slot. */

@@ -71,7 +71,7 @@ const char* msa_status_str(int status) {
     case MSA_E_HEADS: return "bad head count, head index or head kind";
     case MSA_E_WORKSPACE: return "workspace missing or too small";
     case MSA_E_SEQ: return "sequence lengths must satisfy 0 < S_q <= S_k <= 2^20";
-    case MSA_E_SLOTS: return "block_sparse head without a valid index slot or idx/cnt buffers";
+    case MSA_E_SLOTS: return "sparse head without a valid index slot, or bad idx/cnt or vertical_and_slash lists";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
@@ -236,6 +236,94 @@ static VsLayout vs_layout(int64_t B, int64_t n_slots, int64_t s_k, int64_t v_str
   off = up(off + size_t(B * n_slots) * L.nv_pad * D * 2);
   L.total = off;
   return L;
+}
+
+// vertical_and_slash estimator workspace: scores, row max, row sums,
+// column sums, diagonal sums.
+struct VsEstLayout {
+  size_t x, rmax, rsum, vert, slash, total;
+};
+
+static VsEstLayout vs_est_layout(int64_t B, int64_t n_slots, int64_t s) {
+  VsEstLayout L;
+  const int64_t s_pad = cdiv(s, MSA_BLOCK) * MSA_BLOCK;
+  const int64_t bs = B * n_slots;
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  size_t off = 0;
+  L.x = off;
+  off = up(off + size_t(bs) * MSA_BLOCK * s_pad * 2);
+  L.rmax = off;
+  off = up(off + size_t(bs) * MSA_BLOCK * 4);
+  L.rsum = off;
+  off = up(off + size_t(bs) * MSA_BLOCK * 8);
+  L.vert = off;
+  off = up(off + size_t(bs) * s * 4);
+  L.slash = off;
+  off = up(off + size_t(bs) * s * 4);
+  L.total = off;
+  return L;
+}
+
+size_t msa_vs_estimate_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s,
+                                       int32_t head_dim) {
+  if (batch <= 0 || n_slots <= 0 || s <= 0 || head_dim <= 0) return 0;
+  return vs_est_layout(batch, n_slots, s).total;
+}
+
+int msa_vs_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t* slot_heads,
+                    const int32_t* slot_vsize, const int32_t* slot_ssize, int32_t n_slots,
+                    int32_t* v_idx, int32_t* v_cnt, int32_t v_stride, int32_t* s_idx,
+                    int32_t* s_cnt, int32_t s_stride, void* workspace, size_t workspace_bytes,
+                    msa_stream_t stream) {
+  int st = check_qk(q, k);
+  if (st != MSA_OK) return st;
+  if (!slot_heads || !slot_vsize || !slot_ssize || !v_idx || !v_cnt || !s_idx || !s_cnt)
+    return MSA_E_NULL;
+  const int64_t B = q->size[0], H = q->size[1], S = q->size[2];
+  if (k->size[2] != S || S > kVsMaxSeq) return MSA_E_SEQ;
+  if (n_slots < 1 || n_slots > kMaxHeads || B * n_slots > 65535) return MSA_E_SLOTS;
+  if (v_stride < 1 || s_stride < 1) return MSA_E_SLOTS;
+  for (int s = 0; s < n_slots; ++s) {
+    if (slot_heads[s] < 0 || slot_heads[s] >= H) return MSA_E_HEADS;
+    if (slot_vsize[s] < 1 || slot_vsize[s] > S || slot_vsize[s] > v_stride) return MSA_E_TOPK;
+    if (slot_ssize[s] < 1 || slot_ssize[s] > S || slot_ssize[s] > s_stride) return MSA_E_TOPK;
+  }
+  const VsEstLayout L = vs_est_layout(B, n_slots, S);
+  if (!workspace || workspace_bytes < L.total) return MSA_E_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
+  unsigned char* w = static_cast<unsigned char*>(workspace);
+  VsEstParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = q->data;
+  p.k = k->data;
+  p.q_sb = q->stride[0]; p.q_sh = q->stride[1]; p.q_ss = q->stride[2];
+  p.k_sb = k->stride[0]; p.k_sh = k->stride[1]; p.k_ss = k->stride[2];
+  p.batch = int(B);
+  p.kv_group = int(H / k->size[1]);
+  p.s = int(S);
+  p.n_rows = int(std::min<int64_t>(MSA_BLOCK, S));
+  p.n_slots = n_slots;
+  p.s_pad = int(cdiv(S, MSA_BLOCK) * MSA_BLOCK);
+  p.sqrt_d = float(std::sqrt(double(q->size[3])));
+  p.x = reinterpret_cast<uint16_t*>(w + L.x);
+  p.rmax = reinterpret_cast<float*>(w + L.rmax);
+  p.rsum = reinterpret_cast<double*>(w + L.rsum);
+  p.vert = reinterpret_cast<float*>(w + L.vert);
+  p.slash = reinterpret_cast<float*>(w + L.slash);
+  p.v_idx = v_idx;
+  p.v_cnt = v_cnt;
+  p.s_idx = s_idx;
+  p.s_cnt = s_cnt;
+  p.v_stride = v_stride;
+  p.s_stride = s_stride;
+  for (int s = 0; s < n_slots; ++s) {
+    p.slot_heads[s] = int16_t(slot_heads[s]);
+    p.slot_vsize[s] = slot_vsize[s];
+    p.slot_ssize[s] = slot_ssize[s];
+  }
+  const hipError_t e =
+      launch_vs_estimate(p, q->dtype, int(q->size[3]), reinterpret_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSA_OK : int(e);
 }
 
 size_t msa_vs_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_k, int32_t v_stride,

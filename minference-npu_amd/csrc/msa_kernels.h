@@ -85,6 +85,30 @@ struct VsBuildParams {
   int v_stride, s_stride, cap, n_qb, n_kb, s_k;
 };
 
+// vertical_and_slash estimator of a layer (vs_*_kernel): slot s is head
+// slot_heads[s]; S_q == S_k == s.
+struct VsEstParams {
+  const void* q;
+  const void* k;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int batch, kv_group, s, n_rows, n_slots, s_pad;
+  float sqrt_d;       // fp32(sqrt(D)), the divisor of the scores
+  uint16_t* x;        // [batch*slots][64][s_pad]: scores in the input dtype, -inf masked
+  float* rmax;        // [batch*slots][64]
+  double* rsum;       // [batch*slots][64]
+  float* vert;        // [batch*slots][s]
+  float* slash;       // [batch*slots][s]
+  int32_t* v_idx;     // [batch*slots][v_stride]
+  int32_t* v_cnt;     // [batch*slots]
+  int32_t* s_idx;     // [batch*slots][s_stride]
+  int32_t* s_cnt;     // [batch*slots]
+  int v_stride, s_stride;
+  int16_t slot_heads[kMaxHeads];
+  int32_t slot_vsize[kMaxHeads];
+  int32_t slot_ssize[kMaxHeads];
+};
+
 // Longest key axis of a vertical_and_slash head (the tile-list builder keeps
 // one 64-bit mask per key tile in LDS).
 constexpr int kVsMaxSeq = 131072;
@@ -137,5 +161,6 @@ hipError_t launch_attention(const AttnParams& p, int dtype, int out_dtype, int D
 hipError_t launch_attention_vs(const AttnParams& p, int dtype, int out_dtype, int D,
                                hipStream_t st);
 hipError_t launch_vs_build(const VsBuildParams& p, int n_bs, hipStream_t st);
+hipError_t launch_vs_estimate(const VsEstParams& p, int dtype, int D, hipStream_t st);
 
 }  // namespace msa

@@ -65,6 +65,8 @@ EXPORTED_SYMBOLS = (
     "msa_decode_attention",
     "msa_vs_workspace_bytes",
     "msa_layer_attention_ex",
+    "msa_vs_estimate_workspace_bytes",
+    "msa_vs_estimate",
 )
 
 
@@ -178,6 +180,18 @@ def load_library() -> ctypes.CDLL:
             ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
             ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
             ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.msa_vs_estimate_workspace_bytes.restype = ctypes.c_size_t
+        lib.msa_vs_estimate_workspace_bytes.argtypes = [
+            ctypes.c_int64, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+        ]
+        lib.msa_vs_estimate.restype = ctypes.c_int
+        lib.msa_vs_estimate.argtypes = [
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
         lib.msa_vs_workspace_bytes.restype = ctypes.c_size_t
         lib.msa_vs_workspace_bytes.argtypes = [
@@ -325,6 +339,35 @@ def stage_kv(k: torch.Tensor, v: torch.Tensor, ws: torch.Tensor) -> None:
     kd, vd = tensor4(k), tensor4(v)
     check(load_library().msa_stage_kv(ctypes.byref(kd), ctypes.byref(vd), ws.data_ptr(),
                                       ws.numel(), current_stream_handle(v.device)))
+
+
+def vs_estimate_workspace_bytes(batch: int, n_slots: int, s: int, head_dim: int) -> int:
+    return int(load_library().msa_vs_estimate_workspace_bytes(batch, n_slots, s, head_dim))
+
+
+def vs_estimate(q: torch.Tensor, k: torch.Tensor, slot_heads: Sequence[int],
+                slot_vsize: Sequence[int], slot_ssize: Sequence[int], v_idx: torch.Tensor,
+                v_cnt: torch.Tensor, s_idx: torch.Tensor, s_cnt: torch.Tensor,
+                ws: Optional[torch.Tensor] = None) -> None:
+    """Launch msa_vs_estimate on the current stream: v_idx [B,slots,v_stride],
+    s_idx [B,slots,s_stride], v_cnt / s_cnt [B,slots], int32 contiguous."""
+    lib = load_library()
+    n = len(slot_heads)
+    for t in (v_idx, v_cnt, s_idx, s_cnt):
+        if t.dtype != torch.int32 or not t.is_contiguous() or t.device != q.device:
+            raise ValueError("vertical_and_slash lists must be contiguous int32 on q's device")
+    heads_arr = (ctypes.c_int32 * max(n, 1))(*[int(h) for h in slot_heads])
+    v_arr = (ctypes.c_int32 * max(n, 1))(*[int(x) for x in slot_vsize])
+    s_arr = (ctypes.c_int32 * max(n, 1))(*[int(x) for x in slot_ssize])
+    need = vs_estimate_workspace_bytes(q.shape[0], n, q.shape[2], q.shape[3])
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, q.device)
+    qd, kd = tensor4(q), tensor4(k)
+    check(lib.msa_vs_estimate(
+        ctypes.byref(qd), ctypes.byref(kd), heads_arr, v_arr, s_arr, n,
+        v_idx.data_ptr(), v_cnt.data_ptr(), int(v_idx.shape[-1]),
+        s_idx.data_ptr(), s_cnt.data_ptr(), int(s_idx.shape[-1]),
+        ws.data_ptr(), ws.numel(), current_stream_handle(q.device)))
 
 
 def vs_workspace_bytes(batch: int, n_slots: int, s_k: int, v_stride: int, head_dim: int) -> int:

@@ -5,9 +5,10 @@ Drop-in for MInference-NPU/minference/modules/minference_forward.py:
   minference_forward          :258-502  (the patched forward)
 The reference groups heads by (type, params) and runs gather -> op -> scatter
 per group (:398-487).  Here the layer's heads become a descriptor table
-(LayerPlan); the block_sparse heads share one estimator launch and all heads
-share one attention launch that writes the output in [B, S, H, D] order, so
-the o_proj input needs no transpose copy.
+(LayerPlan); the block_sparse heads share one estimator launch, the
+vertical_and_slash heads another, and one library call runs the attention of
+every head (vertical_and_slash heads in their own kernel launch), writing the
+output in [B, S, H, D] order, so the o_proj input needs no transpose copy.
 
 Written against the installed transformers (5.x): the attention module gets
 ``position_embeddings`` from the model and returns a 2-tuple.
@@ -26,6 +27,7 @@ import torch
 
 from .. import _abi
 from ..ops.common import dense_scale, sparse_scale
+from ..ops.vertical_slash_kernel import vs_sizes
 
 __all__ = [
     "DEFAULT_PATTERN",
@@ -65,7 +67,9 @@ class LayerPlan:
     """Head descriptor table of one layer for a given K length.
 
     heads[h] = (kind, p1, p2, slot, scale) as passed to msa_layer_attention;
-    block_heads[s] / block_topk[s] = head and clamped top-k of estimator slot s.
+    block_heads[s] / block_topk[s] = head and clamped top-k of estimator slot s;
+    vs_heads[s] / vs_counts[s] = head and clamped (vertical, slash) counts of
+    vertical_and_slash slot s.
     """
 
     heads: Tuple[tuple, ...]
@@ -73,6 +77,8 @@ class LayerPlan:
     block_topk: Tuple[int, ...]
     topk_max: int
     all_dense: bool
+    vs_heads: Tuple[int, ...] = ()
+    vs_counts: Tuple[Tuple[int, int], ...] = ()
 
 
 def build_layer_plan(patterns: Dict[int, Sequence], n_heads: int, head_dim: int,
@@ -83,9 +89,12 @@ def build_layer_plan(patterns: Dict[int, Sequence], n_heads: int, head_dim: int,
     * ``block_sparse``: p1 = top-k key blocks, clamped to [1, n_k_blocks],
                         scale (padded D)**-0.5 (selector and attention)
     * ``dense``       : causal dense, scale 1/sqrt(D)
-    * ``vertical_and_slash`` (also the default for a missing head) is not part
-      of this build and raises NotImplementedError; unknown types raise
-      ValueError as in the reference (:416-419).
+    * ``vertical_and_slash`` (also the default for a missing head, :229-231):
+                        p1 = vertical count, p2 = slash count, clamped to
+                        min(S, max(p1, 30)) / min(S, max(p2, 50)) (:146-147);
+                        estimator scale 1/sqrt(D), attention scale (padded
+                        D)**-0.5 (vertical_slash_kernel_npu.py:581-587)
+    Unknown types raise ValueError as in the reference (:416-419).
     """
     n_kb = max(1, math.ceil(s_k / _abi.MSA_BLOCK))
     s_sparse = sparse_scale(head_dim)
@@ -93,6 +102,8 @@ def build_layer_plan(patterns: Dict[int, Sequence], n_heads: int, head_dim: int,
     heads: List[tuple] = []
     block_heads: List[int] = []
     block_topk: List[int] = []
+    vs_heads: List[int] = []
+    vs_counts: List[Tuple[int, int]] = []
     for h in range(n_heads):
         rec = patterns.get(h, DEFAULT_PATTERN)
         ty, p1, p2 = rec[0], rec[1], rec[2]
@@ -106,10 +117,10 @@ def build_layer_plan(patterns: Dict[int, Sequence], n_heads: int, head_dim: int,
         elif ty == "dense":
             heads.append((_abi.MSA_KIND_DENSE, 0, 0, -1, s_dense))
         elif ty == "vertical_and_slash":
-            raise NotImplementedError(
-                f"pattern 'vertical_and_slash' (layer={layer_idx} head={h}) is not part of "
-                "the MI355X build; use stream_llm / block_sparse / dense patterns"
-            )
+            nv, ns = vs_sizes(s_k, p1, p2)
+            heads.append((_abi.MSA_KIND_VS, nv, ns, len(vs_heads), s_sparse))
+            vs_heads.append(h)
+            vs_counts.append((nv, ns))
         else:
             raise ValueError(f"unknown best_pattern type {ty!r} (layer={layer_idx} head={h})")
     return LayerPlan(
@@ -118,6 +129,8 @@ def build_layer_plan(patterns: Dict[int, Sequence], n_heads: int, head_dim: int,
         block_topk=tuple(block_topk),
         topk_max=max(block_topk) if block_topk else 0,
         all_dense=all(hd[0] == _abi.MSA_KIND_DENSE for hd in heads),
+        vs_heads=tuple(vs_heads),
+        vs_counts=tuple(vs_counts),
     )
 
 
@@ -129,15 +142,48 @@ def dense_plan(n_heads: int, head_dim: int, scale: Optional[float] = None) -> La
     )
 
 
+def _vs_lists(q: torch.Tensor, k: torch.Tensor, plan: LayerPlan):
+    """Estimator launch for the vertical_and_slash heads: (v_idx, v_cnt, s_idx,
+    s_cnt) for msa_layer_attention_ex."""
+    assert q.shape[2] == k.shape[2], (
+        "vertical_and_slash heads need S_q == S_k (full prefill); got "
+        f"S_q={q.shape[2]}, S_k={k.shape[2]}"
+    )
+    if q.shape[2] > _abi.MSA_VS_MAX_SEQ:
+        raise NotImplementedError(
+            f"vertical_and_slash supports S <= {_abi.MSA_VS_MAX_SEQ} on MI355X, got {q.shape[2]}"
+        )
+    B = q.shape[0]
+    n = len(plan.vs_heads)
+    nv = max(c[0] for c in plan.vs_counts)
+    ns = max(c[1] for c in plan.vs_counts)
+    dev = q.device
+    v_idx = torch.empty((B, n, nv), dtype=torch.int32, device=dev)
+    s_idx = torch.empty((B, n, ns), dtype=torch.int32, device=dev)
+    v_cnt = torch.empty((B, n), dtype=torch.int32, device=dev)
+    s_cnt = torch.empty((B, n), dtype=torch.int32, device=dev)
+    _abi.vs_estimate(q, k, plan.vs_heads, [c[0] for c in plan.vs_counts],
+                     [c[1] for c in plan.vs_counts], v_idx, v_cnt, s_idx, s_cnt)
+    return v_idx, v_cnt, s_idx, s_cnt
+
+
 def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: LayerPlan,
                         out: torch.Tensor) -> torch.Tensor:
-    """Estimator launch (if any block head) + one attention launch for all heads.
+    """Estimator launches (block_sparse and vertical_and_slash heads) + one
+    attention call for all heads.
 
     q [B, H, S_q, D]; k/v [B, H_kv, S_k, D] (H % H_kv == 0, no repeat_kv copy);
     out any [B, H, S_q, D] view with D contiguous (bf16/fp16 or fp32).
     """
     _abi.require_device(q, k, v)
     B, H, S_q, _ = q.shape
+    if plan.vs_heads and B * H > _abi.MSA_MAX_HEADS:
+        # vertical_and_slash layers run in batch slices of at most MSA_MAX_HEADS heads
+        step = max(1, _abi.MSA_MAX_HEADS // H)
+        for b0 in range(0, B, step):
+            b1 = min(B, b0 + step)
+            run_layer_attention(q[b0:b1], k[b0:b1], v[b0:b1], plan, out[b0:b1])
+        return out
     idx = cnt = None
     n_slots = len(plan.block_heads)
     if n_slots:
@@ -147,8 +193,9 @@ def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan:
         s_sparse = sparse_scale(q.shape[-1])
         _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max, s_sparse,
                             idx, cnt)
+    vs = _vs_lists(q, k, plan) if plan.vs_heads else None
     _abi.layer_attention(q, k, v, out, plan.heads, idx=idx, cnt=cnt, idx_slots=n_slots,
-                         topk_max=plan.topk_max)
+                         topk_max=plan.topk_max, vs=vs)
     return out
 
 

@@ -149,3 +149,48 @@ def test_patched_chunked_prefill_and_decode_match_oracle(gpu_device, tmp_path, m
         g = got.cpu().numpy().astype(np.float64)
         bound = 2e-3 + np.abs(ref) * 2.0 ** -8  # bf16 output of the model
         assert (np.abs(g - ref) <= bound).all(), (kind, q.shape, np.abs(g - ref).max())
+
+
+@pytest.mark.parametrize("n_kv", [8, 2])
+def test_patched_model_vertical_and_slash_heads(gpu_device, tmp_path, monkeypatch, n_kv):
+    """vertical_and_slash heads (explicit records and the default for heads
+    missing from the JSON) next to the other kinds; every layer launch is
+    checked against the oracle estimator + attention on its own inputs."""
+    model = _tiny_phi3(gpu_device, n_kv=n_kv)
+    layer0 = {"0": P.record("stream_llm", 64, 256), "2": ["vertical_and_slash", 100, 200, 1],
+              "3": P.record("block_sparse", 4), "5": P.record("dense"),
+              "6": ["vertical_and_slash", 30, 800, 1]}
+    layer1 = {str(h): ["vertical_and_slash", 60 + 10 * h, 100 + 50 * h, 1] for h in range(8)}
+    path = tmp_path / "vs.json"
+    P.write(str(path), [layer0, layer1])
+    captured = []
+    real = MF.run_layer_attention
+
+    def spy(q, k, v, plan, out):
+        res = real(q, k, v, plan, out)
+        captured.append((q.clone(), k.clone(), v.clone(), plan, res.float().clone()))
+        return res
+
+    monkeypatch.setattr(MF, "run_layer_attention", spy)
+    patched = MInference(attn_type="minference", config_path=str(path))(model)
+    ids = torch.randint(3, 256, (1, 1500), device=gpu_device,
+                        generator=torch.Generator(device=gpu_device).manual_seed(7))
+    with torch.no_grad():
+        logits = patched(ids).logits
+    assert torch.isfinite(logits).all()
+    assert len(captured) == 2
+    assert captured[0][3].vs_heads == (1, 2, 4, 6, 7)   # 1, 4, 7 default
+    for q, k, v, plan, got in captured:
+        qn, kn, vn = (t.detach().float().cpu().numpy() for t in (q, k, v))
+        rep = qn.shape[1] // kn.shape[1]
+        kr, vr = np.repeat(kn, rep, 1), np.repeat(vn, rep, 1)
+        ref = _oracle_layer(q, k, v, plan)
+        for h, (kind, p1, p2, slot, scale) in enumerate(plan.heads):
+            if kind == _abi.MSA_KIND_VS:
+                sl = slice(h, h + 1)
+                vi, si = O.vs_estimate(qn[:, sl], kr[:, sl], p1, p2, "bf16")
+                ref[:, sl] = O.vertical_slash_from_indices(qn[:, sl], kr[:, sl], vr[:, sl], vi, si,
+                                                           scale=scale)
+        g = got.cpu().numpy().astype(np.float64)
+        bound = 2e-3 + np.abs(ref) * 2.0 ** -8  # bf16 output of the model
+        assert (np.abs(g - ref) <= bound).all(), np.abs(g - ref).max()

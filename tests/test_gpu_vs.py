@@ -154,3 +154,49 @@ def test_vs_in_mixed_layer(gpu_device, H_kv):
         else:
             ref[:, sl] = O.dense_causal(qn[:, sl], kn[:, sl], vn[:, sl])
     assert_close_f32(out, ref, what=f"mixed layer with VS heads (H_kv={H_kv})")
+
+
+# ---------------------------------------------------------------------------
+# estimator: bit-exact indices
+# ---------------------------------------------------------------------------
+EST_CASES = [
+    # (B, H, H_kv, S, D, vertical_size, slash_size, dtype)
+    (1, 2, 2, 40, 96, 30, 50, torch.bfloat16),          # S < 64 rows, every index taken
+    (1, 2, 2, 100, 96, 30, 50, torch.bfloat16),
+    (1, 2, 2, 1000, 96, 100, 300, torch.bfloat16),
+    (2, 2, 2, 4096 + 17, 96, 1000, 6096, torch.bfloat16),
+    (1, 4, 2, 2048, 64, 200, 80, torch.bfloat16),       # fewer slashes than forced diagonals, GQA
+    (1, 2, 2, 3000, 128, 500, 700, torch.float16),
+]
+
+
+@pytest.mark.parametrize("case", EST_CASES, ids=[f"{c[:7]}{dtype_tag(c[7])}" for c in EST_CASES])
+def test_vs_estimator_bit_exact(gpu_device, case):
+    from minference.ops.vertical_slash_kernel import vertical_and_slash_estimate
+
+    B, H, Hkv, S, D, vsz, ssz, dtype = case
+    print(f"[vs-est] case {case}", flush=True)
+    q, _, _ = make_qkv(B, H, S, S, D, dtype, seed=S + vsz)
+    _, k, _ = make_qkv(B, Hkv, S, S, D, dtype, seed=S + ssz, sink_scale=8.0)
+    v_idx, s_idx = vertical_and_slash_estimate(*to_dev(gpu_device, q, k), vsz, ssz)
+    rv, rs = O.vs_estimate(np32(q), np32(k), vsz, ssz, dtype_tag(dtype))
+    gv, gs = v_idx.cpu().numpy(), s_idx.cpu().numpy()
+    assert gv.shape == rv.shape and gs.shape == rs.shape
+    assert np.array_equal(gv, rv), f"{(gv != rv).sum()} vertical ids differ"
+    assert np.array_equal(gs, rs), f"{(gs != rs).sum()} slash ids differ"
+
+
+@pytest.mark.parametrize("S,vsz,ssz", [(2048, 300, 500), (4096 + 17, 1000, 6096)])
+def test_vs_estimate_and_attention_vs_oracle(gpu_device, S, vsz, ssz):
+    """The reference's _vertical_and_slash_kernel end to end
+    (minference_forward.py:140-167): estimator, then the sparse attention."""
+    from minference.ops.vertical_slash_kernel import vertical_and_slash_attention
+
+    B, H, D = 1, 2, 96
+    q, k, v = make_qkv(B, H, S, S, D, torch.bfloat16, seed=S, sink_scale=8.0)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    vertical_and_slash_attention(dq, dk, dv, vsz, ssz, out=out32)
+    vi, si = O.vs_estimate(np32(q), np32(k), vsz, ssz, "bf16")
+    ref = O.vertical_slash_from_indices(np32(q), np32(k), np32(v), vi, si)
+    assert_close_f32(out32, ref, what=f"vs pipeline S={S}")

@@ -81,9 +81,14 @@ def test_build_layer_plan_semantics():
     assert plan.heads[2] == (_abi.MSA_KIND_DENSE, 0, 0, -1, s_de)
     assert plan.heads[3] == (_abi.MSA_KIND_BLOCK, 1, 0, 1, s_sp)    # clamped to >= 1
     assert plan.block_heads == (1, 3) and plan.block_topk == (64, 1) and plan.topk_max == 64
-    assert not plan.all_dense
-    with pytest.raises(NotImplementedError):
-        MF.build_layer_plan({0: pats[0]}, 2, 96, 4096)  # head 1 -> default vertical_and_slash
+    assert not plan.all_dense and plan.vs_heads == ()
+    # head 1 missing -> the default record ("vertical_and_slash", 1000, 6096, 1),
+    # counts clamped to min(S, max(v, 30)) and min(S, max(s, 50)) (:146-147)
+    vs = MF.build_layer_plan({0: pats[0]}, 2, 96, 4096)
+    assert vs.heads[1] == (_abi.MSA_KIND_VS, 1000, 4096, 0, s_sp)
+    assert vs.vs_heads == (1,) and vs.vs_counts == ((1000, 4096),)
+    small = MF.build_layer_plan({0: ["vertical_and_slash", 10, 20, 1]}, 1, 96, 40)
+    assert small.heads[0] == (_abi.MSA_KIND_VS, 30, 40, 0, s_sp)
     with pytest.raises(ValueError):
         MF.build_layer_plan({0: ["a_shape", 1, 2, 3]}, 1, 96, 4096)
 
@@ -107,6 +112,10 @@ def _oracle_launch(q, k, v, plan, out):
         elif kind == _abi.MSA_KIND_BLOCK:
             idx, _ = O.select_block_sparse_topk_indices(qn[:, sl], kn[:, sl], p1, "fp32", scale)
             res[:, sl] = O.block_sparse_from_indices(qn[:, sl], kn[:, sl], vn[:, sl], idx, scale=scale)
+        elif kind == _abi.MSA_KIND_VS:
+            vi, si = O.vs_estimate(qn[:, sl], kn[:, sl], p1, p2, "fp32")
+            res[:, sl] = O.vertical_slash_from_indices(qn[:, sl], kn[:, sl], vn[:, sl], vi, si,
+                                                       scale=scale)
         else:
             res[:, sl] = O.dense_causal(qn[:, sl], kn[:, sl], vn[:, sl], scale=scale)
     out.copy_(torch.from_numpy(res).to(out.dtype))
@@ -199,3 +208,34 @@ def test_hf_attn_type_leaves_model_unpatched():
     fwd = model.model.layers[0].self_attn.forward
     assert MInference(attn_type="hf")(model) is model
     assert model.model.layers[0].self_attn.forward == fwd
+
+
+def test_missing_heads_run_vertical_and_slash(tmp_path, monkeypatch):
+    """A head absent from the JSON takes the reference default
+    ("vertical_and_slash", 1000, 6096, 1) (minference_forward.py:229-231)."""
+    seen = []
+
+    def spy(q, k, v, plan, out):
+        seen.append(plan)
+        return _oracle_launch(q, k, v, plan, out)
+
+    monkeypatch.setattr(MF, "run_layer_attention", spy)
+    model = _tiny_phi3()
+    path = tmp_path / "partial.json"
+    P.write(str(path), [{"0": ["stream_llm", 16, 64, 1.0]}] * 2)
+    patched = patch_hf(model, "minference", {"config_path": str(path)})
+    ids = torch.randint(3, 128, (1, 150), generator=torch.Generator().manual_seed(4))
+    with torch.no_grad():
+        logits = patched(ids).logits
+    assert torch.isfinite(logits).all()
+    assert seen[0].heads[1] == (_abi.MSA_KIND_VS, 150, 150, 0, 128 ** -0.5)
+    assert seen[0].vs_heads == (1,)
+
+
+def test_vertical_and_slash_needs_full_prefill():
+    """vertical_slash_kernel_npu.py:551-556: S_q != S_k is an AssertionError."""
+    plan = MF.build_layer_plan({0: ["vertical_and_slash", 100, 200, 1]}, 1, 96, 300)
+    q = torch.zeros(1, 1, 100, 96, dtype=torch.bfloat16)
+    k = torch.zeros(1, 1, 300, 96, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        MF._vs_lists(q, k, plan)
