@@ -46,7 +46,20 @@ WORKLOADS = {
     "headline": (65536, 16, 16, 0, 128, 4096, 100),
     "cfg2_block16k": (16384, 0, 32, 0, 128, 4096, 100),
     "cfg3_stream64k": (65536, 32, 0, 0, 128, 4096, 100),
+    "vs64k": (65536, 0, 0, 0, 0, 0, 0),  # VS_MIX below
 }
+
+# The reference's original Phi-3 pattern (1024 heads: vertical_and_slash
+# (3500,100) x378, (1000,6096) x277, (100,750) x184, (500,700) x92,
+# (30,800) x50, stream_llm (100,800) x43) scaled to one layer of 32 heads.
+VS_MIX = [
+    (12, ["vertical_and_slash", 3500, 100, 1.0]),
+    (9, ["vertical_and_slash", 1000, 6096, 1.0]),
+    (6, ["vertical_and_slash", 100, 750, 1.0]),
+    (3, ["vertical_and_slash", 500, 700, 1.0]),
+    (1, ["vertical_and_slash", 30, 800, 1.0]),
+    (1, ["stream_llm", 100, 800, 1.0]),
+]
 
 
 def parse_args():
@@ -202,6 +215,8 @@ def main():
     from minference.ops.common import sparse_scale
 
     dev = torch.device("cuda:0")
+    if args.workload == "vs64k":
+        return vs_bench(args, dev)
     S, n_stream, n_block, n_dense, n_init, n_local, topk = WORKLOADS[args.workload]
     H, D = args.heads, args.dim
     scale_h = H / (n_stream + n_block + n_dense)
@@ -325,6 +340,143 @@ def main():
         result["dense"] = dense_baselines(q, k, v, S, H, D, ms_step)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_heads)
+    print(json.dumps(result), flush=True)
+
+
+def vs_tiles(v_idx, s_idx, S):
+    """Key tiles the attention kernel walks for one vertical_and_slash head:
+    per query block, the tiles a slash window meets (plus the diagonal tile
+    when a vertical column lies in it) and the 64-column groups of gathered
+    vertical columns (the tile-list rule of vs_build_kernel)."""
+    import numpy as np
+
+    nb = -(-S // BLOCK)
+    bq = np.arange(nb)
+    end = BLOCK * (bq + 1)
+    cov = np.zeros((nb, nb), dtype=bool)
+    for s in np.asarray(s_idx).tolist():
+        ok = s < end
+        hi = np.minimum(np.maximum(end - s, BLOCK), S)
+        lo = np.maximum(hi - BLOCK, 0)
+        hc = np.minimum(hi, np.minimum(end, S))
+        ok &= lo < hc
+        rows = bq[ok]
+        cov[rows, lo[ok] // BLOCK] = True
+        cov[rows, (hc[ok] - 1) // BLOCK] = True
+    cov &= bq[None, :] <= bq[:, None]
+    cols = np.asarray(v_idx)
+    ctile = cols // BLOCK
+    total = int(cov.sum())
+    for b in range(nb):
+        in_diag = (ctile == b).any()
+        total += int(in_diag and not cov[b, b])
+        gath = (cols < BLOCK * b) & ~cov[b, np.minimum(ctile, nb - 1)]
+        if gath.any():
+            total += len(np.unique(np.nonzero(gath)[0] // BLOCK))
+    return total
+
+
+def vs_bench(args, dev):
+    """--workload vs64k: one layer of the reference's original Phi-3 pattern mix
+    at 64K (VS_MIX): vertical_and_slash estimator + K/V staging + attention
+    (tile-list build, vertical gather, VS kernel, and the stream head's
+    kernel)."""
+    import random
+
+    import torch
+
+    from minference import _abi
+    from minference.modules.minference_forward import build_layer_plan, _vs_lists
+
+    S, H, D = 65536, args.heads, args.dim
+    kinds = [rec for n, rec in VS_MIX for _ in range(n)]
+    random.Random(args.seed).shuffle(kinds)
+    plan = build_layer_plan({h: kinds[h] for h in range(H)}, H, D, S)
+    q, k, v = make_inputs(S, H, D, args.seed, dev)
+    out = torch.empty_like(q)
+    ws_att = _abi.workspace(_abi.attention_workspace_bytes(1, H, S, D), dev)
+    nv = max(c[0] for c in plan.vs_counts)
+    vs_ws = _abi.workspace(_abi.vs_workspace_bytes(1, len(plan.vs_heads), S, nv, D), dev)
+    stream = torch.cuda.current_stream(dev)
+    lists = [None]
+
+    def step(e=None):
+        if e:
+            e[0].record(stream)
+        lists[0] = _vs_lists(q, k, plan)
+        if e:
+            e[1].record(stream)
+        _abi.stage_kv(k, v, ws_att)
+        if e:
+            e[2].record(stream)
+        _abi.layer_attention(q, k, v, out, plan.heads, ws=ws_att, staged=True, vs=lists[0],
+                             vs_ws=vs_ws)
+        if e:
+            e[3].record(stream)
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(ev[i])
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    t_est = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    t_stage = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    t_attn = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+
+    v_idx, v_cnt, s_idx, s_cnt = (t.cpu() for t in lists[0])
+    tiles = 0
+    for j, h in enumerate(plan.vs_heads):
+        tiles += vs_tiles(v_idx[0, j, :int(v_cnt[0, j])].numpy(),
+                          s_idx[0, j, :int(s_cnt[0, j])].numpy(), S)
+    # the tile-list builder's own totals, read from the workspace (layout of
+    # vs_layout in msa_abi.hip: ids, masks, then (unmasked, total) per row)
+    n_kb = -(-S // BLOCK)
+    nv_pad = -(-max(nv, 1) // BLOCK) * BLOCK
+    cap = n_kb + nv_pad // BLOCK
+    n_rows = len(plan.vs_heads) * n_kb
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    cnt_off = up(up(n_rows * cap * 4) + n_rows * cap * 8)
+    counts = vs_ws[cnt_off:cnt_off + n_rows * 8].view(torch.int32).view(n_rows, 2).cpu()
+    tiles_gpu = int(counts[:, 1].sum())
+    n_stream = sum(1 for hd in plan.heads if hd[0] == _abi.MSA_KIND_STREAM)
+    flop_vs = tiles * 4 * BLOCK * BLOCK * D
+    flop_stream = n_stream * stream_pairs(S, 100, 800) * 4 * D
+    flop = flop_vs + flop_stream
+    dense_flop = H * (S * (S + 1) // 2) * 4 * D
+    result = {
+        "metric": "vertical_and_slash prefill attn ms/layer, Phi-3 64K (original pattern mix)",
+        "value": round(flop / (ms_step * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) Q/K/V, RoPE, K rows 0-3 x8)",
+        "config": {
+            "workload": "vs64k", "seq_len": S, "heads": H, "head_dim": D,
+            "mix": {f"{r[0]}({r[1]},{r[2]})": n for n, r in VS_MIX},
+            "global_batch": 1, "parallelism": "single GPU",
+        },
+        "ms_per_layer": round(ms_step, 4),
+        "kernels_ms": {"vs_estimate": round(t_est, 4), "stage_kv": round(t_stage, 4),
+                       "lists_gather_attention": round(t_attn, 4)},
+        "vs_tiles": tiles,
+        "vs_tiles_builder": tiles_gpu,
+        "vs_tile_density": round(tiles / (len(plan.vs_heads) * block_tiles(S, 1 << 30)), 4),
+        "executed_flop": flop,
+        "attention_tflops": round(flop / (t_attn * 1e-3) / 1e12, 3),
+        "dense_equivalent_tflops": round(dense_flop / (ms_step * 1e-3) / 1e12, 3),
+    }
+    if not args.no_dense:
+        result["dense"] = dense_baselines(q, k, v, S, H, D, ms_step)
     print(json.dumps(result), flush=True)
 
 

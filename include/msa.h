@@ -71,7 +71,8 @@ typedef struct msa_tensor4 {
 
 /* One attention head of a layer.
  *   kind   = MSA_KIND_*
- *   p1, p2 = stream_llm: n_init, n_local;  block_sparse: topk (unused here), 0
+ *   p1, p2 = stream_llm: n_init, n_local;  block_sparse: topk (unused here), 0;
+ *            vertical_and_slash: vertical and slash counts (work estimate only)
  *   slot   = block_sparse: row of idx/cnt written by msa_block_estimate; else -1
  *   scale  = softmax scale applied to q.k (the caller decides)
  * Mirrors the per-head record [type, p1, p2, score] parsed at

@@ -14,6 +14,7 @@ using namespace msa;
 namespace {
 
 constexpr int64_t kMaxSeq = int64_t(1) << 20;  // 1M tokens: 16384 blocks
+constexpr size_t kQueueBytes = 256;             // work-queue counters of an attention launch
 
 int elem_size(int dtype) {
   switch (dtype) {
@@ -158,9 +159,25 @@ int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t
 size_t msa_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t s_k,
                                      int32_t head_dim) {
   if (batch <= 0 || kv_heads <= 0 || s_k <= 0 || head_dim <= 0) return 0;
-  // staged V operands (fp16), then staged K operands (input dtype)
+  // staged V operands (fp16), staged K operands (input dtype), then the
+  // work-queue counters of the attention launch
   const int64_t bytes = 2 * batch * kv_heads * head_dim * cdiv(s_k, MSA_BLOCK) * MSA_BLOCK * 2;
-  return size_t((bytes + 255) / 256 * 256);
+  return size_t((bytes + 255) / 256 * 256) + kQueueBytes;
+}
+
+// work-queue counters at the end of the attention workspace
+static int* queue_of(void* workspace, size_t workspace_bytes) {
+  return reinterpret_cast<int*>(static_cast<unsigned char*>(workspace) + workspace_bytes -
+                                kQueueBytes);
+}
+
+// CUs per XCD of the current device (8 XCDs on gfx950)
+static int cus_per_xcd() {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  return cus >= 8 ? cus / 8 : 1;
 }
 
 // K and V halves of the attention workspace
@@ -332,57 +349,68 @@ size_t msa_vs_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_k, int32
   return vs_layout(batch, n_slots, s_k, v_stride, head_dim).total;
 }
 
-// Work estimate of one head in key tiles, for the XCD balance.
-static double head_cost(const msa_head_desc& hd, int n_kb, int topk_max, const msa_vs_lists* vs) {
+// Work model of one head for the XCD split: query block bq costs
+// min(bq + 1, cap) + fixed, in key tiles (fixed covers the item set-up and
+// the output merge).  The prefix sums have a closed form.
+struct HeadWork {
+  double cap, fixed;
+};
+
+static HeadWork head_work(const msa_head_desc& hd, int n_kb, int topk_max) {
   const double nb = double(n_kb);
-  if (hd.kind == MSA_KIND_DENSE) return nb * (nb + 1) / 2;
+  HeadWork w{nb, 2.0};
   if (hd.kind == MSA_KIND_STREAM) {
-    const double band = fmin(nb, double(hd.p2) / 64.0 + 1.0);
-    const double sink = fmin(nb, ceil(fmax(double(hd.p1), 0.0) / 64.0));
-    return nb * (band + sink);
+    w.cap = fmin(nb, double(hd.p2) / 64.0 + 2.0 + ceil(fmax(double(hd.p1), 0.0) / 64.0));
+  } else if (hd.kind == MSA_KIND_BLOCK) {
+    w.cap = fmin(nb, fmax(1.0, double(hd.p1 > 0 ? hd.p1 : topk_max)));
+  } else if (hd.kind == MSA_KIND_VS) {
+    // slash tiles grow with the slash count; vertical columns add gathered tiles
+    w.cap = fmin(nb, 2.0 + double(hd.p2) / 16.0);
+    w.fixed += double(hd.p1) / 128.0;
   }
-  if (hd.kind == MSA_KIND_VS) {
-    const double per = fmin(nb, 2.0 * vs->s_stride + 1.0 + vs->v_stride / 64.0);
-    return nb * per;
-  }
-  const double kk = fmin(nb, double(topk_max));
-  return nb * kk - kk * (kk - 1) / 2;
+  return w;
 }
 
-// (batch, head) pairs of one launch: with a multiple of 8 pairs, the 8 XCDs
-// (round-robin workgroup dispatch) each get a fixed subset so that its L2
-// serves those heads, balanced by estimated work (greedy
-// longest-processing-time); otherwise plain order.
-static void order_heads(AttnParams& ap, const int* pairs, const double* cost, int n) {
-  ap.n_bh = n;
-  if (n % 8 != 0) {
-    for (int i = 0; i < n; ++i) ap.head_order[i] = int16_t(pairs[i]);
-    ap.xcd_heads = 0;
-    return;
-  }
-  const int per = n / 8;
-  int order[kMaxHeads];
-  for (int i = 0; i < n; ++i) order[i] = i;
-  for (int i = 1; i < n; ++i) {  // insertion sort, descending cost
-    const int x = order[i];
-    int j = i - 1;
-    while (j >= 0 && cost[order[j]] < cost[x]) {
-      order[j + 1] = order[j];
-      --j;
-    }
-    order[j + 1] = x;
-  }
-  double load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  int fill[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+// cost of query blocks 0 .. m-1
+static double prefix_cost(const HeadWork& w, double m) {
+  const double k = w.cap;
+  const double tri = m <= k ? m * (m + 1) / 2 : k * (k + 1) / 2 + (m - k) * k;
+  return tri + w.fixed * m;
+}
+
+// Items of one launch: the listed (batch, head) pairs, head-major, query
+// blocks longest-first; the 8 XCDs (round-robin workgroup dispatch) take
+// contiguous ranges of equal estimated cost, so each XCD's L2 serves few
+// heads and a heavy head can be shared by two XCDs.
+static void order_items(AttnParams& ap, const int* pairs, const HeadWork* work, int n) {
+  const int nq = ap.n_qb;
+  ap.n_hl = n;
+  double head_tot[kMaxHeads], total = 0.0;
   for (int i = 0; i < n; ++i) {
-    int best = -1;
-    for (int x = 0; x < 8; ++x)
-      if (fill[x] < per && (best < 0 || load[x] < load[best])) best = x;
-    ap.head_order[best * per + fill[best]] = int16_t(pairs[order[i]]);
-    ++fill[best];
-    load[best] += cost[order[i]];
+    ap.head_order[i] = int16_t(pairs[i]);
+    head_tot[i] = prefix_cost(work[i], nq);
+    total += head_tot[i];
   }
-  ap.xcd_heads = per;
+  int prev = 0, h = 0;
+  double before = 0.0;  // cost of the heads before h
+  for (int x = 0; x < 8; ++x) {
+    int cut = n * nq;
+    if (x < 7) {
+      const double target = total * (x + 1) / 8.0;
+      while (h < n - 1 && before + head_tot[h] < target) before += head_tot[h++];
+      const double need = target - before;
+      int lo = 0, hi = nq;  // first r items (bq = nq-1 .. nq-r) of head h cost >= need
+      while (lo < hi) {
+        const int mid = (lo + hi) / 2;
+        if (prefix_cost(work[h], nq) - prefix_cost(work[h], nq - mid) >= need) hi = mid;
+        else lo = mid + 1;
+      }
+      cut = std::max(prev, h * nq + lo);
+    }
+    ap.xcd_start[x] = prev;
+    ap.xcd_count[x] = cut - prev;
+    prev = cut;
+  }
 }
 
 static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
@@ -482,6 +510,8 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   ap.cnt = cnt;
   ap.idx_slots = idx_slots;
   ap.topk_max = topk_max;
+  ap.queue = queue_of(workspace, need);
+  ap.wg_per_xcd = cus_per_xcd();
   const double log2e = 1.4426950408889634;
   for (int h = 0; h < n_heads; ++h) {
     const int kd = heads[h].kind;
@@ -494,17 +524,16 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
 
   const int BH = int(B * H);
   if (n_vs == 0) {
-    if (BH % 8 == 0 && BH <= kMaxHeads) {
+    if (BH <= kMaxHeads) {
       int pairs[kMaxHeads];
-      double cost[kMaxHeads];
+      HeadWork work[kMaxHeads];
       for (int i = 0; i < BH; ++i) {
         pairs[i] = i;
-        cost[i] = head_cost(heads[i % H], n_kb, topk_max, vs);
+        work[i] = head_work(heads[i % H], n_kb, topk_max);
       }
-      order_heads(ap, pairs, cost, BH);
+      order_items(ap, pairs, work, BH);
     } else {
-      ap.n_bh = 0;  // every pair, plain order (also for B * H > kMaxHeads)
-      ap.xcd_heads = 0;
+      ap.n_hl = 0;  // every pair, plain order
     }
     const hipError_t e = launch_attention(ap, q->dtype, o->dtype, D, hs);
     return e == hipSuccess ? MSA_OK : int(e);
@@ -551,16 +580,16 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   if (e != hipSuccess) return int(e);
 
   int vs_pairs[kMaxHeads], other[kMaxHeads];
-  double vs_cost[kMaxHeads], other_cost[kMaxHeads];
+  HeadWork vs_work[kMaxHeads], other_work[kMaxHeads];
   int n_v = 0, n_o = 0;
   for (int i = 0; i < BH; ++i) {
     const msa_head_desc& hd = heads[i % H];
     if (hd.kind == MSA_KIND_VS) {
       vs_pairs[n_v] = i;
-      vs_cost[n_v++] = head_cost(hd, n_kb, topk_max, vs);
+      vs_work[n_v++] = head_work(hd, n_kb, topk_max);
     } else {
       other[n_o] = i;
-      other_cost[n_o++] = head_cost(hd, n_kb, topk_max, vs);
+      other_work[n_o++] = head_work(hd, n_kb, topk_max);
     }
   }
   AttnParams vp = ap;
@@ -572,11 +601,11 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   vp.vs_slots = vs->n_slots;
   vp.vs_cap = vl.cap;
   vp.nv_pad = vl.nv_pad;
-  order_heads(vp, vs_pairs, vs_cost, n_v);
+  order_items(vp, vs_pairs, vs_work, n_v);
   e = launch_attention_vs(vp, q->dtype, o->dtype, D, hs);
   if (e != hipSuccess) return int(e);
   if (n_o) {
-    order_heads(ap, other, other_cost, n_o);
+    order_items(ap, other, other_work, n_o);
     e = launch_attention(ap, q->dtype, o->dtype, D, hs);
   }
   return e == hipSuccess ? MSA_OK : int(e);

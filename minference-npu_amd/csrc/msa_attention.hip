@@ -294,6 +294,21 @@ struct AttnShape {
   static constexpr int SLOT = (NO + 4) * 64;      // merge slot of one wave (floats)
 };
 
+// Next item of the persistent attention grid: the home XCD's range first,
+// then the others'; -1 when every range is empty.  One lane calls it.
+__device__ inline int next_item(const AttnParams& P, int xcd) {
+  for (int k = 0; k < 8; ++k) {
+    const int y = (xcd + k) & 7;
+    const int r = atomicAdd(&P.queue[y], 1);
+    if (r < P.xcd_count[y]) return P.xcd_start[y] + r;
+  }
+  return -1;
+}
+
+__global__ void queue_reset_kernel(int* q) {
+  if (threadIdx.x < 8) q[threadIdx.x] = 0;
+}
+
 // VS = false: stream_llm / block_sparse / dense heads; VS = true: the
 // vertical_and_slash heads of a layer (tile lists from vs_build_kernel).
 template <typename T, bool OUT_F32, int D, bool VS>
@@ -310,20 +325,18 @@ void attn_kernel(AttnParams P) {
   const int lc = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // keys 16w .. 16w+15 of every tile
 
-  // ---- work item.  Workgroups are dispatched round-robin over the 8 XCDs;
-  // each XCD walks its own heads one at a time (query blocks longest-first),
-  // so the K/V of the 8 heads in flight stay resident in L2 / Infinity Cache.
-  const int BH = P.n_bh ? P.n_bh : P.batch * P.heads;
-  const int item = blockIdx.x;
-  int hh, bq;
-  if (P.xcd_heads) {
-    const int r = item >> 3;
-    bq = P.n_qb - 1 - r % P.n_qb;
-    hh = P.head_order[(item & 7) * P.xcd_heads + r / P.n_qb];
-  } else {
-    bq = P.n_qb - 1 - item / BH;
-    hh = P.n_bh ? int(P.head_order[item % BH]) : item % BH;
-  }
+  // ---- work items.  Workgroups are dispatched round-robin over the 8 XCDs
+  // and each XCD takes a range of the head-major item list (query blocks
+  // longest-first), so its L2 serves few heads at a time.
+  //   vertical_and_slash (work known only after the tile-list build): the
+  //   grid is persistent; a workgroup takes items of its XCD's range through
+  //   that range's counter, then of the other XCDs' ranges once its own is
+  //   empty, and exits when every range is empty.
+  //   other kinds: workgroup i is item i / 8 of XCD i % 8's range (ranges
+  //   cut by estimated cost); without a list, item i in plain order.
+  __shared__ int s_item;
+  const int xcd = blockIdx.x & 7;
+  auto item_body = [&](const int hh, const int bq) INLINE {
   const int b = hh / P.heads;
   const int h = hh - b * P.heads;
   const int kvh = h / P.kv_group;
@@ -470,14 +483,13 @@ void attn_kernel(AttnParams P) {
       for (int gg = 0; gg < 2; ++gg) s[gg] = mfma_qk<T>(kr[ks], qb[2 * hf + gg][ks], s[gg]);
   };
   // visible iff j <= key_hi and (j >= band_lo or j < sink_hi); for a
-  // vertical_and_slash tile: iff the key's bit is set in the tile's mask and
-  // (gathered tile, all keys in every row's past, or j <= key_hi)
-  auto mask_half = [&](f32x4 (&s)[2], int hf, int t, int p) INLINE {
+  // vertical_and_slash tile: iff the key's bit is set in the tile's mask mk
+  // and (gathered tile, all keys in every row's past, or j <= key_hi)
+  auto mask_half = [&](f32x4 (&s)[2], int hf, int t, uint64_t mk) INLINE {
     const int jb = t * kBlock + 16 * w + 4 * lr;
     uint32_t bits = 0xfu;
     bool past = false;
     if constexpr (VS) {
-      const uint64_t mk = P.vs_masks[vs_base + p];
       bits = uint32_t(mk >> (16 * w + 4 * lr)) & 0xfu;
       past = t >= P.n_kb;
     }
@@ -514,10 +526,10 @@ void attn_kernel(AttnParams P) {
   };
   // Rare path: recompute the half's scores, raise the running max to the
   // row max, rescale the half's O and row sums, and redo the exponentials.
-  auto rescale_half = [&](const u32x4 (&kr)[NKS], f32x4 (&s)[2], int hf, int t, int p,
+  auto rescale_half = [&](const u32x4 (&kr)[NKS], f32x4 (&s)[2], int hf, int t, uint64_t mk,
                           bool mt) INLINE {
     qk_half(kr, hf, s);
-    if (mt) mask_half(s, hf, t, p);
+    if (mt) mask_half(s, hf, t, mk);
     float m0 = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
     float m1 = fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3]));
     swap32(m0, m1);  // lane rows (R0, R2) and (R1, R3) of each group
@@ -578,7 +590,14 @@ void attn_kernel(AttnParams P) {
   const int total = seq.total;
   const int mpos = min(seq.mpos, total);
   u32x4 kA[NKS], vA[NDB], kB[NKS], vB[NDB];
+  // key masks of vertical_and_slash tiles travel with their tile numbers
+  // (looked up three positions ahead, like the tiles)
+  auto mask_at = [&](int q) INLINE -> uint64_t {
+    if constexpr (VS) return P.vs_masks[vs_base + max(min(q, total - 1), 0)];
+    return 0ull;
+  };
   int tA = seq.tile(0), tB = seq.tile(1);
+  uint64_t mA = mask_at(0), mB = mask_at(1), mn = mask_at(2);
   load_k(tA, kA);
   load_v(tA, vA);
   load_k(tB, kB);
@@ -587,39 +606,48 @@ void attn_kernel(AttnParams P) {
   // one step: QK of both halves; half 0's softmax under half 1's QK, half
   // 1's softmax under half 0's PV; K is reloaded once the rare path can no
   // longer need it
-  auto step = [&](auto masked, u32x4 (&kr)[NKS], u32x4 (&vr)[NDB], int& tcur, int p) INLINE {
+  auto step = [&](auto masked, u32x4 (&kr)[NKS], u32x4 (&vr)[NDB], int& tcur, uint64_t& mcur,
+                  int p) INLINE {
     constexpr bool MT = decltype(masked)::value;
     const int tnn = seq.tile(p + 3);
+    const uint64_t mnn = mask_at(p + 3);
     f32x4 sa[2], sb[2];
     qk_half(kr, 0, sa);
     qk_half(kr, 1, sb);
-    if constexpr (MT) mask_half(sa, 0, tcur, p);
-    if (exp_half(sa, 0)) rescale_half(kr, sa, 0, tcur, p, MT);
+    if constexpr (MT) mask_half(sa, 0, tcur, mcur);
+    if (exp_half(sa, 0)) rescale_half(kr, sa, 0, tcur, mcur, MT);
     pv_half(sa, 0, vr);
-    if constexpr (MT) mask_half(sb, 1, tcur, p);
-    if (exp_half(sb, 1)) rescale_half(kr, sb, 1, tcur, p, MT);
+    if constexpr (MT) mask_half(sb, 1, tcur, mcur);
+    if (exp_half(sb, 1)) rescale_half(kr, sb, 1, tcur, mcur, MT);
     load_k(tn, kr);
     pv_half(sb, 1, vr);
     load_v(tn, vr);
     tcur = tn;
     tn = tnn;
+    mcur = mn;
+    mn = mnn;
   };
   auto run = [&](auto masked, int p0, int p1) INLINE {
     int p = p0;
-    if ((p & 1) && p < p1) step(masked, kB, vB, tB, p++);
+    if ((p & 1) && p < p1) step(masked, kB, vB, tB, mB, p++);
     for (; p + 1 < p1; p += 2) {
-      step(masked, kA, vA, tA, p);
-      step(masked, kB, vB, tB, p + 1);
+      step(masked, kA, vA, tA, mA, p);
+      step(masked, kB, vB, tB, mB, p + 1);
     }
-    if (p < p1) step(masked, kA, vA, tA, p);
+    if (p < p1) step(masked, kA, vA, tA, mA, p);
   };
   run(std::integral_constant<bool, false>(), 0, mpos);
   run(std::integral_constant<bool, true>(), mpos, total);
 
   // ---- merge the four chunk partials of each row; wave 0 writes the rows
+  // block layout: lane rows 1, 3 hold group 2rb+1.  Chosen by an exact blend
+  // (the maxima are finite) rather than a select, which the compiler turns
+  // into a lane-indexed load from a private copy of m_g.
   float m_b[2], l_b[2];
+  const float odd = float(lr & 1);
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) m_b[rb] = (lr & 1) ? m_g[2 * rb + 1] : m_g[2 * rb];
+  for (int rb = 0; rb < 2; ++rb)
+    m_b[rb] = __builtin_fmaf(odd, m_g[2 * rb + 1], (1.0f - odd) * m_g[2 * rb]);
   lanes_to_blocks(reduce_rows(l_g[0], l_g[1], l_g[2], l_g[3], RowSum()), l_b);
   if (w > 0) {
     float* slot = lds + (w - 1) * S::SLOT;
@@ -636,8 +664,7 @@ void attn_kernel(AttnParams P) {
     }
   }
   __syncthreads();
-  if (w > 0) return;
-
+  if (w == 0) {
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     float mw[4], lw[4];
@@ -687,11 +714,50 @@ void attn_kernel(AttnParams P) {
       }
     }
   }
+  }  // w == 0
+  };
+
+  if constexpr (VS) {
+    for (;;) {
+      if (tid == 0) s_item = next_item(P, xcd);
+      __syncthreads();
+      const int g = __builtin_amdgcn_readfirstlane(s_item);
+      __syncthreads();
+      if (g < 0) break;
+      const int hl = g / P.n_qb;
+      item_body(int(P.head_order[hl]), P.n_qb - 1 - (g - hl * P.n_qb));
+    }
+  } else if (P.n_hl) {
+    const int r = int(blockIdx.x) >> 3;
+    if (r >= P.xcd_count[xcd]) return;
+    const int g = P.xcd_start[xcd] + r;
+    const int hl = g / P.n_qb;
+    item_body(int(P.head_order[hl]), P.n_qb - 1 - (g - hl * P.n_qb));
+  } else {
+    const int BH = P.batch * P.heads;
+    item_body(int(blockIdx.x) % BH, P.n_qb - 1 - int(blockIdx.x) / BH);
+  }
 }
 
 template <typename T, bool OUT_F32, int D, bool VS>
 static hipError_t launch_attn_t(const AttnParams& p, hipStream_t st) {
-  const int64_t items = int64_t(p.n_qb) * (p.n_bh ? p.n_bh : p.batch * p.heads);
+  int64_t items = int64_t(p.n_qb) * p.batch * p.heads;
+  if (p.n_hl) {
+    int longest = 0;
+    for (int x = 0; x < 8; ++x) longest = p.xcd_count[x] > longest ? p.xcd_count[x] : longest;
+    items = 8 * int64_t(longest);
+  }
+  if (VS) {
+    // persistent grid: the resident workgroups of every XCD (2 per CU at
+    // two waves per SIMD, 1 for D = 128), capped by the work
+    const int64_t per_xcd = p.wg_per_xcd * (D > 96 ? 1 : 2);
+    items = items < 8 * per_xcd ? items : 8 * per_xcd;
+    if (items == 0) return hipSuccess;
+    hipLaunchKernelGGL(queue_reset_kernel, dim3(1), dim3(64), 0, st, p.queue);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (items == 0) return hipSuccess;
   hipLaunchKernelGGL((attn_kernel<T, OUT_F32, D, VS>), dim3(uint32_t(items)), dim3(256), 0, st, p);
   return hipGetLastError();
 }

@@ -53,12 +53,16 @@ struct AttnParams {
   const int32_t* idx;
   const int32_t* cnt;
   int idx_slots, topk_max;
-  // (batch, head) pairs of this launch: n_bh > 0 lists them in head_order
-  // (b * heads + h); n_bh == 0 takes every pair in plain order.
-  // xcd_heads != 0: n_bh = 8 * xcd_heads and head_order holds each XCD's
-  // pairs consecutively.
-  int n_bh;
-  int xcd_heads;
+  // Work items of this launch.  n_hl > 0: the items are (head_order[hl],
+  // query block) for hl < n_hl, listed head-major with query blocks
+  // longest-first; XCD x (workgroup i with i % 8 == x) takes items
+  // xcd_start[x] + (i / 8) for i / 8 < xcd_count[x].  n_hl == 0: every
+  // (batch, head) pair of the layer in plain order.
+  int n_hl;
+  int xcd_start[8];
+  int xcd_count[8];
+  int* queue;      // 8 counters of the XCD ranges (zeroed before each launch)
+  int wg_per_xcd;  // CUs per XCD
   // vertical_and_slash launch: per (b * vs_slots + slot, query block) a list
   // of vs_cap tile ids (gathered vertical tiles as n_kb + g), one 64-bit key
   // mask per entry, and (unmasked prefix, total) counts; gathered vertical

@@ -11,15 +11,16 @@
 // under the causal mask j <= i.
 //
 // vs_build_kernel turns that into a list per (slot, query block):
-//   1. full tiles: key tiles t < bq whose 64 keys are all visible (no mask);
-//   2. partial tiles: the other key tiles t <= bq that a slash window meets,
-//      plus tile bq if a vertical column lies in it; the mask holds the slash
-//      keys and the vertical columns of the tile (the kernel adds the causal
-//      mask for t == bq);
-//   3. gathered tiles n_kb + g: vertical columns c in [64 g, 64 g + 64) of
-//      the slot's column list that lie before 64 bq in a tile no slash window
-//      meets; their K/V rows are staged contiguously (stage_kernel, gather
-//      mode) so that scattered columns cost a dense tile, not one tile each.
+//   * key tiles t <= bq that a slash window meets, plus tile bq if a vertical
+//     column lies in it; the mask holds the slash keys and the vertical
+//     columns of the tile (the kernel adds the causal mask for t == bq);
+//   * gathered tiles n_kb + g: vertical columns c in [64 g, 64 g + 64) of
+//     the slot's column list that lie before 64 bq in a tile no slash window
+//     meets; their K/V rows are staged contiguously (stage_kernel, gather
+//     mode) so that scattered columns cost a dense tile, not one tile each.
+// Entries whose 64 keys are all visible to every row (key tiles t < bq with
+// a full mask, gathered tiles with a full mask) come first and run without
+// a mask; then the key tiles, then the gathered tiles, that need one.
 // Every visible key appears in exactly one entry.
 
 #include "msa_common.h"
@@ -111,8 +112,8 @@ __global__ __launch_bounds__(256) void vs_build_kernel(VsBuildParams P) {
   }
   __syncthreads();
 
-  // counts: full and partial key tiles, gathered tiles
-  int n_full = 0, n_part = 0, n_gath = 0;
+  // counts: full and partial key tiles, full and partial gathered tiles
+  int n_full = 0, n_part = 0, n_gfull = 0, n_gpart = 0;
   for (int t0 = 0; t0 < n_t; t0 += 256) {
     const int t = t0 + tid;
     const uint64_t m = t < n_t ? lds_get64(um, t) : 0ull;
@@ -125,16 +126,20 @@ __global__ __launch_bounds__(256) void vs_build_kernel(VsBuildParams P) {
   }
   for (int g0 = 0; g0 < n_g; g0 += 256) {
     const int g = g0 + tid;
+    const uint64_t m = g < n_g ? lds_get64(gm, g) : 0ull;
     int tot;
-    block_prefix(g < n_g && lds_get64(gm, g) != 0ull, scratch, &tot);
-    n_gath += tot;
+    block_prefix(m == ~0ull, scratch, &tot);
+    n_gfull += tot;
+    block_prefix(m != 0ull && m != ~0ull, scratch, &tot);
+    n_gpart += tot;
   }
 
-  // write the list
+  // write the list: full key tiles, full gathered tiles | partial key tiles,
+  // partial gathered tiles
   const int64_t row = int64_t(bs) * P.n_qb + bq;
   int32_t* ids = P.ids + row * P.cap;
   uint64_t* masks = P.masks + row * P.cap;
-  int off_full = 0, off_part = n_full;
+  int off_full = 0, off_part = n_full + n_gfull;
   for (int t0 = 0; t0 < n_t; t0 += 256) {
     const int t = t0 + tid;
     const uint64_t m = t < n_t ? lds_get64(um, t) : 0ull;
@@ -153,21 +158,28 @@ __global__ __launch_bounds__(256) void vs_build_kernel(VsBuildParams P) {
     off_full += tf;
     off_part += tp;
   }
-  int off_g = n_full + n_part;
+  int off_gfull = n_full, off_gpart = n_full + n_gfull + n_part;
   for (int g0 = 0; g0 < n_g; g0 += 256) {
     const int g = g0 + tid;
     const uint64_t m = g < n_g ? lds_get64(gm, g) : 0ull;
-    int tg;
-    const int pg = block_prefix(m != 0ull, scratch, &tg);
-    if (m != 0ull) {
-      ids[off_g + pg] = P.n_kb + g;
-      masks[off_g + pg] = m;
+    const bool full = m == ~0ull;
+    const bool part = m != 0ull && !full;
+    int tf, tp;
+    const int pf = block_prefix(full, scratch, &tf);
+    const int pp = block_prefix(part, scratch, &tp);
+    if (full) {
+      ids[off_gfull + pf] = P.n_kb + g;
+      masks[off_gfull + pf] = m;
+    } else if (part) {
+      ids[off_gpart + pp] = P.n_kb + g;
+      masks[off_gpart + pp] = m;
     }
-    off_g += tg;
+    off_gfull += tf;
+    off_gpart += tp;
   }
   if (tid == 0) {
-    P.cnt[2 * row] = n_full;
-    P.cnt[2 * row + 1] = n_full + n_part + n_gath;
+    P.cnt[2 * row] = n_full + n_gfull;
+    P.cnt[2 * row + 1] = n_full + n_gfull + n_part + n_gpart;
   }
 }
 
@@ -198,8 +210,8 @@ hipError_t launch_vs_build(const VsBuildParams& p, int n_bs, hipStream_t st) {
 // block of (row, column) pairs, operands in LDS as fp64.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void vs_score_kernel(VsEstParams P) {
-  constexpr int KP = D + 1;  // padded K row (fp64): 16 rows of a wave hit distinct banks
-  __shared__ double qs[kBlock * D];
+  constexpr int KP = D + 1;  // padded rows (fp64): the rows a wave reads hit distinct banks
+  __shared__ double qs[kBlock * KP];
   __shared__ double ks[kBlock * KP];
   const int j0 = blockIdx.x * kBlock;
   const int bs = blockIdx.y;
@@ -212,7 +224,7 @@ __global__ __launch_bounds__(256) void vs_score_kernel(VsEstParams P) {
   const uint16_t* kb = reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + int64_t(kvh) * P.k_sh;
   for (int i = tid; i < kBlock * D; i += 256) {
     const int r = i / D, d = i - r * D;
-    qs[i] = r < n ? double(T::to_float(qb[int64_t(P.s - n + r) * P.q_ss + d])) : 0.0;
+    qs[r * KP + d] = r < n ? double(T::to_float(qb[int64_t(P.s - n + r) * P.q_ss + d])) : 0.0;
     const int j = j0 + r;
     ks[r * KP + d] = j < P.s ? double(T::to_float(kb[int64_t(j) * P.k_ss + d])) : 0.0;
   }
@@ -226,7 +238,7 @@ __global__ __launch_bounds__(256) void vs_score_kernel(VsEstParams P) {
   for (int d = 0; d < D; ++d) {
     double a[4], bb[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = qs[(rg + 16 * i) * D + d];
+    for (int i = 0; i < 4; ++i) a[i] = qs[(rg + 16 * i) * KP + d];
 #pragma unroll
     for (int c = 0; c < 4; ++c) bb[c] = ks[(cg + 16 * c) * KP + d];
 #pragma unroll

@@ -132,7 +132,7 @@ def run_vs_heads(q, k, v, result, v_ids, v_cnt, s_idx, scale):
     s_cnt = torch.full((B, H), s_idx.shape[-1], dtype=torch.int32, device=q.device)
     for h0, h1 in _vs_head_chunks(B, H):
         n = h1 - h0
-        heads = [(_abi.MSA_KIND_VS, 0, 0, s, scale) for s in range(n)]
+        heads = [(_abi.MSA_KIND_VS, v_ids.shape[-1], s_idx.shape[-1], s, scale) for s in range(n)]
         lists = (v_ids[:, h0:h1].contiguous(), v_cnt[:, h0:h1].contiguous(),
                  s_idx[:, h0:h1].contiguous(), s_cnt[:, h0:h1].contiguous())
         _abi.layer_attention(q[:, h0:h1], k[:, h0:h1], v[:, h0:h1], result[:, h0:h1], heads,

@@ -46,9 +46,10 @@ def test_workspace_sizes():
     # estimator: pooled Q + pooled K^T in fp32
     assert _abi.estimate_workspace_bytes(1, 32, 16384, 16384, 96) == 32 * 512 * 96 * 4
     assert _abi.estimate_workspace_bytes(1, 1, 100, 100, 64) == 1024  # 2*2*64*4 rounded to 256
-    # attention: staged K and V operands (16-bit) padded to 64 keys
-    assert _abi.attention_workspace_bytes(1, 32, 65536, 96) == 2 * 32 * 96 * 65536 * 2
-    assert _abi.attention_workspace_bytes(1, 1, 65, 64) == 2 * 64 * 128 * 2
+    # attention: staged K and V operands (16-bit) padded to 64 keys, then
+    # 256 bytes of work-queue counters
+    assert _abi.attention_workspace_bytes(1, 32, 65536, 96) == 2 * 32 * 96 * 65536 * 2 + 256
+    assert _abi.attention_workspace_bytes(1, 1, 65, 64) == 2 * 64 * 128 * 2 + 256
     assert _abi.attention_workspace_bytes(0, 1, 65, 64) == 0
 
 
