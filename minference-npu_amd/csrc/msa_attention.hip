@@ -153,23 +153,6 @@ hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st) 
 // ---------------------------------------------------------------------------
 // attention
 // ---------------------------------------------------------------------------
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-template <typename T>
-__device__ inline f32x4 mfma_qk(u32x4 a, u32x4 b, f32x4 c);
-
-template <>
-__device__ inline f32x4 mfma_qk<Bf16>(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-template <>
-__device__ inline f32x4 mfma_qk<F16>(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-
 __device__ inline f32x16 mfma_pv(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);

@@ -47,6 +47,25 @@ __device__ inline _Float16 to_f16_sat(uint16_t b) {
 
 __device__ inline u32x4 zero_u32x4() { return u32x4{0u, 0u, 0u, 0u}; }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 16x16x32 MFMA on 16-bit inputs, fp32 accumulation.  Lane l: A[l % 16][8 (l / 16) + j],
+// B[8 (l / 16) + j][l % 16], C[4 (l / 16) + i][l % 16].
+template <typename T>
+__device__ inline f32x4 mfma_qk(u32x4 a, u32x4 b, f32x4 c);
+
+template <>
+__device__ inline f32x4 mfma_qk<Bf16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <>
+__device__ inline f32x4 mfma_qk<F16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
 __device__ inline u32x4 load16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }

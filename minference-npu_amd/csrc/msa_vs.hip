@@ -206,63 +206,163 @@ hipError_t launch_vs_build(const VsBuildParams& p, int n_bs, hipStream_t st) {
 // sum rounded once to fp32; top-k ties go to the lower index.
 // ---------------------------------------------------------------------------
 
-// Scores of the n last rows against 64 key columns: 256 threads, each a 4x4
-// block of (row, column) pairs, operands in LDS as fp64.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// 16x16x16 MFMA on 16-bit inputs (16 products per output), fp32 accumulation.
+// Lane l: A[l % 16][4 (l / 16) + j], B[4 (l / 16) + j][l % 16], C as 16x16x32.
+template <typename T>
+__device__ inline f32x4 mfma16(u32x2 a, u32x2 b, f32x4 c);
+template <>
+__device__ inline f32x4 mfma16<Bf16>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                   __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+template <>
+__device__ inline f32x4 mfma16<F16>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                               __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+}
+
+// Scores of the n last rows against 64 key columns.  Wave w takes rows
+// 16w .. 16w+15; per 16-key block, S^T = K . Q^T on the MFMA (lane l: keys
+// 4 (l / 16) + i, row l % 16) as 2 D / 32 partial sums of 16 exact products
+// each (16x16x16, separate accumulators; a lane's 8 dims of a 32-dim step
+// feed two of them), added in fp32, and sum |q_d k_d| on the 16x16x32.
+// Whatever order the hardware adds in, a partial is off by at most
+// 16 2^-23 times its sum of |products| (fp32 rounding or truncation) and the
+// 2 D / 32 - 1 adds by 6 2^-23 sum |q_d k_d| more, so the total is within
+// 24 2^-23 sum |q_d k_d| (plus a term for flushed tiny values; the MFMAs keep
+// 16-bit denormals, checked on gfx950).  Rounding to the input dtype is
+// monotonic: when both ends of that interval round to the same value, it is
+// the rounding of the exact dot product (rounded to fp32 first); otherwise
+// (about 1 in 40 entries on N(0,1) data) the wave recomputes the dot
+// product exactly in fp64, 16 lanes per entry.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void vs_score_kernel(VsEstParams P) {
-  constexpr int KP = D + 1;  // padded rows (fp64): the rows a wave reads hit distinct banks
-  __shared__ double qs[kBlock * KP];
-  __shared__ double ks[kBlock * KP];
+  constexpr int NKS = D / 32;
+  constexpr int DPL = D / 16;  // dims per lane of an exact dot product
+  __shared__ int32_t flist[4][256];  // per wave: flagged (row, key) of a key block
+  __shared__ uint16_t fres[4][256];
   const int j0 = blockIdx.x * kBlock;
   const int bs = blockIdx.y;
   const int b = bs / P.n_slots;
   const int h = P.slot_heads[bs - b * P.n_slots];
   const int kvh = h / P.kv_group;
   const int tid = threadIdx.x;
+  const int lane = tid & 63, lr = lane >> 4, lc = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = P.n_rows;
+  if (16 * w >= n) return;  // no rows for this wave (S < 64)
   const uint16_t* qb = reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + int64_t(h) * P.q_sh;
   const uint16_t* kb = reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + int64_t(kvh) * P.k_sh;
-  for (int i = tid; i < kBlock * D; i += 256) {
-    const int r = i / D, d = i - r * D;
-    qs[r * KP + d] = r < n ? double(T::to_float(qb[int64_t(P.s - n + r) * P.q_ss + d])) : 0.0;
-    const int j = j0 + r;
-    ks[r * KP + d] = j < P.s ? double(T::to_float(kb[int64_t(j) * P.k_ss + d])) : 0.0;
+  const uint32_t kAbs = 0x7fff7fffu;  // clears the sign bit of both 16-bit halves
+
+  const int r = 16 * w + lc;  // this lane's row of the n last rows (B operand)
+  const uint16_t* qrow = qb + int64_t(P.s - n + min(r, n - 1)) * P.q_ss;
+  u32x4 qa[NKS], qm[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    qa[ks] = r < n ? load16(qrow + 32 * ks + 8 * lr) : zero_u32x4();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qm[ks][e] = qa[ks][e] & kAbs;
   }
-  __syncthreads();
-  const int rg = tid >> 4, cg = tid & 15;
-  double acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[i][c] = 0.0;
-  for (int d = 0; d < D; ++d) {
-    double a[4], bb[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = qs[(rg + 16 * i) * KP + d];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) bb[c] = ks[(cg + 16 * c) * KP + d];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) acc[i][c] = __builtin_fma(a[i], bb[c], acc[i][c]);
-  }
+  const float c1 = 24.0f * 0x1p-23f * 1.01f;
+  const float c0 = float(D + 2) * 0x1p-126f;
   uint16_t* xrow = P.x + int64_t(bs) * kBlock * P.s_pad;
+#pragma unroll 1
+  for (int c = 0; c < 4; ++c) {
+    const int key0 = j0 + 16 * c;
+    if (key0 >= P.s) break;
+    const int ka = min(key0 + lc, P.s - 1);  // A operand: key row of this lane
+    const uint16_t* krow = kb + int64_t(ka) * P.k_ss;
+    const f32x4 zero = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 part[2 * NKS];
+    f32x4 aacc = zero;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = rg + 16 * i;
-    if (r >= n) continue;
+    for (int ks = 0; ks < NKS; ++ks) {
+      const u32x4 kk = load16(krow + 32 * ks + 8 * lr);
+      u32x4 km;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int j = j0 + cg + 16 * c;
-      if (j >= P.s) continue;
-      uint16_t out;
-      if (j - (P.s - n) > r) {
-        out = T::from_float(-__builtin_inff());
-      } else {
-        const uint16_t a = T::from_float(float(acc[i][c]));
-        out = T::from_float(T::to_float(a) / P.sqrt_d);
+      for (int e = 0; e < 4; ++e) km[e] = kk[e] & kAbs;
+      part[2 * ks] = mfma16<T>(u32x2{kk[0], kk[1]}, u32x2{qa[ks][0], qa[ks][1]}, zero);
+      part[2 * ks + 1] = mfma16<T>(u32x2{kk[2], kk[3]}, u32x2{qa[ks][2], qa[ks][3]}, zero);
+      aacc = mfma_qk<T>(km, qm[ks], aacc);
+    }
+    // entries (key0 + 4 lr + i, row r); only existing ones are redone
+    uint16_t a16[4];
+    uint32_t redo = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = part[0][i];
+#pragma unroll
+      for (int p = 1; p < 2 * NKS; ++p) v += part[p][i];
+      // the +-bnd adds round too: 2 more 2^-23 units of sum |q_d k_d| >= |v|
+      const float bnd = __builtin_fmaf(aacc[i], c1 + 2.0f * 0x1p-23f, c0);
+      const uint16_t lo = T::from_float(v - bnd), hi = T::from_float(v + bnd);
+      a16[i] = T::from_float(v);
+      if (lo != hi && r < n && key0 + 4 * lr + i < P.s) redo |= 1u << i;
+    }
+    // ambiguous entries: a wave-wide list, 16 lanes per exact dot product
+    int pos[4], nflag = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool f = (redo >> i) & 1u;
+      const uint64_t bal = __ballot(f);
+      pos[i] = nflag + __popcll(bal & ((1ull << lane) - 1ull));
+      if (f) flist[w][pos[i]] = (r << 17) | (key0 + 4 * lr + i);
+      nflag += __popcll(bal);
+    }
+    if (nflag) {
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      const int grp = lane >> 4, sl = lane & 15;
+      for (int e0 = 0; e0 < nflag; e0 += 4) {
+        const int e = e0 + grp;
+        double dot = 0.0;
+        if (e < nflag) {
+          const int code = flist[w][e];
+          const uint16_t* qe = qb + int64_t(P.s - n + (code >> 17)) * P.q_ss + DPL * sl;
+          const uint16_t* ke = kb + int64_t(code & 0x1ffff) * P.k_ss + DPL * sl;
+#pragma unroll
+          for (int d = 0; d < DPL; d += 2) {
+            const uint32_t qw = *reinterpret_cast<const uint32_t*>(qe + d);
+            const uint32_t kw = *reinterpret_cast<const uint32_t*>(ke + d);
+            dot = __builtin_fma(double(T::to_float(uint16_t(qw & 0xffffu))),
+                                double(T::to_float(uint16_t(kw & 0xffffu))), dot);
+            dot = __builtin_fma(double(T::to_float(uint16_t(qw >> 16))),
+                                double(T::to_float(uint16_t(kw >> 16))), dot);
+          }
+        }
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
+        if (sl == 0 && e < nflag) fres[w][e] = T::from_float(float(dot));
       }
-      xrow[int64_t(r) * P.s_pad + j] = out;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if ((redo >> i) & 1u) a16[i] = fres[w][pos[i]];
+      __builtin_amdgcn_wave_barrier();  // list reused by the next key block
+    }
+    if (r < n) {
+      uint16_t out[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = key0 + 4 * lr + i;
+        out[i] = j - (P.s - n) > r ? T::from_float(-__builtin_inff())
+                                   : T::from_float(T::to_float(a16[i]) / P.sqrt_d);
+      }
+      uint16_t* dst = xrow + int64_t(r) * P.s_pad + key0 + 4 * lr;
+      if (key0 + 4 * lr + 3 < P.s) {  // 4 keys, 8-byte aligned (s_pad and key0 + 4 lr are)
+        *reinterpret_cast<uint2*>(dst) = uint2{uint32_t(out[0]) | (uint32_t(out[1]) << 16),
+                                               uint32_t(out[2]) | (uint32_t(out[3]) << 16)};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (key0 + 4 * lr + i < P.s) dst[i] = out[i];
+      }
     }
   }
 }
@@ -303,29 +403,41 @@ __global__ __launch_bounds__(256) void vs_rowstat_kernel(VsEstParams P) {
 }
 
 // Column sums and diagonal sums of p, rounded to fp32, with the forced
-// entries set to +inf.
+// entries set to +inf.  Thread t of a block owns column / diagonal
+// c0 + t; row by row, the block forms p for columns [c0 - 63, c0 + 256)
+// once in LDS, and each thread adds its column's p and its diagonal's p
+// (column t + 1 - n + r), rows in order r = 0 .. n-1.
 template <typename T>
 __global__ __launch_bounds__(256) void vs_sums_kernel(VsEstParams P) {
+  constexpr int W = 256 + kBlock - 1;  // columns one block needs per row
   __shared__ double sm[kBlock], sl[kBlock];
+  __shared__ double prow[W];
   const int bs = blockIdx.y;
   const int n = P.n_rows;
-  if (threadIdx.x < n) {
-    sm[threadIdx.x] = double(P.rmax[bs * kBlock + threadIdx.x]);
-    sl[threadIdx.x] = P.rsum[bs * kBlock + threadIdx.x];
+  const int tid = threadIdx.x;
+  if (tid < n) {
+    sm[tid] = double(P.rmax[bs * kBlock + tid]);
+    sl[tid] = P.rsum[bs * kBlock + tid];
   }
-  __syncthreads();
-  const int t = blockIdx.x * 256 + threadIdx.x;
-  if (t >= P.s) return;
+  const int c0 = blockIdx.x * 256;
+  const int t = c0 + tid;
   const uint16_t* x = P.x + int64_t(bs) * kBlock * P.s_pad;
   double cv = 0.0, cs = 0.0;
   for (int r = 0; r < n; ++r) {
-    const double p = exp(double(T::to_float(x[int64_t(r) * P.s_pad + t])) - sm[r]) / sl[r];
-    cv += p;
+    __syncthreads();  // previous row consumed (and sm / sl written)
+    for (int idx = tid; idx < W; idx += 256) {
+      const int col = c0 - (kBlock - 1) + idx;
+      prow[idx] = (col >= 0 && col < P.s)
+                      ? exp(double(T::to_float(x[int64_t(r) * P.s_pad + col])) - sm[r]) / sl[r]
+                      : 0.0;
+    }
+    __syncthreads();
+    if (t < P.s) {
+      cv += prow[tid + kBlock - 1];
+      if (r >= n - 1 - t) cs += prow[tid + kBlock - 1 + 1 - n + r];
+    }
   }
-  for (int r = max(0, n - 1 - t); r < n; ++r) {
-    const int j = t + 1 - n + r;
-    cs += exp(double(T::to_float(x[int64_t(r) * P.s_pad + j])) - sm[r]) / sl[r];
-  }
+  if (t >= P.s) return;
   float fv = float(cv), fs = float(cs);
   if (t < 30) fv = __builtin_inff();
   if (t >= P.s - 100) fs = __builtin_inff();
@@ -333,64 +445,84 @@ __global__ __launch_bounds__(256) void vs_sums_kernel(VsEstParams P) {
   P.slash[int64_t(bs) * P.s + t] = fs;
 }
 
-// Top-k of one score row (z = 0: vertical, z = 1: slash): 4-pass MSD radix
-// select of the k-th largest key (non-negative floats order like their
-// bits), then the keys above it and the lowest-index keys equal to it, in
-// index order.
-__global__ __launch_bounds__(256) void vs_topk_kernel(VsEstParams P) {
-  __shared__ int hist[256];
-  __shared__ int sel[2];  // digit, remaining rank
-  __shared__ int scratch[4];
+// Block-wide exclusive prefix of a 0/1 flag over NT threads (see
+// block_prefix).
+template <int NT>
+__device__ inline int block_prefix_n(bool flag, int* scratch, int* total) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint64_t bal = __ballot(flag);
+  const int in_wave = __popcll(bal & ((1ull << lane) - 1ull));
+  if (lane == 0) scratch[w] = __popcll(bal);
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    before += v < w ? scratch[v] : 0;
+    all += scratch[v];
+  }
+  __syncthreads();
+  *total = all;
+  return before + in_wave;
+}
+
+// Top-k of one score row (y = 0: vertical, y = 1: slash): the k-th largest
+// key T by a 32-step bitwise search (the largest T with at least k keys >= T;
+// non-negative floats order like their bits), counting with wave ballots
+// (no atomics: the keys share their leading bits), then every key above T and
+// the lowest-index keys equal to T, in index order.  The first 64K keys stay
+// in registers across the passes.
+constexpr int kTopkThreads = 1024;
+constexpr int kTopkRegs = 64;  // keys per thread held in registers
+
+__global__ __launch_bounds__(kTopkThreads) void vs_topk_kernel(VsEstParams P) {
+  __shared__ int scratch[kTopkThreads / 64];
   const int bs = blockIdx.x;
   const int slot = bs % P.n_slots;
   const bool is_slash = blockIdx.y == 1;
   const uint32_t* keys = reinterpret_cast<const uint32_t*>(is_slash ? P.slash : P.vert) +
                          int64_t(bs) * P.s;
   const int kk0 = is_slash ? P.slot_ssize[slot] : P.slot_vsize[slot];
-  const int tid = threadIdx.x;
-  uint32_t prefix = 0u, mask = 0u;
-  int kk = kk0;
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
-    hist[tid] = 0;
-    __syncthreads();
-    for (int i = tid; i < P.s; i += 256) {
-      const uint32_t key = keys[i];
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      int cum = 0, digit = 0;
-      for (int d = 255; d >= 0; --d) {
-        if (cum + hist[d] >= kk) {
-          digit = d;
-          break;
-        }
-        cum += hist[d];
-      }
-      sel[0] = digit;
-      sel[1] = kk - cum;
-    }
-    __syncthreads();
-    prefix |= uint32_t(sel[0]) << shift;
-    mask |= 255u << shift;
-    kk = sel[1];
-    __syncthreads();
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  uint32_t kr[kTopkRegs];
+#pragma unroll
+  for (int m = 0; m < kTopkRegs; ++m) {
+    const int i = tid + kTopkThreads * m;
+    kr[m] = i < P.s ? keys[i] : 0u;  // 0 never counts: candidates are >= 1
   }
-  // prefix = the k-th largest key; take every key above it and the first kk
-  // keys equal to it
+  auto count_ge = [&](uint32_t c) -> int {
+    int cnt = 0;
+#pragma unroll
+    for (int m = 0; m < kTopkRegs; ++m) cnt += int(kr[m] >= c);
+    for (int i = tid + kTopkThreads * kTopkRegs; i < P.s; i += kTopkThreads) cnt += int(keys[i] >= c);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    if (lane == 0) scratch[w] = cnt;
+    __syncthreads();
+    int all = 0;
+#pragma unroll
+    for (int v = 0; v < kTopkThreads / 64; ++v) all += scratch[v];
+    __syncthreads();
+    return all;
+  };
+  uint32_t t = 0u;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = t | (1u << bit);
+    if (count_ge(cand) >= kk0) t = cand;
+  }
+  const int need_eq = kk0 - count_ge(t + 1u);  // keys equal to t to take
   int32_t* out = is_slash ? P.s_idx + int64_t(bs) * P.s_stride : P.v_idx + int64_t(bs) * P.v_stride;
   int taken = 0, eq_seen = 0;
-  for (int i0 = 0; i0 < P.s; i0 += 256) {
+  for (int i0 = 0; i0 < P.s; i0 += kTopkThreads) {
     const int i = i0 + tid;
     const uint32_t key = i < P.s ? keys[i] : 0u;
-    const bool gt = i < P.s && key > prefix;
-    const bool eq = i < P.s && key == prefix;
+    const bool gt = i < P.s && key > t;
+    const bool eq = i < P.s && key == t;
     int n_eq;
-    const int eq_rank = eq_seen + block_prefix(eq, scratch, &n_eq);
-    const bool take = gt || (eq && eq_rank < kk);
+    const int eq_rank = eq_seen + block_prefix_n<kTopkThreads>(eq, scratch, &n_eq);
+    const bool take = gt || (eq && eq_rank < need_eq);
     int n_take;
-    const int pos = taken + block_prefix(take, scratch, &n_take);
+    const int pos = taken + block_prefix_n<kTopkThreads>(take, scratch, &n_take);
     if (take) out[pos] = is_slash ? P.s - 1 - i : i;
     taken += n_take;
     eq_seen += n_eq;
@@ -410,7 +542,7 @@ static hipError_t launch_vs_est_t(const VsEstParams& p, hipStream_t st) {
   hipLaunchKernelGGL((vs_sums_kernel<T>), dim3((p.s + 255) / 256, n_bs), dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(vs_topk_kernel, dim3(n_bs, 2), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(vs_topk_kernel, dim3(n_bs, 2), dim3(kTopkThreads), 0, st, p);
   return hipGetLastError();
 }
 
