@@ -284,8 +284,9 @@ def minference_forward():
             key, value = past_key_values.update(key, value, self.layer_idx)
 
         if self.is_search:
-            warnings.warn("is_search=True is not supported by the MI355X build; running the "
-                          "configured patterns", stacklevel=2)
+            # reference :374-382 warns and :392-396 runs the layer dense
+            warnings.warn("is_search=True: no pattern search runs; the layer runs dense "
+                          "attention", stacklevel=2)
 
         # output written in [B, S, H, D] order; the kernel sees a [B, H, S, D] view
         out_bshd = torch.empty((bsz, q_len, n_heads, hd), dtype=query.dtype,
@@ -295,7 +296,8 @@ def minference_forward():
             # decode: one query row sees the whole cache (reference :488-490)
             run_decode_attention(query, key, value, out, dense_scale(hd))
         else:
-            if self._minference_attn_type == "dense" or self.layer_idx < self.starting_layer:
+            if (self._minference_attn_type == "dense" or self.layer_idx < self.starting_layer
+                    or self.is_search):
                 plan = dense_plan(n_heads, hd)
             else:
                 plan = _layer_plan(self, n_heads, hd, key.shape[2])

@@ -11,6 +11,8 @@ registered attention function run the HIP dense kernel.
 
 from __future__ import annotations
 
+import json
+import os
 import warnings
 from typing import Any
 
@@ -68,6 +70,25 @@ def register_attention_implementation() -> str:
     return ATTN_IMPL
 
 
+def _check_pattern_file(config: Any, model_config: Any) -> None:
+    """Validate the pattern file against the model's layer and head counts
+    once, at patch time.  Problems are warnings, not errors: the reference
+    dispatcher reads the file lazily per layer (minference_forward.py:187-198)
+    and fails, if at all, only in the forward that reaches the bad record."""
+    path = getattr(config, "config_path", "")
+    if getattr(config, "attn_type", "") != "minference" or not path or not os.path.exists(path):
+        return
+    from .configs.patterns import PatternConfigError, validate_config
+
+    try:
+        with open(path) as f:
+            cfg = json.load(f)
+        validate_config(cfg, getattr(model_config, "num_hidden_layers", None),
+                        getattr(model_config, "num_attention_heads", None), where=path)
+    except (ValueError, PatternConfigError) as e:
+        warnings.warn(f"pattern file check failed: {e}", stacklevel=3)
+
+
 def minference_patch(model: torch.nn.Module, config: Any) -> torch.nn.Module:
     """Bind the MI355X minference forward onto ``model.model.layers[*].self_attn``.
 
@@ -84,6 +105,7 @@ def minference_patch(model: torch.nn.Module, config: Any) -> torch.nn.Module:
 
     AttentionClass = attention_module.__class__
     forward_closure = minference_forward()
+    _check_pattern_file(config, model.config)
 
     model.config.starting_layer = config.starting_layer
     model.config.config_path = config.config_path

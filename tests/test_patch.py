@@ -239,3 +239,40 @@ def test_vertical_and_slash_needs_full_prefill():
     k = torch.zeros(1, 1, 300, 96, dtype=torch.bfloat16)
     with pytest.raises(AssertionError):
         MF._vs_lists(q, k, plan)
+
+
+def test_patch_time_pattern_check_warns(tmp_path):
+    """The pattern file is validated against the model once at patch time;
+    problems warn (the reference only fails in the forward that reaches a bad
+    record) and a clean file is silent."""
+    import warnings
+
+    bad = tmp_path / "bad.json"
+    P.write(str(bad), [{"0": ["stream_llm", 16, 64, 1.0], "5": ["dense", 0, 0, 1.0]}] * 3)
+    with pytest.warns(UserWarning, match=r"head 5 >= 2 heads.*|3 layers, the model has 2"):
+        patch_hf(_tiny_phi3(), "minference", {"config_path": str(bad)})
+    good = tmp_path / "good.json"
+    P.write(str(good), P.uniform_config("block_sparse", 4, n_layers=2, n_heads=2))
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        patch_hf(_tiny_phi3(), "minference", {"config_path": str(good)})
+
+
+def test_is_search_runs_layers_dense(tmp_path, monkeypatch):
+    """is_search=True warns and runs every layer dense (reference
+    minference_forward.py:374-382, :392-396), whatever the pattern file says."""
+    seen = []
+
+    def spy(q, k, v, plan, out):
+        seen.append(plan)
+        return _oracle_launch(q, k, v, plan, out)
+
+    monkeypatch.setattr(MF, "run_layer_attention", spy)
+    path = tmp_path / "mix.json"
+    P.write(str(path), [{"0": ["stream_llm", 16, 64, 1.0], "1": ["block_sparse", 2, 0, 1.0]}] * 2)
+    patched = MInference(attn_type="minference", config_path=str(path), is_search=True)(_tiny_phi3())
+    ids = torch.randint(3, 128, (1, 100), generator=torch.Generator().manual_seed(5))
+    with pytest.warns(UserWarning, match="is_search"), torch.no_grad():
+        patched(ids)
+    assert len(seen) == 2 and all(p.all_dense for p in seen)
+    assert seen[0].heads[0][4] == 1.0 / math.sqrt(96)
