@@ -16,7 +16,8 @@ the attention kernel alone (HIP events on the launch stream) against the
 bf16 MFMA peak; dense = same-GPU dense attention on the same tensors
 (PyTorch SDPA flash and this build's dense kind); cpu_baseline = the oracle's
 stream_llm restatement of the reference CPU path timed on
-the host cores.
+the host cores; decode = one decode step against the layer's K/V cache;
+rope = the fused RoPE kernel on the layer's q and k against HF's eager one.
 """
 
 from __future__ import annotations
@@ -74,6 +75,7 @@ def parse_args():
     ap.add_argument("--no-dense", action="store_true", help="skip the same-GPU dense baselines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
+    ap.add_argument("--no-rope", action="store_true", help="skip the RoPE measurement")
     ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads of BASELINE config 1 timed on the CPU (scaled to 32)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -336,6 +338,8 @@ def main():
 
     if not args.no_decode:
         result["decode"] = decode_bench(k, v, S, H, D, args.seed)
+    if not args.no_rope:
+        result["rope"] = rope_bench(S, H, D, args.seed)
     if not args.no_dense:
         result["dense"] = dense_baselines(q, k, v, S, H, D, ms_step)
     if not args.no_cpu:
@@ -512,6 +516,52 @@ def decode_bench(k, v, S, H, D, seed, reps=20):
     return {"s_k": S, "heads": H, "us_per_layer": round(us, 2), "kv_bytes": nbytes,
             "hbm_gbps": round(gbps, 1), "frac_hbm_peak": round(gbps / PEAK_HBM_GBPS, 4),
             "kernels": "msa::decode_kernel + msa::decode_combine_kernel"}
+
+
+def rope_bench(S, H, D, seed, reps=10):
+    """RoPE of one layer's q and k (msa_rope_qk, in place on the views of a
+    fused qkv projection output, as the patched forward runs it) against the
+    eager HF apply_rotary_pos_emb on the same views, HIP events on the launch
+    stream.  Algorithmic bytes: q and k read and written once, plus the
+    cos/sin tables."""
+    import torch
+
+    from minference.ops.rope import apply_rotary_pos_emb
+    from transformers.models.phi3.modeling_phi3 import apply_rotary_pos_emb as hf_rope
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed + 11)
+    qkv = torch.randn((1, S, 3 * H * D), generator=g, device=dev).to(torch.bfloat16)
+    q = qkv[..., :H * D].view(1, S, H, D).transpose(1, 2)
+    k = qkv[..., H * D:2 * H * D].view(1, S, H, D).transpose(1, 2)
+    inv = 1.0 / (1e4 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
+    f = torch.arange(S, device=dev, dtype=torch.float32)[:, None] * inv[None]
+    emb = torch.cat([f, f], -1)[None]
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reps)]
+        torch.cuda.synchronize()
+        for i in range(reps):
+            ev[2 * i].record(stream)
+            fn()
+            ev[2 * i + 1].record(stream)
+        torch.cuda.synchronize()
+        return sum(ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(reps)) / reps
+
+    ms = timed(lambda: apply_rotary_pos_emb(q, k, cos, sin, inplace=True))
+    ms_hf = timed(lambda: hf_rope(q, k, cos, sin))
+    nbytes = 2 * (2 * S * H * D * 2) + 2 * S * D * 2
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    del qkv
+    torch.cuda.empty_cache()
+    return {"s": S, "heads": H, "ms_per_layer": round(ms, 4), "bytes": nbytes,
+            "hbm_gbps": round(gbps, 1), "frac_hbm_peak": round(gbps / PEAK_HBM_GBPS, 4),
+            "hf_eager_ms": round(ms_hf, 4), "speedup_vs_hf_eager": round(ms_hf / ms, 2),
+            "kernel": "msa::rope_kernel<Bf16>"}
 
 
 def dense_baselines(q, k, v, S, H, D, ms_sparse):

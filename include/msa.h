@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MSA_ABI_VERSION 4
+#define MSA_ABI_VERSION 5
 
 /* status codes (negative: validation, nothing launched) */
 #define MSA_OK 0
@@ -251,6 +251,25 @@ size_t msa_decode_workspace_bytes(int64_t batch, int64_t heads, int64_t s_k, int
 int msa_decode_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
                          const msa_tensor4* o, float scale, void* workspace,
                          size_t workspace_bytes, msa_stream_t stream);
+
+/* Rotary position embedding of one layer's query and key heads, one launch.
+ * Replaces the apply_rotary_pos_emb call of the patched forward
+ * (minference/modules/minference_forward.py:336-341, HF's rotate-half RoPE):
+ *   out[:rot/2]    = q[:rot/2] * cos[:rot/2] - q[rot/2:rot] * sin[:rot/2]
+ *   out[rot/2:rot] = q[rot/2:rot] * cos[rot/2:] + q[:rot/2] * sin[rot/2:]
+ *   out[rot:]      = q[rot:]                       (partial rotary)
+ * with every product and sum rounded to the input dtype as the eager
+ * elementwise ops round them, so the result is bit-identical to
+ * q * cos + rotate_half(q) * sin.  Same for k.
+ *   q [B][H][S][D], k [B][H_kv][S][D]: views (e.g. of a fused qkv projection)
+ *   cos, sin [B or 1][1][S][rot]: the position tables (a batch size of 1
+ *     broadcasts); rot % 16 == 0, rot <= min(D, 256), D % 8 == 0, D <= 512
+ *   q_out, k_out: same shapes; may be q / k themselves (in place), must not
+ *     overlap them otherwise
+ * All bf16 or all fp16, D contiguous, 16-byte aligned rows. */
+int msa_rope_qk(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* cos,
+                const msa_tensor4* sin, const msa_tensor4* q_out, const msa_tensor4* k_out,
+                msa_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -708,4 +708,52 @@ int msa_decode_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_t
   return e == hipSuccess ? MSA_OK : int(e);
 }
 
+int msa_rope_qk(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* cos,
+                const msa_tensor4* sin, const msa_tensor4* q_out, const msa_tensor4* k_out,
+                msa_stream_t stream) {
+  const msa_tensor4* all[6] = {q, k, cos, sin, q_out, k_out};
+  for (const msa_tensor4* t : all) {
+    if (!t || !t->data) return MSA_E_NULL;
+    for (int i = 0; i < 4; ++i)
+      if (t->size[i] <= 0) return MSA_E_RANK;
+  }
+  const int64_t B = q->size[0], H = q->size[1], S = q->size[2], D = q->size[3];
+  const int64_t Hkv = k->size[1], rot = cos->size[3];
+  if (k->size[0] != B || k->size[2] != S || k->size[3] != D) return MSA_E_RANK;
+  for (int i = 0; i < 4; ++i)
+    if (q_out->size[i] != q->size[i] || k_out->size[i] != k->size[i] ||
+        sin->size[i] != cos->size[i])
+      return MSA_E_RANK;
+  if ((cos->size[0] != 1 && cos->size[0] != B) || cos->size[1] != 1 || cos->size[2] != S)
+    return MSA_E_RANK;
+  if (q->dtype != MSA_DTYPE_BF16 && q->dtype != MSA_DTYPE_FP16) return MSA_E_DTYPE;
+  for (const msa_tensor4* t : all)
+    if (t->dtype != q->dtype) return MSA_E_DTYPE;
+  if (D % 8 != 0 || D > 512 || rot % 16 != 0 || rot > D || rot > kRopeMaxRot)
+    return MSA_E_HEAD_DIM;
+  for (const msa_tensor4* t : all)
+    if (!aligned(t)) return MSA_E_ALIGN;
+  const int64_t n_pair = rot / 16, n_pass = (D - rot) / 8;
+  if (H + Hkv > 65535 || S > kMaxSeq || B > 65535)
+    return MSA_E_SEQ;
+
+  RopeParams rp;
+  memset(&rp, 0, sizeof(rp));
+  rp.q = q->data; rp.k = k->data; rp.cos = cos->data; rp.sin = sin->data;
+  rp.qo = q_out->data; rp.ko = k_out->data;
+  rp.q_sb = q->stride[0]; rp.q_sh = q->stride[1]; rp.q_ss = q->stride[2];
+  rp.k_sb = k->stride[0]; rp.k_sh = k->stride[1]; rp.k_ss = k->stride[2];
+  rp.qo_sb = q_out->stride[0]; rp.qo_sh = q_out->stride[1]; rp.qo_ss = q_out->stride[2];
+  rp.ko_sb = k_out->stride[0]; rp.ko_sh = k_out->stride[1]; rp.ko_ss = k_out->stride[2];
+  rp.c_sb = cos->size[0] == 1 ? 0 : cos->stride[0];
+  rp.c_ss = cos->stride[2];
+  rp.n_sb = sin->size[0] == 1 ? 0 : sin->stride[0];
+  rp.n_ss = sin->stride[2];
+  rp.batch = int(B); rp.heads = int(H); rp.kv_heads = int(Hkv); rp.s = int(S);
+  rp.rot = int(rot); rp.half = int(rot / 2);
+  rp.n_pair = int(n_pair); rp.n_pass = int(n_pass);
+  const hipError_t e = launch_rope(rp, q->dtype, reinterpret_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSA_OK : int(e);
+}
+
 }  // extern "C"

@@ -151,6 +151,28 @@ struct DecodeParams {
   float* ml;           // workspace [batch*heads][n_split][2]: (m, l) per split
 };
 
+// Rotary embedding of one layer's q and k heads (rope_kernel).  q/k/qo/ko
+// strides are [B][H][S][D] element strides; cos/sin are [B or 1][S][rot]
+// (c_sb / n_sb = 0 broadcasts one table over the batch).  n_pair = rot / 16
+// chunk pairs and n_pass = (D - rot) / 8 copied chunks per head row.
+struct RopeParams {
+  const void* q;
+  const void* k;
+  const void* cos;
+  const void* sin;
+  void* qo;
+  void* ko;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t qo_sb, qo_sh, qo_ss;
+  int64_t ko_sb, ko_sh, ko_ss;
+  int64_t c_sb, c_ss, n_sb, n_ss;
+  int batch, heads, kv_heads, s, rot, half, n_pair, n_pass;
+};
+
+// Widest rotary part msa_rope_qk takes (its cos/sin rows are staged in LDS).
+constexpr int kRopeMaxRot = 256;
+
 // Most splits a decode call uses (one head alone gets this many).
 constexpr int kDecodeMaxSplit = 2048;
 
@@ -166,5 +188,6 @@ hipError_t launch_attention_vs(const AttnParams& p, int dtype, int out_dtype, in
                                hipStream_t st);
 hipError_t launch_vs_build(const VsBuildParams& p, int n_bs, hipStream_t st);
 hipError_t launch_vs_estimate(const VsEstParams& p, int dtype, int D, hipStream_t st);
+hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t st);
 
 }  // namespace msa

@@ -43,7 +43,7 @@ MSA_VS_MAX_SEQ = 131072
 
 MSA_MAX_HEADS = 128
 MSA_BLOCK = 64
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _DTYPE_CODE = {
     torch.bfloat16: MSA_DTYPE_BF16,
@@ -67,6 +67,7 @@ EXPORTED_SYMBOLS = (
     "msa_layer_attention_ex",
     "msa_vs_estimate_workspace_bytes",
     "msa_vs_estimate",
+    "msa_rope_qk",
 )
 
 
@@ -206,6 +207,8 @@ def load_library() -> ctypes.CDLL:
             ctypes.POINTER(MsaVsLists), ctypes.c_void_p, ctypes.c_size_t,
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_void_p,
         ]
+        lib.msa_rope_qk.restype = ctypes.c_int
+        lib.msa_rope_qk.argtypes = [ctypes.POINTER(MsaTensor4)] * 6 + [ctypes.c_void_p]
         ver = lib.msa_abi_version()
         if ver != ABI_VERSION:
             raise ImportError(f"libmsa ABI version {ver} != expected {ABI_VERSION}")
@@ -282,6 +285,16 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: tor
     check(load_library().msa_decode_attention(
         ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ctypes.byref(od), float(scale),
         ws.data_ptr(), ws.numel(), current_stream_handle(q.device)))
+
+
+def rope_qk(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+            q_out: torch.Tensor, k_out: torch.Tensor) -> None:
+    """Launch msa_rope_qk on the current stream: q [B,H,S,D], k [B,H_kv,S,D],
+    cos/sin [B or 1, 1, S, rot] views; q_out/k_out may be q/k (in place)."""
+    require_device(q, k, cos, sin, q_out, k_out)
+    ds = [tensor4(t) for t in (q, k, cos, sin, q_out, k_out)]
+    check(load_library().msa_rope_qk(*[ctypes.byref(d) for d in ds],
+                                     current_stream_handle(q.device)))
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:

@@ -18,7 +18,8 @@ CSRC_DIR = os.path.join(os.path.dirname(PKG_DIR), "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmsa.so")
 
-SOURCES = ("msa_abi.hip", "msa_estimator.hip", "msa_attention.hip", "msa_decode.hip", "msa_vs.hip")
+SOURCES = ("msa_abi.hip", "msa_estimator.hip", "msa_attention.hip", "msa_decode.hip", "msa_vs.hip",
+           "msa_rope.hip")
 
 HIPCC_FLAGS = (
     "--offload-arch=gfx950",

@@ -27,6 +27,7 @@ import torch
 
 from .. import _abi
 from ..ops.common import dense_scale, sparse_scale
+from ..ops.rope import apply_rotary_pos_emb as apply_rotary_pos_emb_gpu, rope_supported
 from ..ops.vertical_slash_kernel import vs_sizes
 
 __all__ = [
@@ -234,6 +235,15 @@ def _layer_plan(self, n_heads: int, head_dim: int, s_k: int) -> LayerPlan:
 
 
 def _apply_rope(self, q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    """RoPE of the layer's fresh q/k projections (reference :205-212, :336-341).
+
+    On the GPU the one-pass HIP kernel rotates q and k in place (they are
+    views of this forward's own projection outputs), bit-identical to the
+    model's eager function.  Other inputs (CPU tensors of the host-side
+    tests, tables the kernel does not take) go to the model module's
+    ``apply_rotary_pos_emb``."""
+    if rope_supported(q, k, cos, sin):
+        return apply_rotary_pos_emb_gpu(q, k, cos, sin, inplace=True)
     from importlib import import_module
 
     rope = getattr(import_module(self.__class__.__module__), "apply_rotary_pos_emb")

@@ -25,6 +25,10 @@ something other than its own formula):
   block_sparse_from_indices : full top-k equals causal dense; Q = 0 closed form;
                         per-row brute force over the expanded token set
   dense_causal        : torch scaled_dot_product_attention(is_causal=True) in fp64
+  rope_rotate_half    : HF Phi-3's apply_rotary_pos_emb on CPU torch in bf16 / fp16
+                        (the call the reference makes), bit for bit, full and
+                        partial rotary; in fp64 a norm-preserving rotation of
+                        the (i, i + rot/2) pairs
 """
 
 from __future__ import annotations
@@ -62,6 +66,7 @@ __all__ = [
     "stream_pairs",
     "block_tiles",
     "causal_pairs",
+    "rope_rotate_half",
 ]
 
 BLOCK = 64
@@ -119,6 +124,29 @@ def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
     if dtype == "fp32":
         return np.asarray(x, dtype=np.float32)
     raise ValueError(dtype)
+
+
+# ---------------------------------------------------------------------------
+# rotary embedding (minference_forward.py:205-212 looks up the model module's
+# apply_rotary_pos_emb, :336-341 calls it; HF Phi-3 / Llama rotate-half form)
+# ---------------------------------------------------------------------------
+def rope_rotate_half(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, dtype: str) -> np.ndarray:
+    """x * cos + rotate_half(x) * sin on the first rot = cos.shape[-1] dims,
+    the rest passed through, with the eager op-by-op rounding of 16-bit
+    tensors: each product and the sum are computed in fp32 and rounded to
+    ``dtype``.  x [B, H, S, D]; cos, sin [B or 1, S, rot]; all float32
+    holding ``dtype`` values."""
+    x = np.asarray(x, dtype=np.float32)
+    c = np.asarray(cos, dtype=np.float32)[:, None]
+    s = np.asarray(sin, dtype=np.float32)[:, None]
+    rot = c.shape[-1]
+    half = rot // 2
+    x1, x2 = x[..., :half], x[..., half:rot]
+    r = lambda a: round_to(a, dtype)  # noqa: E731
+    out = x.copy()
+    out[..., :half] = r(r(x1 * c[..., :half]) - r(x2 * s[..., :half]))
+    out[..., half:rot] = r(r(x2 * c[..., half:]) + r(x1 * s[..., half:]))
+    return out
 
 
 # ---------------------------------------------------------------------------

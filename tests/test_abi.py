@@ -201,6 +201,41 @@ def test_decode_workspace_sizes():
     assert _abi.decode_workspace_bytes(1, 1, 0, 96) == 0
 
 
+def rope(q, k, c, s, qo, ko):
+    lib = _abi.load_library()
+    return lib.msa_rope_qk(*[ctypes.byref(x) for x in (q, k, c, s, qo, ko)], None)
+
+
+RQ, RK, RC = [2, 8, 300, 96], [2, 2, 300, 96], [1, 1, 300, 96]
+
+
+@pytest.mark.parametrize(
+    "mutate,expected",
+    [
+        (lambda a: a.__setitem__("k", t4([2, 2, 299, 96])) or a.__setitem__("ko", t4([2, 2, 299, 96])), _abi.MSA_E_RANK),
+        (lambda a: a.__setitem__("qo", t4([2, 8, 300, 64])), _abi.MSA_E_RANK),
+        (lambda a: a.__setitem__("c", t4([3, 1, 300, 96])) or a.__setitem__("s", t4([3, 1, 300, 96])), _abi.MSA_E_RANK),
+        (lambda a: a.__setitem__("c", t4([1, 2, 300, 96])) or a.__setitem__("s", t4([1, 2, 300, 96])), _abi.MSA_E_RANK),
+        (lambda a: a.__setitem__("s", t4([1, 1, 300, 64])), _abi.MSA_E_RANK),
+        (lambda a: a.__setitem__("c", t4([1, 1, 300, 40])) or a.__setitem__("s", t4([1, 1, 300, 40])), _abi.MSA_E_HEAD_DIM),
+        (lambda a: a.__setitem__("c", t4([1, 1, 300, 112])) or a.__setitem__("s", t4([1, 1, 300, 112])), _abi.MSA_E_HEAD_DIM),
+        (lambda a: [a.__setitem__(n, t4([2, 8, 300, 36])) for n in ("q", "qo")]
+         and [a.__setitem__(n, t4([2, 2, 300, 36])) for n in ("k", "ko")]
+         and [a.__setitem__(n, t4([1, 1, 300, 16])) for n in ("c", "s")], _abi.MSA_E_HEAD_DIM),
+        (lambda a: a.__setitem__("q", t4(RQ, _abi.MSA_DTYPE_FP16)), _abi.MSA_E_DTYPE),
+        (lambda a: [a.__setitem__(n, t4(sh, _abi.MSA_DTYPE_FP32)) for n, sh in
+                    (("q", RQ), ("k", RK), ("c", RC), ("s", RC), ("qo", RQ), ("ko", RK))], _abi.MSA_E_DTYPE),
+        (lambda a: a.__setitem__("c", t4(RC, data=FAKE + 4)), _abi.MSA_E_ALIGN),
+        (lambda a: a.__setitem__("ko", t4(RK, strides=[300 * 96 * 2, 300 * 96, 99, 1])), _abi.MSA_E_ALIGN),
+        (lambda a: a.__setitem__("qo", t4(RQ, data=0)), _abi.MSA_E_NULL),
+    ],
+)
+def test_rope_validation(mutate, expected):
+    a = {"q": t4(RQ), "k": t4(RK), "c": t4(RC), "s": t4(RC), "qo": t4(RQ), "ko": t4(RK)}
+    mutate(a)
+    assert rope(a["q"], a["k"], a["c"], a["s"], a["qo"], a["ko"]) == expected
+
+
 def test_python_ops_refuse_cpu_tensors():
     import torch
 
@@ -221,3 +256,8 @@ def test_python_ops_refuse_cpu_tensors():
         decode_dense(q[:, :, :1], q, q)
     with pytest.raises(NotImplementedError):
         decode_dense(q, q, q)
+    from minference.ops.rope import apply_rotary_pos_emb
+
+    cos = torch.zeros(1, 128, 96, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        apply_rotary_pos_emb(q, q, cos, cos)
