@@ -48,6 +48,17 @@ WORKLOADS = {
     "cfg2_block16k": (16384, 0, 32, 0, 128, 4096, 100),
     "cfg3_stream64k": (65536, 32, 0, 0, 128, 4096, 100),
     "vs64k": (65536, 0, 0, 0, 0, 0, 0),  # VS_MIX below
+    # full-model prefill (BASELINE configs 4 and 5): (S, mix) in MODEL_MIX
+    "cfg4_prefill32k": (32768, 0, 0, 0, 0, 0, 0),
+    "cfg5_prefill128k": (131072, 0, 0, 0, 0, 0, 0),
+}
+
+# Per-head pattern mixes of the full-prefill workloads over all 1024 heads,
+# drawn by configs.patterns.mixed_config from the bench seed.
+MODEL_MIX = {
+    "cfg4_prefill32k": [(0.3, ["stream_llm", 128, 4096]), (0.6, ["block_sparse", 100, 0]),
+                        (0.1, ["dense", 0, 0])],
+    "cfg5_prefill128k": [(0.5, ["stream_llm", 128, 8192]), (0.5, ["block_sparse", 160, 0])],
 }
 
 # The reference's original Phi-3 pattern (1024 heads: vertical_and_slash
@@ -219,6 +230,8 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload == "vs64k":
         return vs_bench(args, dev)
+    if args.workload in MODEL_MIX:
+        return model_bench(args, dev)
     S, n_stream, n_block, n_dense, n_init, n_local, topk = WORKLOADS[args.workload]
     H, D = args.heads, args.dim
     scale_h = H / (n_stream + n_block + n_dense)
@@ -378,6 +391,124 @@ def vs_tiles(v_idx, s_idx, S):
         if gath.any():
             total += len(np.unique(np.nonzero(gath)[0] // BLOCK))
     return total
+
+
+def phi3_mini_128k(dev, n_layers=32):
+    """Random-init Phi-3-mini-128k-shaped model in bf16 on ``dev``: 32 layers,
+    hidden 3072, 32 heads x 96, MLP 8192, vocab 32064, LongRoPE tables (the
+    checkpoint's factor lists are not available offline; their values do not
+    change the work)."""
+    import torch
+    from transformers import Phi3Config, Phi3ForCausalLM
+
+    cfg = Phi3Config(vocab_size=32064, hidden_size=3072, intermediate_size=8192,
+                     num_hidden_layers=n_layers, num_attention_heads=32, num_key_value_heads=32,
+                     max_position_embeddings=131072, original_max_position_embeddings=4096,
+                     rope_scaling={"type": "longrope", "short_factor": [1.0] * 48,
+                                   "long_factor": [4.0] * 48},
+                     pad_token_id=32000, bos_token_id=1, eos_token_id=32000)
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            torch.manual_seed(0)
+            model = Phi3ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(old)
+    return model.eval()
+
+
+def model_bench(args, dev):
+    """--workload cfg4_prefill32k / cfg5_prefill128k: full prefill of the
+    random-init Phi-3-mini-128k-shaped model through the patched forward
+    (MInference with a seeded per-head pattern file over all 1024 heads),
+    use_cache=True, last-token logits.  value = TTFT (ms).  The patched
+    forward's attention launches (estimators + staging + attention of each
+    layer) and RoPE launches are bracketed by HIP events, which gives the
+    attention fraction of prefill time; the unpatched model (PyTorch SDPA) on
+    the same ids is the dense baseline."""
+    import tempfile
+
+    import torch
+
+    from minference import MInference
+    from minference.configs import patterns as PAT
+    from minference.modules import minference_forward as MF
+
+    S = WORKLOADS[args.workload][0]
+    mix = [(f, PAT.record(*rec)) for f, rec in MODEL_MIX[args.workload]]
+    model = phi3_mini_128k(dev)
+    ids = torch.randint(3, 32000, (1, S), device=dev,
+                        generator=torch.Generator(device=dev).manual_seed(args.seed))
+    stream = torch.cuda.current_stream(dev)
+
+    def ttft(m, reps):
+        times = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            with torch.no_grad():
+                m(input_ids=ids, use_cache=True, logits_to_keep=1)
+            torch.cuda.synchronize()
+            times.append((time.perf_counter() - t0) * 1e3)
+        return times
+
+    dense = None
+    if not args.no_dense:
+        ttft(model, 1)
+        dense = ttft(model, 1)[0]
+        torch.cuda.empty_cache()
+
+    cfg = PAT.mixed_config(mix, seed=args.seed)
+    with tempfile.NamedTemporaryFile("w", suffix=".json", delete=False) as f:
+        path = f.name
+    PAT.write(path, cfg)
+    model = MInference(attn_type="minference", config_path=path)(model)
+    events = {"attention": [], "rope": []}
+    real_attn, real_rope = MF.run_layer_attention, MF._apply_rope
+
+    def timed(key, fn):
+        def wrapper(*a, **kw):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            r = fn(*a, **kw)
+            e1.record(stream)
+            events[key].append((e0, e1))
+            return r
+        return wrapper
+
+    MF.run_layer_attention = timed("attention", real_attn)
+    MF._apply_rope = timed("rope", real_rope)
+    try:
+        for _ in range(args.warmup):
+            ttft(model, 1)
+        for v in events.values():
+            v.clear()
+        runs = ttft(model, max(1, args.steps))
+        torch.cuda.synchronize()
+        per_run = {k: sum(a.elapsed_time(b) for a, b in v) / len(runs) for k, v in events.items()}
+    finally:
+        MF.run_layer_attention, MF._apply_rope = real_attn, real_rope
+        os.unlink(path)
+    t = sum(runs) / len(runs)
+    kinds = PAT.validate_config(cfg).kind_counts()
+    result = {
+        "metric": "Phi-3-mini-128k-shaped full prefill TTFT (patched, all heads per the mix)",
+        "value": round(t, 2), "unit": "ms", "n_gpus": 1, "steps": len(runs), "warmup": args.warmup,
+        "ms_per_step": round(t, 2), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights, random token ids)",
+        "config": {"workload": args.workload, "model": "Phi-3-mini-128k shape, 32 layers",
+                   "seq_len": S, "heads": 32, "head_dim": 96, "mix": kinds,
+                   "global_batch": 1, "parallelism": "single GPU"},
+        "ttft_runs_ms": [round(x, 2) for x in runs],
+        "attention_ms": round(per_run["attention"], 2),
+        "attention_fraction": round(per_run["attention"] / t, 4),
+        "rope_ms": round(per_run["rope"], 2),
+        "dense_sdpa_ttft_ms": round(dense, 2) if dense is not None else None,
+        "speedup_vs_dense_ttft": round(dense / t, 2) if dense is not None else None,
+    }
+    print(json.dumps(result), flush=True)
 
 
 def vs_bench(args, dev):
