@@ -605,6 +605,7 @@ def vs_bench(args, dev):
                        "lists_gather_attention": round(t_attn, 4)},
         "vs_tiles": tiles,
         "vs_tiles_builder": tiles_gpu,
+        "vs_tiles_unmasked": int(counts[:, 0].sum()),
         "vs_tile_density": round(tiles / (len(plan.vs_heads) * block_tiles(S, 1 << 30)), 4),
         "executed_flop": flop,
         "attention_tflops": round(flop / (t_attn * 1e-3) / 1e12, 3),

@@ -475,6 +475,18 @@ void attn_kernel(AttnParams P) {
     if constexpr (VS) {
       bits = uint32_t(mk >> (16 * w + 4 * lr)) & 0xfu;
       past = t >= P.n_kb;
+      // every key of a gathered tile or of a tile before the first row's
+      // tile lies in every row's past: visibility is the key's bit, the same
+      // for all rows of a lane (wave-uniform branch)
+      if (past || t * kBlock + kBlock - 1 < a0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool on = (bits >> i) & 1u;
+#pragma unroll
+          for (int gg = 0; gg < 2; ++gg) s[gg][i] = on ? s[gg][i] : -__builtin_inff();
+        }
+        return;
+      }
     }
 #pragma unroll
     for (int gg = 0; gg < 2; ++gg) {
