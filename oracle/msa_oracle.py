@@ -55,6 +55,7 @@ __all__ = [
     "vs_scores",
     "vs_estimate",
     "vs_token_visible",
+    "vs_row_visible",
     "vertical_slash_from_indices",
     "stream_visible",
     "streaming_attention",
@@ -366,6 +367,24 @@ def vs_token_visible(v_idx_row: np.ndarray, s_idx_row: np.ndarray, s_q: int, s_k
     i = np.arange(s_q)[:, None]
     j = np.arange(s_k)[None, :]
     return tok & (j <= i)
+
+
+def vs_row_visible(v_idx_row: np.ndarray, s_idx_row: np.ndarray, row: int, s_k: int,
+                   block: int = BLOCK) -> np.ndarray:
+    """Key ids (ascending) that query row ``row`` of a vertical_and_slash head
+    sees: row ``row`` of vs_token_visible without building the S x S mask
+    (same rule: the slash windows of its 64-row block, the vertical columns,
+    then j <= row)."""
+    end_m = (row // block + 1) * block
+    keys = [np.clip(np.asarray(v_idx_row, dtype=np.int64), 0, s_k - 1)]
+    s = np.asarray(s_idx_row, dtype=np.int64)
+    s = s[s < end_m]
+    hi = np.minimum(np.maximum(end_m - s, block), s_k)
+    lo = np.minimum(np.maximum(hi - block, 0), s_k)
+    for a, b in zip(lo.tolist(), hi.tolist()):
+        keys.append(np.arange(a, b))
+    js = np.unique(np.concatenate(keys))
+    return js[js <= row]
 
 
 # ---------------------------------------------------------------------------

@@ -131,3 +131,40 @@ def test_kinds_agree_where_they_coincide(gpu_device, S):
     block = block_sparse_attention(q, k, v, math.ceil(S / 64))
     assert torch.equal(stream, dense)
     assert torch.equal(block, dense)
+
+
+@pytest.mark.parametrize("S,vsz,ssz", [(65536, 1000, 6096), (131072, 3500, 100)],
+                         ids=["64k-1000-6096", "128k-3500-100"])
+def test_vs_full_length_estimator_and_rows(gpu_device, S, vsz, ssz):
+    """vertical_and_slash at the bench length and at MSA_VS_MAX_SEQ: estimator
+    indices bit-exact with the oracle, sampled rows of the attention against
+    the oracle's per-row visibility, and constant V reproduced on every row."""
+    from minference.ops.vertical_slash_kernel import (vertical_and_slash_estimate,
+                                                      vertical_slash_sparse_attention)
+
+    H, D = 2, 96
+    q, k, v = device_qkv(gpu_device, H, S, D, seed=S % 997)
+    print(f"[vs-full] estimator S={S} ({vsz}, {ssz})", flush=True)
+    vi, si = vertical_and_slash_estimate(q, k, vsz, ssz)
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    rv, rs = O.vs_estimate(qn, kn, vsz, ssz, "bf16")
+    gv, gs = vi.cpu().numpy(), si.cpu().numpy()
+    assert np.array_equal(gv, rv), f"{(gv != rv).sum()} vertical ids differ"
+    assert np.array_equal(gs, rs), f"{(gs != rs).sum()} slash ids differ"
+
+    print(f"[vs-full] attention S={S}", flush=True)
+    out = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    vertical_slash_sparse_attention(q, k, v, vi, si, out=out)
+    rows = rows_for(S, extra=(S - 64 * 50 - 3, S - 200, S - 6096, S - 6097))
+    scale = O.sparse_scale(D)
+    for h in range(H):
+        ref = oracle_rows(qn[0, h], kn[0, h], vn[0, h], rows,
+                          lambda r, h=h: O.vs_row_visible(rv[0, h], rs[0, h], r, S), scale)
+        err = np.abs(out[0, h, rows].cpu().numpy() - ref).max()
+        assert err < TOL, (h, err)
+    del out
+
+    print(f"[vs-full] constant-V property S={S}", flush=True)
+    vc = torch.full_like(v, -1.25)
+    o1 = vertical_slash_sparse_attention(q, k, vc, vi, si)
+    assert torch.all(o1 == -1.25)

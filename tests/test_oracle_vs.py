@@ -199,6 +199,20 @@ def test_vs_token_visible_dual_form(S, nv, ns, seed):
     assert (O.vs_token_visible(v, s, S, S) == _visible_dual(v, s, S)).all()
 
 
+@pytest.mark.parametrize("S,nv,ns,seed", [(130, 35, 60, 0), (256, 40, 70, 1), (200, 30, 150, 2),
+                                         (300, 20, 40, 3)])
+def test_vs_row_visible_equals_mask_rows(S, nv, ns, seed):
+    """The per-row form used at full sizes gives exactly the rows of the
+    token mask (which the slash-side dual form pins above), including
+    out-of-range and repeated indices."""
+    g = np.random.default_rng(seed)
+    v = np.sort(g.integers(-10, S + 10, nv))
+    s = np.sort(g.integers(-20, S + 20, ns))[::-1]
+    vis = O.vs_token_visible(v, s, S, S)
+    for r in range(S):
+        assert np.array_equal(O.vs_row_visible(v, s, r, S), np.nonzero(vis[r])[0]), r
+
+
 def test_vs_token_visible_reference_properties():
     """tests/test_vertical_slash_kernel.py:207-238: the strict upper triangle is
     masked, the diagonal is not all masked, the 30 sink columns are visible to
