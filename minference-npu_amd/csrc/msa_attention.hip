@@ -506,23 +506,24 @@ void attn_kernel(AttnParams P) {
       }
     }
   };
-  // P = 2^(s*c - m) in place, with the current running max.  Returns true
-  // when some P exceeds 2^8 (P >= 0, so the float bits order like integers).
-  auto exp_half = [&](f32x4 (&s)[2], int hf) INLINE -> bool {
-    uint32_t mx = 0;
+  // P = 2^(s*c - m) in place, with the current running max, and ps[gg] =
+  // the lane's sum of its four P of group gg (its share of the row sum).
+  // Returns true when some sum exceeds 2^8; every P is at most its sum
+  // (P >= 0), so otherwise no P is large enough to need a rescale.
+  auto exp_half = [&](f32x4 (&s)[2], int hf, float (&ps)[2]) INLINE -> bool {
 #pragma unroll
-    for (int gg = 0; gg < 2; ++gg)
+    for (int gg = 0; gg < 2; ++gg) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 4; ++i)
         s[gg][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[gg][i], c_log2, -m_g[2 * hf + gg]));
-        mx = max(mx, __float_as_uint(s[gg][i]));
-      }
-    return __ballot(mx > 0x43800000u) != 0;  // 256.0f
+      ps[gg] = (s[gg][0] + s[gg][1]) + (s[gg][2] + s[gg][3]);
+    }
+    return __ballot(fmaxf(ps[0], ps[1]) > 256.0f) != 0;
   };
   // Rare path: recompute the half's scores, raise the running max to the
   // row max, rescale the half's O and row sums, and redo the exponentials.
-  auto rescale_half = [&](const u32x4 (&kr)[NKS], f32x4 (&s)[2], int hf, int t, uint64_t mk,
-                          bool mt) INLINE {
+  auto rescale_half = [&](const u32x4 (&kr)[NKS], f32x4 (&s)[2], float (&ps)[2], int hf, int t,
+                          uint64_t mk, bool mt) INLINE {
     qk_half(kr, hf, s);
     if (mt) mask_half(s, hf, t, mk);
     float m0 = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
@@ -545,23 +546,21 @@ void attn_kernel(AttnParams P) {
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[db][hf][i] *= ab;
-    exp_half(s, hf);
+    exp_half(s, hf, ps);
   };
-  // P rounded to fp16, row sums of the rounded P, and PV of the half:
-  // groups 2h, 2h+1 -> B operand of row block h (keys 8(l>>5) .. +7 of row
-  // 32h + (l&31)) with one lane-row swap per register pair.
+  // Row sums take the fp32 P (the half's ps), P rounded to fp16 goes to
+  // PV: groups 2h, 2h+1 -> B operand of row block h (keys 8(l>>5) .. +7 of
+  // row 32h + (l&31)) with one lane-row swap per register pair.
   typedef float f2 __attribute__((ext_vector_type(2)));
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  auto pv_half = [&](const f32x4 (&s)[2], int hf, const u32x4 (&vr)[NDB]) INLINE {
+  auto pv_half = [&](const f32x4 (&s)[2], const float (&ps)[2], int hf,
+                     const u32x4 (&vr)[NDB]) INLINE {
     uint32_t pk[2][2];
 #pragma unroll
     for (int gg = 0; gg < 2; ++gg) {
       pk[gg][0] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{s[gg][0], s[gg][1]}, h2));
       pk[gg][1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{s[gg][2], s[gg][3]}, h2));
-      l_g[2 * hf + gg] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk[gg][0]), h2{1, 1},
-                                                l_g[2 * hf + gg], false);
-      l_g[2 * hf + gg] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk[gg][1]), h2{1, 1},
-                                                l_g[2 * hf + gg], false);
+      l_g[2 * hf + gg] += ps[gg];
     }
     uint32_t x0 = pk[0][0], y0 = pk[1][0], x1 = pk[0][1], y1 = pk[1][1];
     swap16(x0, y0);
@@ -607,15 +606,16 @@ void attn_kernel(AttnParams P) {
     const int tnn = seq.tile(p + 3);
     const uint64_t mnn = mask_at(p + 3);
     f32x4 sa[2], sb[2];
+    float pa[2], pb[2];
     qk_half(kr, 0, sa);
     qk_half(kr, 1, sb);
     if constexpr (MT) mask_half(sa, 0, tcur, mcur);
-    if (exp_half(sa, 0)) rescale_half(kr, sa, 0, tcur, mcur, MT);
-    pv_half(sa, 0, vr);
+    if (exp_half(sa, 0, pa)) rescale_half(kr, sa, pa, 0, tcur, mcur, MT);
+    pv_half(sa, pa, 0, vr);
     if constexpr (MT) mask_half(sb, 1, tcur, mcur);
-    if (exp_half(sb, 1)) rescale_half(kr, sb, 1, tcur, mcur, MT);
+    if (exp_half(sb, 1, pb)) rescale_half(kr, sb, pb, 1, tcur, mcur, MT);
     load_k(tn, kr);
-    pv_half(sb, 1, vr);
+    pv_half(sb, pb, 1, vr);
     load_v(tn, vr);
     tcur = tn;
     tn = tnn;
