@@ -187,6 +187,19 @@ def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan:
         return out
     idx = cnt = None
     n_slots = len(plan.block_heads)
+    staged = False
+    ws = None
+    if n_slots or plan.vs_heads:
+        # K/V staging does not depend on the estimators: it runs on a side
+        # stream while they run here, and the attention waits for both.
+        main = torch.cuda.current_stream(q.device)
+        side = _side_stream(q.device)
+        ws = _abi.workspace(_abi.attention_workspace_bytes(k.shape[0], k.shape[1], k.shape[2],
+                                                           k.shape[3]), q.device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            _abi.stage_kv(k, v, ws)
+        staged = True
     if n_slots:
         n_qb = math.ceil(S_q / _abi.MSA_BLOCK)
         idx = torch.empty((B, n_slots, n_qb, plan.topk_max), dtype=torch.int32, device=q.device)
@@ -195,9 +208,25 @@ def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan:
         _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max, s_sparse,
                             idx, cnt)
     vs = _vs_lists(q, k, plan) if plan.vs_heads else None
+    if staged:
+        main.wait_stream(side)
     _abi.layer_attention(q, k, v, out, plan.heads, idx=idx, cnt=cnt, idx_slots=n_slots,
-                         topk_max=plan.topk_max, vs=vs)
+                         topk_max=plan.topk_max, ws=ws, staged=staged, vs=vs)
     return out
+
+
+_SIDE_STREAMS: Dict[int, "torch.cuda.Stream"] = {}
+
+
+def _side_stream(device: torch.device) -> "torch.cuda.Stream":
+    """The per-device stream K/V staging overlaps the estimators on (default
+    priority, created once)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    st = _SIDE_STREAMS.get(index)
+    if st is None:
+        st = torch.cuda.Stream(device=torch.device("cuda", index))
+        _SIDE_STREAMS[index] = st
+    return st
 
 
 def run_decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
