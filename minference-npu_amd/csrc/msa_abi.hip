@@ -387,7 +387,7 @@ static void order_items(AttnParams& ap, const int* pairs, const HeadWork* work, 
   ap.n_hl = n;
   double head_tot[kMaxHeads], total = 0.0;
   for (int i = 0; i < n; ++i) {
-    ap.head_order[i] = int16_t(pairs[i]);
+    ap.head_order[i] = pairs[i];
     head_tot[i] = prefix_cost(work[i], nq);
     total += head_tot[i];
   }
@@ -515,8 +515,8 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   const double log2e = 1.4426950408889634;
   for (int h = 0; h < n_heads; ++h) {
     const int kd = heads[h].kind;
-    ap.hd[h].kind = int16_t(kd);
-    ap.hd[h].slot = int16_t(kd == MSA_KIND_BLOCK || kd == MSA_KIND_VS ? heads[h].slot : 0);
+    ap.hd[h].kind = kd;
+    ap.hd[h].slot = kd == MSA_KIND_BLOCK || kd == MSA_KIND_VS ? heads[h].slot : 0;
     ap.hd[h].p1 = heads[h].p1;
     ap.hd[h].p2 = heads[h].p2;
     ap.hd[h].scale_log2 = float(double(heads[h].scale) * log2e);

@@ -245,7 +245,7 @@ struct TileSeq {
     i = q < c1 ? lo0 + q : i;
     // the load is unconditional (element 0 of `any` when there is no list)
     // so that no branch splits the caller's instruction stream
-    const int32_t v = (list ? list : any)[list ? i : 0];
+    const int32_t v = load_uniform((list ? list : any) + (list ? i : 0));
     const int t = list ? v : i;
     return min(max(t, 0), n_kb - 1);
   }
@@ -346,8 +346,8 @@ void attn_kernel(AttnParams P) {
     // full tiles (no mask), then partial tiles, then gathered vertical tiles
     // (ids n_kb + g), every entry with its key mask
     vs_base = ((int64_t(b) * P.vs_slots + hd.slot) * P.n_qb + bq);
-    const int nf = P.vs_cnt[2 * vs_base];
-    const int nt = P.vs_cnt[2 * vs_base + 1];
+    const int nf = load_uniform(P.vs_cnt + 2 * vs_base);
+    const int nt = load_uniform(P.vs_cnt + 2 * vs_base + 1);
     vs_base *= P.vs_cap;
     seq.list = P.vs_ids + vs_base;
     seq.n_kb = P.n_kb + P.nv_pad / kBlock;
@@ -355,10 +355,10 @@ void attn_kernel(AttnParams P) {
   } else if (kind == KIND_BLOCK) {
     // canonical list: ascending causal ids, so the boundary ids come last
     const int64_t base = (int64_t(b) * P.idx_slots + hd.slot) * P.n_qb + bq;
-    const int cnt = max(0, min(P.cnt[base], P.topk_max));
+    const int cnt = max(0, min(load_uniform(P.cnt + base), P.topk_max));
     const int32_t* list = P.idx + base * P.topk_max;
     int nf = cnt;
-    while (nf > 0 && list[nf - 1] >= Fe) --nf;
+    while (nf > 0 && load_uniform(list + nf - 1) >= Fe) --nf;
     seq.list = list;
     seq.set({0, nf, 0, 0, 0}, {nf, cnt, 0, 0, 0}, 1);
   } else if (kind == KIND_STREAM) {
@@ -397,14 +397,20 @@ void attn_kernel(AttnParams P) {
   {
     const uint16_t* qbase =
         reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + int64_t(h) * P.q_sh;
+    // rows past S_q load row S_q - 1 and are zeroed after the load, so the
+    // loads issue back to back with no branch between them
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int row = q0 + 16 * g + lc;
+      const int64_t roff = int64_t(min(row, P.s_q - 1)) * P.q_ss;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) qb[g][ks] = load16(qbase + roff + 32 * ks + 8 * lr);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks)
-        qb[g][ks] = row < P.s_q ? load16(qbase + int64_t(row) * P.q_ss + 32 * ks + 8 * lr)
-                                : zero_u32x4();
-    }
+        qb[g][ks] = q0 + 16 * g + lc < P.s_q ? qb[g][ks] : zero_u32x4();
   }
 
   // K and V chunk operands of tile t: wave w reads chunk 4t + w of the staged
@@ -587,7 +593,7 @@ void attn_kernel(AttnParams P) {
   // key masks of vertical_and_slash tiles travel with their tile numbers
   // (looked up three positions ahead, like the tiles)
   auto mask_at = [&](int q) INLINE -> uint64_t {
-    if constexpr (VS) return P.vs_masks[vs_base + max(min(q, total - 1), 0)];
+    if constexpr (VS) return load_uniform(P.vs_masks + vs_base + max(min(q, total - 1), 0));
     return 0ull;
   };
   int tA = seq.tile(0), tB = seq.tile(1);

@@ -47,6 +47,18 @@ __device__ inline _Float16 to_f16_sat(uint16_t b) {
 
 __device__ inline u32x4 zero_u32x4() { return u32x4{0u, 0u, 0u, 0u}; }
 
+// Load of read-only data at a wave-uniform address through the constant
+// address space, which the compiler lowers to a scalar load.  For data a
+// kernel never writes (tile lists, counts, masks written by earlier
+// launches).  A vector load would land in a VGPR behind the wave's
+// outstanding operand loads: its wait, which counts vector loads in order,
+// would also wait for every operand load issued before it.
+template <typename T>
+__device__ inline T load_uniform(const T* p) {
+  return *reinterpret_cast<const __attribute__((address_space(4))) T*>(
+      __builtin_bit_cast(uintptr_t, p));
+}
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // 16x16x32 MFMA on 16-bit inputs, fp32 accumulation.  Lane l: A[l % 16][8 (l / 16) + j],

@@ -32,9 +32,11 @@ struct ScoreParams {
   int16_t slot_topk[kMaxHeads];
 };
 
+// 32-bit fields throughout: the kernel reads these with scalar loads, which
+// have no 16-bit form on gfx950.
 struct HeadArg {
-  int16_t kind;
-  int16_t slot;
+  int32_t kind;
+  int32_t slot;
   int32_t p1;  // stream: n_init
   int32_t p2;  // stream: n_local
   float scale_log2;  // softmax scale * log2(e)
@@ -73,9 +75,10 @@ struct AttnParams {
   const uint16_t* gkt;
   const uint16_t* gvt;
   int vs_slots, vs_cap, nv_pad;
-  int16_t head_order[kMaxHeads];
+  int32_t head_order[kMaxHeads];
   HeadArg hd[kMaxHeads];
 };
+static_assert(sizeof(AttnParams) <= 4096, "attention kernel arguments exceed 4 KB");
 
 // vertical_and_slash tile lists of one layer (vs_build_kernel).
 struct VsBuildParams {
