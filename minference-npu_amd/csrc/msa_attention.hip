@@ -27,10 +27,7 @@
 //   QK; only when some P exceeds 2^8 (the row max grew by more than 8 in
 //   log2 units) does a rare path recompute the half's scores, reduce the row
 //   maxima over the four lanes of each row with permlane swaps and rescale
-//   O.  Only the first step and the boundary tiles run that test; the
-//   other mask-free steps keep the largest per-lane P sum, and a wave whose
-//   maximum ends above 2^8 redoes those steps tested.  Row sums accumulate
-//   per lane and reduce once at the end.
+//   O.  Row sums accumulate per lane and reduce once at the end.
 //   Tiles that need no mask run first; boundary tiles (diagonal, band start,
 //   partial sink, S_k end) run last with the elementwise mask.
 
@@ -447,27 +444,17 @@ void attn_kernel(AttnParams P) {
   };
 
   f32x16 o[NDB][2];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[db][rb][i] = 0.0f;
   // Running max per row in scaled log2 units, group layout (each group's
   // value in all 4 lane rows).  It only moves when some P would exceed 2^8,
   // so the O rescale is rare.
-  float m_g[4];
-  float l_g[4];  // per-lane partial row sums, group layout
-  auto reset = [&]() INLINE {
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][rb][i] = 0.0f;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      m_g[g] = -1e30f;
-      l_g[g] = 0.0f;
-    }
-  };
-  reset();
-  // largest per-lane P sum of the steps that run without the overflow test
-  float p_hi = 0.0f;
+  float m_g[4] = {-1e30f, -1e30f, -1e30f, -1e30f};
+  float l_g[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // per-lane partial row sums, group layout
   const float c_log2 = hd.scale_log2;
   const int arow0 = a0 + lc;  // absolute position of this lane's row in group 0
   const int skm1 = P.s_k - 1;
@@ -529,7 +516,7 @@ void attn_kernel(AttnParams P) {
   // the lane's sum of its four P of group gg (its share of the row sum).
   // Returns true when some sum exceeds 2^8; every P is at most its sum
   // (P >= 0), so otherwise no P is large enough to need a rescale.
-  auto exp_sum = [&](f32x4 (&s)[2], int hf, float (&ps)[2]) INLINE {
+  auto exp_half = [&](f32x4 (&s)[2], int hf, float (&ps)[2]) INLINE -> bool {
 #pragma unroll
     for (int gg = 0; gg < 2; ++gg) {
 #pragma unroll
@@ -537,9 +524,6 @@ void attn_kernel(AttnParams P) {
         s[gg][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[gg][i], c_log2, -m_g[2 * hf + gg]));
       ps[gg] = (s[gg][0] + s[gg][1]) + (s[gg][2] + s[gg][3]);
     }
-  };
-  auto exp_half = [&](f32x4 (&s)[2], int hf, float (&ps)[2]) INLINE -> bool {
-    exp_sum(s, hf, ps);
     return __ballot(fmaxf(ps[0], ps[1]) > 256.0f) != 0;
   };
   // Rare path: recompute the half's scores, raise the running max to the
@@ -612,31 +596,19 @@ void attn_kernel(AttnParams P) {
     if constexpr (VS) return load_uniform(P.vs_masks + vs_base + max(min(q, total - 1), 0));
     return 0ull;
   };
-  int tA, tB, tn;
-  uint64_t mA, mB, mn;
-  // the first two positions' operands in flight
-  auto prime = [&]() INLINE {
-    tA = seq.tile(0);
-    tB = seq.tile(1);
-    mA = mask_at(0);
-    mB = mask_at(1);
-    mn = mask_at(2);
-    load_k(tA, kA);
-    load_v(tA, vA);
-    load_k(tB, kB);
-    load_v(tB, vB);
-    tn = seq.tile(2);
-  };
+  int tA = seq.tile(0), tB = seq.tile(1);
+  uint64_t mA = mask_at(0), mB = mask_at(1), mn = mask_at(2);
+  load_k(tA, kA);
+  load_v(tA, vA);
+  load_k(tB, kB);
+  load_v(tB, vB);
+  int tn = seq.tile(2);
   // one step: QK of both halves; half 0's softmax under half 1's QK, half
   // 1's softmax under half 0's PV; K is reloaded once the rare path can no
-  // longer need it.  A step with the overflow test (TESTED) takes the rare
-  // path when some P exceeds 2^8; one without it only records the largest
-  // per-lane P sum in p_hi (one max3 per half instead of a compare and a
-  // branch).
-  auto step = [&](auto masked, auto tested, u32x4 (&kr)[NKS], u32x4 (&vr)[NDB], int& tcur,
-                  uint64_t& mcur, int p) INLINE {
+  // longer need it
+  auto step = [&](auto masked, u32x4 (&kr)[NKS], u32x4 (&vr)[NDB], int& tcur, uint64_t& mcur,
+                  int p) INLINE {
     constexpr bool MT = decltype(masked)::value;
-    constexpr bool TESTED = decltype(tested)::value;
     const int tnn = seq.tile(p + 3);
     const uint64_t mnn = mask_at(p + 3);
     f32x4 sa[2], sb[2];
@@ -644,20 +616,10 @@ void attn_kernel(AttnParams P) {
     qk_half(kr, 0, sa);
     qk_half(kr, 1, sb);
     if constexpr (MT) mask_half(sa, 0, tcur, mcur);
-    if constexpr (TESTED) {
-      if (exp_half(sa, 0, pa)) rescale_half(kr, sa, pa, 0, tcur, mcur, MT);
-    } else {
-      exp_sum(sa, 0, pa);
-      p_hi = fmaxf(p_hi, fmaxf(pa[0], pa[1]));
-    }
+    if (exp_half(sa, 0, pa)) rescale_half(kr, sa, pa, 0, tcur, mcur, MT);
     pv_half(sa, pa, 0, vr);
     if constexpr (MT) mask_half(sb, 1, tcur, mcur);
-    if constexpr (TESTED) {
-      if (exp_half(sb, 1, pb)) rescale_half(kr, sb, pb, 1, tcur, mcur, MT);
-    } else {
-      exp_sum(sb, 1, pb);
-      p_hi = fmaxf(p_hi, fmaxf(pb[0], pb[1]));
-    }
+    if (exp_half(sb, 1, pb)) rescale_half(kr, sb, pb, 1, tcur, mcur, MT);
     load_k(tn, kr);
     pv_half(sb, pb, 1, vr);
     load_v(tn, vr);
@@ -666,38 +628,17 @@ void attn_kernel(AttnParams P) {
     mcur = mn;
     mn = mnn;
   };
-  auto run = [&](auto masked, auto tested, int p0, int p1) INLINE {
+  auto run = [&](auto masked, int p0, int p1) INLINE {
     int p = p0;
-    if ((p & 1) && p < p1) step(masked, tested, kB, vB, tB, mB, p++);
+    if ((p & 1) && p < p1) step(masked, kB, vB, tB, mB, p++);
     for (; p + 1 < p1; p += 2) {
-      step(masked, tested, kA, vA, tA, mA, p);
-      step(masked, tested, kB, vB, tB, mB, p + 1);
+      step(masked, kA, vA, tA, mA, p);
+      step(masked, kB, vB, tB, mB, p + 1);
     }
-    if (p < p1) step(masked, tested, kA, vA, tA, mA, p);
+    if (p < p1) step(masked, kA, vA, tA, mA, p);
   };
-  // The first step sets the running max from the first tile's scores (its
-  // rare path); the other mask-free steps run without the overflow test,
-  // and the boundary tiles with it.  While no P of the untested steps
-  // exceeds 2^8 none of them would have taken the rare path, so the result
-  // is exactly that of testing every step.  Otherwise the wave runs the
-  // mask-free steps again, all tested, before the boundary tiles.
-  constexpr std::integral_constant<bool, false> kNo{};
-  constexpr std::integral_constant<bool, true> kYes{};
-  prime();
-  if constexpr (VS) {
-    // (the persistent vertical_and_slash kernel keeps every step tested: the
-    // untested variant adds register spills there)
-    run(kNo, kYes, 0, mpos);
-  } else if (mpos > 0) {
-    step(kNo, kYes, kA, vA, tA, mA, 0);
-    run(kNo, kNo, 1, mpos);
-    if (__ballot(p_hi > 256.0f) != 0) {
-      reset();
-      prime();
-      run(kNo, kYes, 0, mpos);
-    }
-  }
-  run(kYes, kYes, mpos, total);
+  run(std::integral_constant<bool, false>(), 0, mpos);
+  run(std::integral_constant<bool, true>(), mpos, total);
 
   // ---- merge the four chunk partials of each row; wave 0 writes the rows
   // block layout: lane rows 1, 3 hold group 2rb+1.  Chosen by an exact blend
