@@ -74,7 +74,8 @@ typedef struct msa_tensor4 {
  *   p1, p2 = stream_llm: n_init, n_local;  block_sparse: topk (unused here), 0;
  *            vertical_and_slash: vertical and slash counts (work estimate only)
  *   slot   = block_sparse: row of idx/cnt written by msa_block_estimate; else -1
- *   scale  = softmax scale applied to q.k (the caller decides)
+ *   scale  = softmax scale applied to q.k, as the calling op defines it (the
+ *            reference ops use different conventions, e.g. a padded head dim)
  * Mirrors the per-head record [type, p1, p2, score] parsed at
  * minference/modules/minference_forward.py:187-198, 404-419. */
 typedef struct msa_head_desc {

@@ -376,7 +376,7 @@ def test_dense_vs_torch_sdpa(s_q, s_k):
 
 
 # ---------------------------------------------------------------------------
-# algorithmic work counts (closed forms quoted in the survey / baseline)
+# algorithmic work counts (closed forms for the benchmark configurations)
 # ---------------------------------------------------------------------------
 def test_work_counts_small_bruteforce():
     for S, ni, nl in [(300, 20, 50), (1000, 128, 256), (64, 0, 64)]:
