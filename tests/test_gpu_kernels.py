@@ -209,9 +209,10 @@ def test_dense_vs_oracle(gpu_device, s_q, s_k, D, dtype):
 @pytest.mark.parametrize("kind", ["dense", "stream", "block"])
 def test_late_outlier_keys(gpu_device, kind, factor):
     """Keys scaled by `factor` in the middle of the sequence make a row's max
-    logit jump after its first tiles: by a few units (no rescale), past the
-    lazy slack (rescale from the tracked maxima) or far enough that P would
-    overflow fp16 (the work item is redone)."""
+    logit jump after its first tiles: by a few units (P stays below 2^8, no
+    rescale), past that slack, or far enough that P taken with the stale
+    maximum would overflow fp16 and fp32; the last two take the rare path
+    (scores recomputed, O and the row sums rescaled) mid-item."""
     from minference import block_sparse_attention, dense_attention, streaming_forward
 
     S, H, D = 2048, 2, 96
