@@ -1,5 +1,8 @@
 """Parity at the BASELINE configurations' full sizes.
 
+config 1: stream_llm, 32 heads, S=4096, 64 sinks + 1024 band, RoPE (theta
+10000) applied to Q and K first (the reference runs it on the CPU in fp32;
+here the fused RoPE and the stream kernel run on bf16 inputs).
 config 2: block_sparse, 32 heads, S=16384, top-100, K rows 0-3 x8.
 config 3: stream_llm, 32 heads, S=65536, 128 sinks + 4096 band.
 Block ids are compared with the oracle in full; outputs on sampled rows
@@ -83,6 +86,33 @@ def test_cfg2_block_ids_bit_exact_and_rows(gpu_device):
         ref = oracle_rows(qn[0, h], kn[0, h], vn[0, h], rows, vis, scale)
         err = np.abs(og[0, h, rows] - ref).max()
         assert err < TOL, (h, err)
+
+
+def test_cfg1_rope_then_stream_all_rows(gpu_device):
+    from minference import streaming_forward
+    from minference.ops.rope import apply_rotary_pos_emb
+    from test_rope import rope_tables
+
+    H, S, D, n_init, n_local = 32, 4096, 96, 64, 1024
+    print(f"[cfg1] RoPE + stream H={H} S={S} ({n_init}, {n_local})", flush=True)
+    g = torch.Generator(device=gpu_device).manual_seed(1)
+    q, k, v = (torch.randn(1, H, S, D, generator=g, device=gpu_device).to(torch.bfloat16)
+               for _ in range(3))
+    cos, sin = (t.to(gpu_device) for t in rope_tables(1, S, D, torch.bfloat16, theta=10000.0))
+    qr, kr = apply_rotary_pos_emb(q, k, cos, sin)
+    heads = [0, 9, 20, 31]
+    cn, sn = cos.float().cpu().numpy(), sin.float().cpu().numpy()
+    qn = O.rope_rotate_half(q[:, heads].float().cpu().numpy(), cn, sn, "bf16")
+    kn = O.rope_rotate_half(k[:, heads].float().cpu().numpy(), cn, sn, "bf16")
+    assert np.array_equal(qr[:, heads].float().cpu().numpy(), qn)
+    assert np.array_equal(kr[:, heads].float().cpu().numpy(), kn)
+    out = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    streaming_forward(qr, kr, v, n_init, n_local, out=out)
+    ref = O.streaming_attention(qn, kn, v[:, heads].float().cpu().numpy(), n_init, n_local)
+    err = np.abs(out[:, heads].cpu().numpy() - ref).max()
+    assert err < TOL, err
+    vc = torch.full_like(v, -1.25)
+    assert torch.all(streaming_forward(qr, kr, vc, n_init, n_local) == -1.25)
 
 
 def test_cfg3_stream_rows_and_properties(gpu_device):
