@@ -413,6 +413,23 @@ static void order_items(AttnParams& ap, const int* pairs, const HeadWork* work, 
   }
 }
 
+// Puts the block_sparse entries of list[0..n) evenly between the others
+// (stable within each group).  The XCDs take contiguous ranges of the item
+// list, so this gives every XCD the same mix of L2-friendly band / dense
+// heads and block heads, whose scattered tiles miss the L2 more.
+static void interleave_kinds(int* list, int n, const msa_head_desc* heads, int H) {
+  int blk[kMaxHeads], oth[kMaxHeads], nb = 0, no = 0;
+  for (int i = 0; i < n; ++i) {
+    if (heads[list[i] % H].kind == MSA_KIND_BLOCK) blk[nb++] = list[i];
+    else oth[no++] = list[i];
+  }
+  int ib = 0, io = 0;
+  for (int i = 0; i < n; ++i) {
+    const bool take_b = ib < nb && (io >= no || int64_t(ib) * n <= int64_t(i) * nb);
+    list[i] = take_b ? blk[ib++] : oth[io++];
+  }
+}
+
 static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
                                 const msa_tensor4* o, const msa_head_desc* heads, int32_t n_heads,
                                 const int32_t* idx, const int32_t* cnt, int32_t idx_slots,
@@ -527,10 +544,9 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
     if (BH <= kMaxHeads) {
       int pairs[kMaxHeads];
       HeadWork work[kMaxHeads];
-      for (int i = 0; i < BH; ++i) {
-        pairs[i] = i;
-        work[i] = head_work(heads[i % H], n_kb, topk_max);
-      }
+      for (int i = 0; i < BH; ++i) pairs[i] = i;
+      interleave_kinds(pairs, BH, heads, int(H));
+      for (int i = 0; i < BH; ++i) work[i] = head_work(heads[pairs[i] % H], n_kb, topk_max);
       order_items(ap, pairs, work, BH);
     } else {
       ap.n_hl = 0;  // every pair, plain order
@@ -588,10 +604,11 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
       vs_pairs[n_v] = i;
       vs_work[n_v++] = head_work(hd, n_kb, topk_max);
     } else {
-      other[n_o] = i;
-      other_work[n_o++] = head_work(hd, n_kb, topk_max);
+      other[n_o++] = i;
     }
   }
+  interleave_kinds(other, n_o, heads, int(H));
+  for (int i = 0; i < n_o; ++i) other_work[i] = head_work(heads[other[i] % H], n_kb, topk_max);
   AttnParams vp = ap;
   vp.vs_ids = bp.ids;
   vp.vs_masks = bp.masks;
