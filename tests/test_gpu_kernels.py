@@ -301,6 +301,40 @@ def _mixed_patterns(H):
     return {h: list(kinds[h % len(kinds)]) + [1.0] for h in range(H)}
 
 
+MIXED_SHAPES = [
+    # (B, H, H_kv, S_q, S_k, D, dtype)
+    (2, 8, 8, 777, 777, 96, torch.bfloat16),     # batch 2, S not a multiple of 64
+    (1, 6, 1, 1000, 1000, 64, torch.float16),    # one kv head (MQA), D 64, fp16
+    (1, 4, 2, 640, 640, 128, torch.bfloat16),    # D 128, GQA
+    (2, 8, 4, 300, 1324, 96, torch.bfloat16),    # chunked prefill, batch 2
+    (1, 8, 8, 130, 4000, 96, torch.float16),     # short chunk after a long cache
+]
+
+
+@pytest.mark.parametrize("case", MIXED_SHAPES,
+                         ids=[str(c[:6]) + dtype_tag(c[6]) for c in MIXED_SHAPES])
+def test_mixed_layer_shapes(gpu_device, case):
+    """The patched layer's mixed dispatch (stream / block with its estimator /
+    dense in one launch) over batch, GQA / MQA, head dims, fp16 and
+    chunked prefill, against the oracle's per-head layer."""
+    from minference.modules.minference_forward import build_layer_plan, run_layer_attention
+
+    B, H, Hkv, S_q, S_k, D, dtype = case
+    print(f"[mixed] case {case}", flush=True)
+    pats = _mixed_patterns(H)
+    q, k, v = make_qkv(B, H, S_q, S_k, D, dtype, seed=S_q + 7 * H, sink_scale=8.0)
+    k, v = k[:, :Hkv].contiguous(), v[:, :Hkv].contiguous()
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    plan = build_layer_plan(pats, H, D, S_k)
+    out = torch.empty((B, H, S_q, D), dtype=torch.float32, device=gpu_device)
+    run_layer_attention(dq, dk, dv, plan, out)
+    rep = H // Hkv
+    ref, _ = O.layer_attention(np32(q), np.repeat(np32(k), rep, axis=1),
+                               np.repeat(np32(v), rep, axis=1), [pats[h] for h in range(H)],
+                               dtype_tag(dtype))
+    assert_close_f32(out, ref, what=f"mixed layer {case}")
+
+
 @pytest.mark.parametrize("S,H,H_kv", [(1024, 8, 8), (1000, 8, 2), (2048, 16, 16)])
 def test_mixed_layer_strided_views(gpu_device, S, H, H_kv):
     from minference.modules.minference_forward import build_layer_plan, run_layer_attention
