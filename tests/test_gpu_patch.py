@@ -20,17 +20,17 @@ from minference.modules import minference_forward as MF
 pytestmark = pytest.mark.gpu
 
 
-def _tiny_phi3(device, n_heads=8, n_kv=8, layers=2, seed=0):
+def _tiny_phi3(device, n_heads=8, n_kv=8, layers=2, seed=0, dtype=torch.bfloat16):
     from transformers import Phi3Config, Phi3ForCausalLM
 
     torch.manual_seed(seed)
     cfg = Phi3Config(hidden_size=96 * n_heads, intermediate_size=512, num_hidden_layers=layers,
                      num_attention_heads=n_heads, num_key_value_heads=n_kv, vocab_size=256,
                      max_position_embeddings=8192, pad_token_id=0, bos_token_id=1, eos_token_id=2)
-    return Phi3ForCausalLM(cfg).to(device=device, dtype=torch.bfloat16).eval()
+    return Phi3ForCausalLM(cfg).to(device=device, dtype=dtype).eval()
 
 
-def _oracle_layer(q, k, v, plan):
+def _oracle_layer(q, k, v, plan, tag="bf16"):
     qn, kn, vn = (t.detach().float().cpu().numpy() for t in (q, k, v))
     rep = qn.shape[1] // kn.shape[1]
     kn, vn = np.repeat(kn, rep, 1), np.repeat(vn, rep, 1)
@@ -40,16 +40,18 @@ def _oracle_layer(q, k, v, plan):
         if kind == _abi.MSA_KIND_STREAM:
             out[:, sl] = O.streaming_attention(qn[:, sl], kn[:, sl], vn[:, sl], p1, p2, scale=scale)
         elif kind == _abi.MSA_KIND_BLOCK:
-            idx, _ = O.select_block_sparse_topk_indices(qn[:, sl], kn[:, sl], p1, "bf16", scale)
+            idx, _ = O.select_block_sparse_topk_indices(qn[:, sl], kn[:, sl], p1, tag, scale)
             out[:, sl] = O.block_sparse_from_indices(qn[:, sl], kn[:, sl], vn[:, sl], idx, scale=scale)
         else:
             out[:, sl] = O.dense_causal(qn[:, sl], kn[:, sl], vn[:, sl], scale=scale)
     return out
 
 
-@pytest.mark.parametrize("n_kv", [8, 2])
-def test_patched_model_layers_match_oracle(gpu_device, tmp_path, monkeypatch, n_kv):
-    model = _tiny_phi3(gpu_device, n_kv=n_kv)
+@pytest.mark.parametrize("n_kv,dtype", [(8, torch.bfloat16), (2, torch.bfloat16), (8, torch.float16)],
+                         ids=["kv8-bf16", "kv2-bf16", "kv8-fp16"])
+def test_patched_model_layers_match_oracle(gpu_device, tmp_path, monkeypatch, n_kv, dtype):
+    model = _tiny_phi3(gpu_device, n_kv=n_kv, dtype=dtype)
+    tag = "bf16" if dtype == torch.bfloat16 else "fp16"
     recs = [P.record("stream_llm", 64, 256), P.record("block_sparse", 4), P.record("dense"),
             P.record("block_sparse", 100), P.record("stream_llm", 0, 128), P.record("block_sparse", 1),
             P.record("stream_llm", 128, 512), P.record("dense")]
@@ -73,9 +75,11 @@ def test_patched_model_layers_match_oracle(gpu_device, tmp_path, monkeypatch, n_
     assert len(captured) == 2
     for q, k, v, plan, got in captured:
         assert not plan.all_dense
-        ref = _oracle_layer(q, k, v, plan)
+        assert q.dtype == dtype
+        ref = _oracle_layer(q, k, v, plan, tag)
         g = got.cpu().numpy().astype(np.float64)
-        bound = 2e-3 + np.abs(ref) * 2.0 ** -8  # bf16 output of the model
+        # the model's output dtype: one rounding (bf16 2^-8, fp16 2^-11 relative)
+        bound = 2e-3 + np.abs(ref) * (2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11)
         assert (np.abs(g - ref) <= bound).all(), np.abs(g - ref).max()
 
 
