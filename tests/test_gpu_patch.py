@@ -155,12 +155,14 @@ def test_patched_chunked_prefill_and_decode_match_oracle(gpu_device, tmp_path, m
         assert (np.abs(g - ref) <= bound).all(), (kind, q.shape, np.abs(g - ref).max())
 
 
-@pytest.mark.parametrize("n_kv", [8, 2])
-def test_patched_model_vertical_and_slash_heads(gpu_device, tmp_path, monkeypatch, n_kv):
+@pytest.mark.parametrize("n_kv,dtype", [(8, torch.bfloat16), (2, torch.bfloat16), (8, torch.float16)],
+                         ids=["kv8-bf16", "kv2-bf16", "kv8-fp16"])
+def test_patched_model_vertical_and_slash_heads(gpu_device, tmp_path, monkeypatch, n_kv, dtype):
     """vertical_and_slash heads (explicit records and the default for heads
     missing from the JSON) next to the other kinds; every layer launch is
     checked against the oracle estimator + attention on its own inputs."""
-    model = _tiny_phi3(gpu_device, n_kv=n_kv)
+    model = _tiny_phi3(gpu_device, n_kv=n_kv, dtype=dtype)
+    tag = "bf16" if dtype == torch.bfloat16 else "fp16"
     layer0 = {"0": P.record("stream_llm", 64, 256), "2": ["vertical_and_slash", 100, 200, 1],
               "3": P.record("block_sparse", 4), "5": P.record("dense"),
               "6": ["vertical_and_slash", 30, 800, 1]}
@@ -188,13 +190,14 @@ def test_patched_model_vertical_and_slash_heads(gpu_device, tmp_path, monkeypatc
         qn, kn, vn = (t.detach().float().cpu().numpy() for t in (q, k, v))
         rep = qn.shape[1] // kn.shape[1]
         kr, vr = np.repeat(kn, rep, 1), np.repeat(vn, rep, 1)
-        ref = _oracle_layer(q, k, v, plan)
+        ref = _oracle_layer(q, k, v, plan, tag)
         for h, (kind, p1, p2, slot, scale) in enumerate(plan.heads):
             if kind == _abi.MSA_KIND_VS:
                 sl = slice(h, h + 1)
-                vi, si = O.vs_estimate(qn[:, sl], kr[:, sl], p1, p2, "bf16")
+                vi, si = O.vs_estimate(qn[:, sl], kr[:, sl], p1, p2, tag)
                 ref[:, sl] = O.vertical_slash_from_indices(qn[:, sl], kr[:, sl], vr[:, sl], vi, si,
                                                            scale=scale)
         g = got.cpu().numpy().astype(np.float64)
-        bound = 2e-3 + np.abs(ref) * 2.0 ** -8  # bf16 output of the model
+        # the model's output dtype: one rounding (bf16 2^-8, fp16 2^-11 relative)
+        bound = 2e-3 + np.abs(ref) * (2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11)
         assert (np.abs(g - ref) <= bound).all(), np.abs(g - ref).max()
