@@ -178,6 +178,9 @@ def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan:
     """
     _abi.require_device(q, k, v)
     B, H, S_q, _ = q.shape
+    if H > _abi.MSA_MAX_HEADS:
+        raise NotImplementedError(
+            f"one attention launch takes at most {_abi.MSA_MAX_HEADS} query heads, got {H}")
     if plan.vs_heads and B * H > _abi.MSA_MAX_HEADS:
         # vertical_and_slash layers run in batch slices of at most MSA_MAX_HEADS heads
         step = max(1, _abi.MSA_MAX_HEADS // H)

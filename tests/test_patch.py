@@ -9,6 +9,7 @@ unpatched HF model.  The product code itself has no CPU path."""
 from __future__ import annotations
 
 import json
+import os
 import math
 
 import numpy as np
@@ -42,14 +43,33 @@ def test_config_semantics(tmp_path):
         patch_hf(torch.nn.Module(), attn_type="hf")
 
 
-def test_registered_config_is_headline_mix():
-    from minference.configs.model2path import MODEL2PATH
+def test_registered_config_is_reference_default():
+    """The Phi-3 name selects the reference's registered pattern
+    (minference/configs/model2path.py:16-19): stream_llm(128, 896) on the 43
+    probe heads, dense elsewhere; same content as the reference's file
+    (hash recorded from it in tests/golden/pattern_configs.json)."""
+    import hashlib
 
-    cfg = json.load(open(MODEL2PATH["microsoft/Phi-3-mini-128k-instruct"]))
+    from minference.configs import model2path as M
+
+    path = M.MODEL2PATH["microsoft/Phi-3-mini-128k-instruct"]
+    assert os.path.basename(path) == M.PHI3_DEFAULT_NAME
+    cfg = json.load(open(path))
     assert len(cfg) == 32 and all(len(layer) == 32 for layer in cfg)
-    kinds = [rec[0] for layer in cfg for rec in layer.values()]
+    recs = [tuple(rec[:3]) for layer in cfg for rec in layer.values()]
+    assert recs.count(("stream_llm", 128, 896)) == 43 and recs.count(("dense", 0, 0)) == 981
+    golden = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                         "pattern_configs.json")))
+    sha = hashlib.sha256(json.dumps(cfg).encode()).hexdigest()
+    assert sha == golden["files"][M.PHI3_DEFAULT_NAME]["sha256"]
+    assert cfg == M.default_phi3_config()
+    # the probe table is the stream_llm heads of the original best pattern
+    assert [list(t) for t in M.PHI3_PROBE_HEADS] == golden["best_pattern"]["stream_scores"]
+    # the benchmark's all-sparse mix stays available by path
+    mix = json.load(open(M.NAMED_CONFIGS["phi3_stream_block_50_50"]))
+    kinds = [rec[0] for layer in mix for rec in layer.values()]
     assert kinds.count("stream_llm") == 512 and kinds.count("block_sparse") == 512
-    assert cfg == P.headline_config(seed=0)
+    assert mix == P.headline_config(seed=0)
 
 
 def test_mixed_config_counts_and_seed():
@@ -201,6 +221,61 @@ def test_patched_sparse_layer_uses_plan(tmp_path, cpu_launch, monkeypatch):
     assert seen[0].all_dense and seen[0].heads[0][4] == 1.0 / math.sqrt(96)  # layer 0 < starting_layer
     assert seen[1].heads[0] == (_abi.MSA_KIND_STREAM, 16, 64, -1, 128 ** -0.5)
     assert seen[1].heads[1] == (_abi.MSA_KIND_BLOCK, 2, 0, 0, 128 ** -0.5)
+
+
+def _mask_spy(model):
+    """Wraps every attention module's forward to record the attention_mask
+    it receives."""
+    seen = []
+    for layer in model.model.layers:
+        attn = layer.self_attn
+        inner = attn.forward
+
+        def spy(*a, _inner=inner, **kw):
+            seen.append(kw.get("attention_mask", a[2] if len(a) > 2 else None))
+            return _inner(*a, **kw)
+
+        attn.forward = spy
+    return seen
+
+
+def test_patched_layers_receive_no_mask(tmp_path, cpu_launch):
+    """The 4D-mask skip (reference minference/patch.py:39-87): under the
+    "minference" implementation HF builds no [B, 1, S, S] mask and every
+    patched layer gets attention_mask=None (a 128K eager mask is 34 GB).  The
+    unpatched eager model on the same ids does get a 4D mask, so the spy
+    sees what it claims to."""
+    ids = torch.randint(3, 128, (1, 96), generator=torch.Generator().manual_seed(5))
+    eager = _tiny_phi3()
+    eager.set_attn_implementation("eager")
+    seen_eager = _mask_spy(eager)
+    with torch.no_grad():
+        eager(ids)
+    assert len(seen_eager) == 2
+    assert all(isinstance(m, torch.Tensor) and m.dim() == 4 for m in seen_eager)
+
+    path = tmp_path / "dense.json"
+    P.write(str(path), P.uniform_config("dense", n_layers=2, n_heads=2))
+    patched = MInference(attn_type="minference", config_path=str(path))(_tiny_phi3())
+    seen = _mask_spy(patched)
+    with torch.no_grad():
+        patched(ids, attention_mask=torch.ones_like(ids))
+        patched(ids)
+    assert len(seen) == 4 and all(m is None for m in seen)
+
+
+def test_more_heads_than_one_launch_raises(monkeypatch):
+    """A layer with more than MSA_MAX_HEADS query heads is refused with a
+    clear error before any launch (no recursion through batch slices)."""
+    monkeypatch.setattr(_abi, "require_device", lambda *t: None)
+    H = _abi.MSA_MAX_HEADS + 8
+    plan = MF.build_layer_plan({}, H, 64, 64)  # every head defaults to vertical_and_slash
+    q = torch.zeros(2, H, 64, 64, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="heads"):
+        MF.run_layer_attention(q, q, q, plan, torch.empty_like(q))
+    dense = MF.dense_plan(H, 64)
+    with pytest.raises(NotImplementedError, match="heads"):
+        MF.run_layer_attention(q, q, q, dense, torch.empty_like(q))
 
 
 def test_hf_attn_type_leaves_model_unpatched():
