@@ -54,6 +54,12 @@ WORKLOADS = {
     "cfg5_prefill128k": (131072, 0, 0, 0, 0, 0, 0),
 }
 
+# Selector option per single-layer workload: BASELINE config 2 states "with
+# the diagonal and first block always included" (MSA_SELECT_FORCE_FIRST |
+# MSA_SELECT_FORCE_DIAG, inside the top-k); the others use the reference's
+# plain top-k.
+SELECT_FORCE = {"cfg2_block16k": (True, True)}
+
 # Per-head pattern mixes of the full-prefill workloads over all 1024 heads,
 # drawn by configs.patterns.mixed_config from the bench seed.
 MODEL_MIX = {
@@ -108,6 +114,24 @@ def block_tiles(s, topk):
     nb = -(-s // BLOCK)
     k = min(topk, nb)
     return sum(min(k, b + 1) for b in range(nb))
+
+
+def layer_patterns(workload, H, seed):
+    """Per-head pattern records of a single-layer workload: the workload's
+    stream / block / dense counts scaled to H heads, assigned to heads by a
+    seeded shuffle.  Returns ({head: record}, (n_stream, n_block, n_dense))."""
+    import random
+
+    S, n_stream, n_block, n_dense, n_init, n_local, topk = WORKLOADS[workload]
+    scale_h = H / (n_stream + n_block + n_dense)
+    n_stream, n_block = int(round(n_stream * scale_h)), int(round(n_block * scale_h))
+    n_dense = H - n_stream - n_block
+    kinds = (["stream_llm"] * n_stream + ["block_sparse"] * n_block + ["dense"] * n_dense)
+    random.Random(seed).shuffle(kinds)
+    rec = {"stream_llm": ["stream_llm", n_init, n_local, 1.0],
+           "block_sparse": ["block_sparse", topk, 0, 1.0],
+           "dense": ["dense", 0, 0, 1.0]}
+    return {h: list(rec[kd]) for h, kd in enumerate(kinds)}, (n_stream, n_block, n_dense)
 
 
 def make_inputs(S, H, D, seed, device):
@@ -235,18 +259,7 @@ def main():
         return model_bench(args, dev)
     S, n_stream, n_block, n_dense, n_init, n_local, topk = WORKLOADS[args.workload]
     H, D = args.heads, args.dim
-    scale_h = H / (n_stream + n_block + n_dense)
-    n_stream, n_block = int(round(n_stream * scale_h)), int(round(n_block * scale_h))
-    n_dense = H - n_stream - n_block
-    kinds = (["stream_llm"] * n_stream + ["block_sparse"] * n_block + ["dense"] * n_dense)
-    import random
-
-    random.Random(args.seed).shuffle(kinds)
-    pats = {}
-    for h, kd in enumerate(kinds):
-        pats[h] = {"stream_llm": ["stream_llm", n_init, n_local, 1.0],
-                   "block_sparse": ["block_sparse", topk, 0, 1.0],
-                   "dense": ["dense", 0, 0, 1.0]}[kd]
+    pats, (n_stream, n_block, n_dense) = layer_patterns(args.workload, H, args.seed)
     plan = build_layer_plan(pats, H, D, S)
 
     q, k, v = make_inputs(S, H, D, args.seed, dev)
@@ -260,10 +273,14 @@ def main():
     s_sparse = sparse_scale(D)
     stream = torch.cuda.current_stream(dev)
 
+    force_first, force_diag = SELECT_FORCE.get(args.workload, (False, False))
+    sel_flags = ((_abi.MSA_SELECT_FORCE_FIRST if force_first else 0)
+                 | (_abi.MSA_SELECT_FORCE_DIAG if force_diag else 0))
+
     def launch_est():
         if n_slots:
             _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max,
-                                s_sparse, idx, cnt, ws_est)
+                                s_sparse, idx, cnt, ws_est, flags=sel_flags)
 
     def launch_stage():
         _abi.stage_kv(k, v, ws_att)
@@ -340,6 +357,8 @@ def main():
             "head_dim": D,
             "mix": {"stream_llm(%d,%d)" % (n_init, n_local): n_stream,
                     "block_sparse(top-%d)" % topk: n_block, "dense": n_dense},
+            "selector": ("top-%d, first and diagonal blocks forced" % topk if sel_flags
+                         else "top-%d (reference selector)" % topk),
             "global_batch": 1,
             "parallelism": "single GPU",
         },

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MSA_ABI_VERSION 5
+#define MSA_ABI_VERSION 6
 
 /* status codes (negative: validation, nothing launched) */
 #define MSA_OK 0
@@ -42,7 +42,7 @@ extern "C" {
 #define MSA_E_TOPK (-7)        /* topk < 1 or topk > n_kv_blocks */
 #define MSA_E_HEADS (-8)       /* bad head count / head index / kind */
 #define MSA_E_WORKSPACE (-9)   /* workspace missing or too small */
-#define MSA_E_SEQ (-10)        /* S_q > S_k, S_q == 0, or too long */
+#define MSA_E_SEQ (-10)        /* S_q > S_k (causal kinds), S_q == 0, or too long */
 #define MSA_E_SLOTS (-11)      /* sparse head without an index slot, or bad index lists */
 
 /* element types */
@@ -55,6 +55,11 @@ extern "C" {
 #define MSA_KIND_STREAM 1 /* "stream_llm"   */
 #define MSA_KIND_BLOCK 2  /* "block_sparse" */
 #define MSA_KIND_VS 3     /* "vertical_and_slash" */
+#define MSA_KIND_FULL 4   /* dense without the causal mask (dense_attention(causal=False)) */
+
+/* msa_block_estimate_ex flags */
+#define MSA_SELECT_FORCE_FIRST 1 /* block 0 always selected */
+#define MSA_SELECT_FORCE_DIAG 2  /* the query block's own block always selected */
 
 #define MSA_VS_MAX_SEQ 131072 /* longest S of a vertical_and_slash head */
 
@@ -123,8 +128,26 @@ int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k,
                        void* workspace, size_t workspace_bytes,
                        msa_stream_t stream);
 
+/* msa_block_estimate with selection flags (MSA_SELECT_*; 0 = the reference
+ * selector, identical to msa_block_estimate).  FORCE_FIRST / FORCE_DIAG keep
+ * block 0 / block bq (the query block's own, q-block frame) in every row's
+ * selection, inside the top-k: forced ids rank above every scored id, and
+ * between the two the lower id wins (top-k 1 with both flags keeps block 0).
+ * The reference selector has no such option; it serves selection rules that
+ * always keep the diagonal and first block.  Same counterpart as
+ * msa_block_estimate
+ * (minference/ops/block_sparse_kernel_npu.py:230-263). */
+int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k,
+                          const int32_t* slot_heads, const int32_t* slot_topk,
+                          int32_t n_slots, int32_t block, int32_t topk_max,
+                          float score_scale, int32_t flags, int32_t* idx,
+                          int32_t* cnt, void* workspace, size_t workspace_bytes,
+                          msa_stream_t stream);
+
 /* Bytes of workspace msa_layer_attention needs: K and V staged once per
- * layer in MFMA operand order (V as fp16). */
+ * layer in MFMA operand order (V as fp16, scaled per kv head by a power of
+ * two when its magnitude exceeds the fp16 range, with the exponent kept in
+ * the workspace and undone at the output; Inf and NaN pass through). */
 size_t msa_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t s_k,
                                      int32_t head_dim);
 
@@ -138,7 +161,10 @@ size_t msa_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t s_
  * msa_block_estimate outputs (or caller-built lists sorted ascending; entries
  * outside [0, n_kv_blocks), repeated or in the causal future are skipped);
  * they may be NULL when no head is block_sparse.  o may be bf16/fp16 (== q's
- * dtype) or fp32.  Rows with no visible key are written as 0. */
+ * dtype) or fp32.  Rows with no visible key are written as 0.
+ * MSA_KIND_FULL heads see every key (dense_attention(causal=False),
+ * minference/backend_npu/attention.py:221-230); S_q > S_k is accepted only
+ * when every head is MSA_KIND_FULL. */
 int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k,
                         const msa_tensor4* v, const msa_tensor4* o,
                         const msa_head_desc* heads, int32_t n_heads,

@@ -39,6 +39,12 @@ bool aligned(const msa_tensor4* t) {
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Typed pointer at a byte offset of a caller's workspace.
+template <typename P>
+P* ws_at(void* workspace, size_t off) {
+  return reinterpret_cast<P*>(static_cast<unsigned char*>(workspace) + off);
+}
+
 int check_qk(const msa_tensor4* q, const msa_tensor4* k) {
   if (!q || !k || !q->data || !k->data) return MSA_E_NULL;
   for (int i = 0; i < 4; ++i)
@@ -71,7 +77,7 @@ const char* msa_status_str(int status) {
     case MSA_E_TOPK: return "topk must be in [1, n_kv_blocks]";
     case MSA_E_HEADS: return "bad head count, head index or head kind";
     case MSA_E_WORKSPACE: return "workspace missing or too small";
-    case MSA_E_SEQ: return "sequence lengths must satisfy 0 < S_q <= S_k <= 2^20";
+    case MSA_E_SEQ: return "sequence lengths must satisfy 0 < S_q <= S_k <= 2^20 (S_q > S_k only for full heads)";
     case MSA_E_SLOTS: return "sparse head without a valid index slot, or bad idx/cnt or vertical_and_slash lists";
     default: break;
   }
@@ -91,6 +97,16 @@ int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t
                        const int32_t* slot_topk, int32_t n_slots, int32_t block,
                        int32_t topk_max, float score_scale, int32_t* idx, int32_t* cnt,
                        void* workspace, size_t workspace_bytes, msa_stream_t stream) {
+  return msa_block_estimate_ex(q, k, slot_heads, slot_topk, n_slots, block, topk_max,
+                               score_scale, 0, idx, cnt, workspace, workspace_bytes, stream);
+}
+
+int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int32_t* slot_heads,
+                          const int32_t* slot_topk, int32_t n_slots, int32_t block,
+                          int32_t topk_max, float score_scale, int32_t flags, int32_t* idx,
+                          int32_t* cnt, void* workspace, size_t workspace_bytes,
+                          msa_stream_t stream) {
+  if ((flags & ~(MSA_SELECT_FORCE_FIRST | MSA_SELECT_FORCE_DIAG)) != 0) return MSA_E_TOPK;
   int st = check_qk(q, k);
   if (st != MSA_OK) return st;
   if (block != MSA_BLOCK) return MSA_E_BLOCK;
@@ -151,18 +167,35 @@ int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t
   sp.s_q = int(q->size[2]);
   sp.s_k = int(k->size[2]);
   sp.scale = score_scale;
+  sp.flags = flags;
   for (int s = 0; s < n_slots; ++s) sp.slot_topk[s] = int16_t(slot_topk ? slot_topk[s] : topk_max);
   e = launch_score(sp, D, hs);
   return e == hipSuccess ? MSA_OK : int(e);
 }
 
+// Attention workspace: staged V operands (fp16), staged K operands (input
+// dtype), per-tile V maxima (fp32), per-head V exponents (int32), then the
+// work-queue counters of the attention launch.
+struct AttnLayout {
+  size_t vt, kt, tmax, vexp, total;
+};
+
+static AttnLayout attn_layout(int64_t B, int64_t Hkv, int64_t Sk, int64_t D) {
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  const int64_t n_kb = cdiv(Sk, MSA_BLOCK);
+  AttnLayout L;
+  L.vt = 0;
+  L.kt = size_t(B * Hkv * D * n_kb * MSA_BLOCK) * 2;
+  L.tmax = L.kt * 2;
+  L.vexp = up(L.tmax + size_t(B * Hkv * n_kb) * 4);
+  L.total = up(L.vexp + size_t(B * Hkv) * 4) + kQueueBytes;
+  return L;
+}
+
 size_t msa_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t s_k,
                                      int32_t head_dim) {
   if (batch <= 0 || kv_heads <= 0 || s_k <= 0 || head_dim <= 0) return 0;
-  // staged V operands (fp16), staged K operands (input dtype), then the
-  // work-queue counters of the attention launch
-  const int64_t bytes = 2 * batch * kv_heads * head_dim * cdiv(s_k, MSA_BLOCK) * MSA_BLOCK * 2;
-  return size_t((bytes + 255) / 256 * 256) + kQueueBytes;
+  return attn_layout(batch, kv_heads, s_k, head_dim).total;
 }
 
 // work-queue counters at the end of the attention workspace
@@ -180,11 +213,6 @@ static int cus_per_xcd() {
   return cus >= 8 ? cus / 8 : 1;
 }
 
-// K and V halves of the attention workspace
-static uint16_t* staged_v(void* workspace) { return static_cast<uint16_t*>(workspace); }
-static uint16_t* staged_k(void* workspace, int64_t B, int64_t Hkv, int64_t Sk, int D) {
-  return staged_v(workspace) + B * Hkv * D * cdiv(Sk, MSA_BLOCK) * MSA_BLOCK;
-}
 
 static int stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
                     size_t workspace_bytes, hipStream_t hs) {
@@ -210,13 +238,17 @@ static int stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
   sp.v = v->data;
   sp.k_sb = k->stride[0]; sp.k_sh = k->stride[1]; sp.k_ss = k->stride[2];
   sp.v_sb = v->stride[0]; sp.v_sh = v->stride[1]; sp.v_ss = v->stride[2];
-  sp.vt = staged_v(workspace);
-  sp.kt = staged_k(workspace, B, Hkv, Sk, D);
+  const AttnLayout L = attn_layout(B, Hkv, Sk, D);
+  sp.vt = ws_at<uint16_t>(workspace, L.vt);
+  sp.kt = ws_at<uint16_t>(workspace, L.kt);
+  sp.tmax = ws_at<float>(workspace, L.tmax);
+  sp.vexp = ws_at<int32_t>(workspace, L.vexp);
   sp.batch = int(B);
   sp.kv_heads = int(Hkv);
   sp.s_k = int(Sk);
   sp.s_pad = int(cdiv(Sk, MSA_BLOCK) * MSA_BLOCK);
-  const hipError_t e = launch_stage(sp, v->dtype, D, hs);
+  hipError_t e = launch_stage(sp, v->dtype, D, hs);
+  if (e == hipSuccess) e = launch_vscale(sp, v->dtype, D, hs);
   return e == hipSuccess ? MSA_OK : int(e);
 }
 
@@ -354,11 +386,12 @@ size_t msa_vs_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_k, int32
 // the output merge).  The prefix sums have a closed form.
 struct HeadWork {
   double cap, fixed;
+  bool flat;  // every query block costs cap (no causal triangle)
 };
 
 static HeadWork head_work(const msa_head_desc& hd, int n_kb, int topk_max) {
   const double nb = double(n_kb);
-  HeadWork w{nb, 2.0};
+  HeadWork w{nb, 2.0, hd.kind == MSA_KIND_FULL};
   if (hd.kind == MSA_KIND_STREAM) {
     w.cap = fmin(nb, double(hd.p2) / 64.0 + 2.0 + ceil(fmax(double(hd.p1), 0.0) / 64.0));
   } else if (hd.kind == MSA_KIND_BLOCK) {
@@ -374,6 +407,7 @@ static HeadWork head_work(const msa_head_desc& hd, int n_kb, int topk_max) {
 // cost of query blocks 0 .. m-1
 static double prefix_cost(const HeadWork& w, double m) {
   const double k = w.cap;
+  if (w.flat) return m * (k + w.fixed);
   const double tri = m <= k ? m * (m + 1) / 2 : k * (k + 1) / 2 + (m - k) * k;
   return tri + w.fixed * m;
 }
@@ -449,7 +483,6 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   const int64_t B = q->size[0], H = q->size[1], Hkv = k->size[1];
   const int64_t Sq = q->size[2], Sk = k->size[2];
   const int D = int(q->size[3]);
-  if (Sq > Sk) return MSA_E_SEQ;
   if (n_heads != H || H > kMaxHeads) return MSA_E_HEADS;
   const int n_qb = int(cdiv(Sq, MSA_BLOCK));
   const int n_kb = int(cdiv(Sk, MSA_BLOCK));
@@ -459,8 +492,11 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   for (int h = 0; h < n_heads; ++h) {
     const msa_head_desc& hd = heads[h];
     if (hd.kind != MSA_KIND_DENSE && hd.kind != MSA_KIND_STREAM && hd.kind != MSA_KIND_BLOCK &&
-        hd.kind != MSA_KIND_VS)
+        hd.kind != MSA_KIND_VS && hd.kind != MSA_KIND_FULL)
       return MSA_E_HEADS;
+    // S_q > S_k only without causal masking (no absolute row of the causal
+    // kinds would exist for the first query rows)
+    if (Sq > Sk && hd.kind != MSA_KIND_FULL) return MSA_E_SEQ;
     if (!(hd.scale > 0.0f) || !isfinite(hd.scale)) return MSA_E_HEADS;
     if (hd.kind == MSA_KIND_BLOCK) {
       any_block = true;
@@ -509,8 +545,11 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   memset(&ap, 0, sizeof(ap));
   ap.q = q->data;
   ap.k = k->data;
-  ap.vt = staged_v(workspace);
-  ap.kt = staged_k(workspace, B, Hkv, Sk, D);
+  const AttnLayout AL = attn_layout(B, Hkv, Sk, D);
+  ap.vt = ws_at<uint16_t>(workspace, AL.vt);
+  ap.kt = ws_at<uint16_t>(workspace, AL.kt);
+  int32_t* vexp = ws_at<int32_t>(workspace, AL.vexp);
+  ap.vexp = vexp;
   ap.o = o->data;
   ap.q_sb = q->stride[0]; ap.q_sh = q->stride[1]; ap.q_ss = q->stride[2];
   ap.k_sb = k->stride[0]; ap.k_sh = k->stride[1]; ap.k_ss = k->stride[2];
@@ -587,6 +626,7 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   gp.kv_heads = int(Hkv);
   gp.s_k = int(Sk);
   gp.s_pad = vl.nv_pad;
+  gp.vexp = vexp;  // the heads' V exponents from the plain staging
   gp.rows = vs->v_idx;
   gp.rows_cnt = vs->v_cnt;
   gp.rows_stride = vs->v_stride;

@@ -3,12 +3,13 @@
 // Work item = (head, 64-row query block).  Each item walks a list of 64-key
 // tiles whose shape depends on the head kind:
 //   dense        : every causal tile 0..diag              (backend_npu/attention.py:192-255)
+//   full         : every key tile (dense, causal=False)   (backend_npu/attention.py:221-230)
 //   stream_llm   : sink tiles, then the local band tiles  (ops/streaming_kernel_npu.py:94-146)
 //   block_sparse : the estimator's block ids              (ops/block_sparse_kernel_npu.py:266-348,
 //                                                          ops/tilelang_sparse_attention_h1.py:367-683)
 // Token visibility (exact reference masks; row a is the absolute position
 // i + S_k - S_q):
-//   all kinds : j <= a and j < S_k
+//   all kinds : j < S_k, and j <= a except for full heads
 //   stream    : and (j > a - n_local or j < n_init)
 // Rows with no visible key produce 0 (the reference's nan_to_num).
 //
@@ -44,6 +45,7 @@ constexpr int KIND_DENSE = 0;
 constexpr int KIND_STREAM = 1;
 constexpr int KIND_BLOCK = 2;
 constexpr int KIND_VS = 3;
+constexpr int KIND_FULL = 4;  // dense without the causal mask
 
 // ---------------------------------------------------------------------------
 // Per-layer staging of K and V into MFMA operand order, zero padded to
@@ -54,42 +56,116 @@ constexpr int KIND_VS = 3;
 //     V[16 chunk + 8 (l >> 5) + e][32 db + (l & 31)]     (PV A operand, 32x32x16)
 // so a wave reads every operand as one contiguous 1 KB.  blockIdx.z = 1
 // stages K (a permutation of 16-byte granules), 0 stages V (a transpose
-// through LDS, converted to fp16 with saturation).  In gather mode the keys
-// of a slot are the listed rows (the vertical columns of a
-// vertical_and_slash head) instead of 0 .. s_k-1.
+// through LDS, converted to fp16).  In gather mode the keys of a slot are
+// the listed rows (the vertical columns of a vertical_and_slash head)
+// instead of 0 .. s_k-1.
+//
+// V range: fp16 holds finite magnitudes up to 65504, bf16 far more.  A V
+// tile is converted with saturation and reports its largest finite |V|
+// (tmax); vscale_kernel then restages, times an exact power of two 2^-e, the
+// V of any head whose maximum exceeds 65504, and the attention kernel
+// multiplies that head's output by 2^e.  Inf and NaN are kept as they are.
 // ---------------------------------------------------------------------------
+template <int D>
+struct StageShape {
+  static constexpr int KCH = D / 8;   // 16-byte chunks per row
+  static constexpr int NDB = D / 32;  // 32-dim operand blocks
+  static constexpr int LP = D + 8;    // padded LDS row (halves)
+};
+
+// Source row of staged key j of head bk (-1: a zero key).
+struct StageRows {
+  const int32_t* rows;
+  int rcnt, s_k;
+  __device__ int operator()(int j) const {
+    if (rows) return j < rcnt ? min(max(rows[j], 0), s_k - 1) : -1;
+    return j < s_k ? j : -1;
+  }
+};
+
+__device__ inline float block_max256(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return v;
+}
+
+// V of 64 keys from j0 (staged row index) of head bk, times sc, into the
+// operand layout; returns the largest finite |V| read (before scaling),
+// reduced over the workgroup.
+template <typename T, int D>
+__device__ float stage_v_tile(const StageParams& P, const uint16_t* src, const StageRows& src_row,
+                              int64_t bk, int j0, float sc, uint16_t* tile, float* red) {
+  using SS = StageShape<D>;
+  float vmax = 0.0f;
+  for (int ci = threadIdx.x; ci < kBlock * SS::KCH; ci += 256) {
+    const int r = ci / SS::KCH, c = ci - r * SS::KCH;
+    const int j = src_row(j0 + r);
+    u32x4 out = zero_u32x4();
+    if (j >= 0) {
+      const u32x4 in = load16(src + int64_t(j) * P.v_ss + c * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float flo = T::to_float(uint16_t(in[e] & 0xffffu));
+        const float fhi = T::to_float(uint16_t(in[e] >> 16));
+        vmax = fmaxf(vmax, fmaxf(finite_abs(flo), finite_abs(fhi)));
+        const _Float16 lo = to_f16_scaled(flo, sc);
+        const _Float16 hi = to_f16_scaled(fhi, sc);
+        out[e] = uint32_t(__builtin_bit_cast(uint16_t, lo)) |
+                 (uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16);
+      }
+    }
+    store16(&tile[r * SS::LP + c * 8], out);
+  }
+  __syncthreads();
+  const int64_t dst0 = (bk * P.s_pad + j0) * D;
+  for (int ci = threadIdx.x; ci < 4 * SS::NDB * 64; ci += 256) {
+    const int l = ci & 63;
+    const int cd = ci >> 6;  // chunk * NDB + db
+    const int c = cd / SS::NDB, db = cd - c * SS::NDB;
+    const int key0 = 16 * c + 8 * (l >> 5);
+    const int d = 32 * db + (l & 31);
+    u32x4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t lo = tile[(key0 + 2 * e) * SS::LP + d];
+      const uint16_t hi = tile[(key0 + 2 * e + 1) * SS::LP + d];
+      out[e] = uint32_t(lo) | (uint32_t(hi) << 16);
+    }
+    store16(P.vt + dst0 + ci * 8, out);
+  }
+  return block_max256(vmax, red);  // its barriers also free `tile` for reuse
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
-  constexpr int KCH = D / 8;
-  constexpr int NDB = D / 32;
-  constexpr int LP = D + 8;  // padded LDS row (halves)
-  __shared__ __align__(16) uint16_t tile[kBlock * LP];
+  using SS = StageShape<D>;
+  __shared__ __align__(16) uint16_t tile[kBlock * SS::LP];
+  __shared__ float red[4];
   const int j0 = blockIdx.x * kBlock;
   const int bk = blockIdx.y;  // b * kv_heads + kvh (gather mode: b * n_slots + slot)
-  int b, kvh, rcnt = 0;
-  const int32_t* rows = nullptr;
+  int b, kvh;
+  StageRows src_row{nullptr, 0, P.s_k};
   if (P.rows) {
     b = bk / P.n_slots;
     kvh = P.slot_kvh[bk - b * P.n_slots];
-    rows = P.rows + int64_t(bk) * P.rows_stride;
-    rcnt = min(max(P.rows_cnt[bk], 0), P.rows_stride);
+    src_row.rows = P.rows + int64_t(bk) * P.rows_stride;
+    src_row.rcnt = min(max(P.rows_cnt[bk], 0), P.rows_stride);
   } else {
     b = bk / P.kv_heads;
     kvh = bk - b * P.kv_heads;
   }
-  // source row of staged key j, -1 for a zero key
-  auto src_row = [&](int j) -> int {
-    if (rows) return j < rcnt ? min(max(rows[j], 0), P.s_k - 1) : -1;
-    return j < P.s_k ? j : -1;
-  };
   // the tile's 4 chunks are 64*D consecutive halves starting at key j0
   const int64_t dst0 = (int64_t(bk) * P.s_pad + j0) * D;
   if (blockIdx.z == 1) {
     const uint16_t* src = reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + kvh * P.k_sh;
-    for (int gi = threadIdx.x; gi < 4 * NDB * 64; gi += 256) {
+    for (int gi = threadIdx.x; gi < 4 * SS::NDB * 64; gi += 256) {
       const int l = gi & 63;
       const int cks = gi >> 6;  // chunk * NDB + ks
-      const int c = cks / NDB, ks = cks - c * NDB;
+      const int c = cks / SS::NDB, ks = cks - c * SS::NDB;
       const int j = src_row(j0 + 16 * c + (l & 15));
       const u32x4 x = j >= 0 ? load16(src + int64_t(j) * P.k_ss + 32 * ks + 8 * (l >> 4))
                              : zero_u32x4();
@@ -98,44 +174,46 @@ __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
     return;
   }
   const uint16_t* src = reinterpret_cast<const uint16_t*>(P.v) + b * P.v_sb + kvh * P.v_sh;
-  for (int ci = threadIdx.x; ci < kBlock * KCH; ci += 256) {
-    const int r = ci / KCH, c = ci - r * KCH;
-    const int j = src_row(j0 + r);
-    u32x4 out = zero_u32x4();
-    if (j >= 0) {
-      const u32x4 in = load16(src + int64_t(j) * P.v_ss + c * 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const _Float16 lo = to_f16_sat<T>(uint16_t(in[e] & 0xffffu));
-        const _Float16 hi = to_f16_sat<T>(uint16_t(in[e] >> 16));
-        out[e] = uint32_t(__builtin_bit_cast(uint16_t, lo)) |
-                 (uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16);
-      }
-    }
-    store16(&tile[r * LP + c * 8], out);
-  }
-  __syncthreads();
-  for (int ci = threadIdx.x; ci < 4 * NDB * 64; ci += 256) {
-    const int l = ci & 63;
-    const int cd = ci >> 6;  // chunk * NDB + db
-    const int c = cd / NDB, db = cd - c * NDB;
-    const int key0 = 16 * c + 8 * (l >> 5);
-    const int d = 32 * db + (l & 31);
-    u32x4 out;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint16_t lo = tile[(key0 + 2 * e) * LP + d];
-      const uint16_t hi = tile[(key0 + 2 * e + 1) * LP + d];
-      out[e] = uint32_t(lo) | (uint32_t(hi) << 16);
-    }
-    store16(P.vt + dst0 + ci * 8, out);
-  }
+  // gather mode uses the scale the head's plain staging chose
+  const float sc = P.rows ? __builtin_amdgcn_ldexpf(1.0f, -P.vexp[b * P.kv_heads + kvh]) : 1.0f;
+  const float m = stage_v_tile<T, D>(P, src, src_row, bk, j0, sc, tile, red);
+  if (!P.rows && threadIdx.x == 0) P.tmax[int64_t(bk) * (P.s_pad / kBlock) + blockIdx.x] = m;
+}
+
+// One workgroup per (batch, kv head): picks the head's V exponent from the
+// tile maxima and, in the rare case it is not 0, restages the head's V.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void vscale_kernel(StageParams P) {
+  using SS = StageShape<D>;
+  __shared__ __align__(16) uint16_t tile[kBlock * SS::LP];
+  __shared__ float red[4];
+  const int bk = blockIdx.x;
+  const int n_kb = P.s_pad / kBlock;
+  float m = 0.0f;
+  for (int t = threadIdx.x; t < n_kb; t += 256) m = fmaxf(m, P.tmax[int64_t(bk) * n_kb + t]);
+  m = block_max256(m, red);
+  int e = 0;
+  while (m * __builtin_amdgcn_ldexpf(1.0f, -e) > kF16Max) ++e;  // m < 2^128: e <= 113
+  if (threadIdx.x == 0) P.vexp[bk] = e;
+  if (e == 0) return;
+  const int b = bk / P.kv_heads;
+  const int kvh = bk - b * P.kv_heads;
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(P.v) + b * P.v_sb + kvh * P.v_sh;
+  const StageRows src_row{nullptr, 0, P.s_k};
+  const float sc = __builtin_amdgcn_ldexpf(1.0f, -e);
+  for (int t = 0; t < n_kb; ++t) stage_v_tile<T, D>(P, src, src_row, bk, t * kBlock, sc, tile, red);
 }
 
 template <typename T, int D>
 static hipError_t launch_stage_t(const StageParams& p, hipStream_t st) {
   dim3 grid(p.s_pad / kBlock, p.batch * (p.rows ? p.n_slots : p.kv_heads), 2);
   hipLaunchKernelGGL((stage_kernel<T, D>), grid, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t launch_vscale_t(const StageParams& p, hipStream_t st) {
+  hipLaunchKernelGGL((vscale_kernel<T, D>), dim3(p.batch * p.kv_heads), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -148,6 +226,17 @@ hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st) 
   if (D == 64) return launch_stage_t<F16, 64>(p, st);
   if (D == 96) return launch_stage_t<F16, 96>(p, st);
   return launch_stage_t<F16, 128>(p, st);
+}
+
+hipError_t launch_vscale(const StageParams& p, int dtype, int D, hipStream_t st) {
+  if (dtype == Bf16::id) {
+    if (D == 64) return launch_vscale_t<Bf16, 64>(p, st);
+    if (D == 96) return launch_vscale_t<Bf16, 96>(p, st);
+    return launch_vscale_t<Bf16, 128>(p, st);
+  }
+  if (D == 64) return launch_vscale_t<F16, 64>(p, st);
+  if (D == 96) return launch_vscale_t<F16, 96>(p, st);
+  return launch_vscale_t<F16, 128>(p, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -372,11 +461,16 @@ void attn_kernel(AttnParams P) {
     // full sink, full band | partial sink, band tiles cut by the window
     // start, diagonal / S_k boundary
     seq.set({0, bf0, sf, lo, fb_hi}, {sf, fb_hi, nsink, bf0, last_tile + 1}, 2);
+  } else if (kind == KIND_FULL) {
+    const int ff = P.s_k >> 6;  // tiles whose keys are all below S_k
+    seq.set({0, ff, 0, 0, 0}, {ff, P.n_kb, 0, 0, 0}, 1);
   } else {
     seq.set({0, Fe, 0, 0, 0}, {Fe, last_tile + 1, 0, 0, 0}, 1);
   }
 
   const int64_t bk = int64_t(b) * (P.heads / P.kv_group) + kvh;
+  // staged V is V * 2^-vexp (stage_kernel); the output takes the 2^vexp back
+  const float vfac = __builtin_amdgcn_ldexpf(1.0f, load_uniform(P.vexp + bk));
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(P.kt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -458,6 +552,7 @@ void attn_kernel(AttnParams P) {
   const float c_log2 = hd.scale_log2;
   const int arow0 = a0 + lc;  // absolute position of this lane's row in group 0
   const int skm1 = P.s_k - 1;
+  const bool is_full = kind == KIND_FULL;
   const bool is_stream = kind == KIND_STREAM;
   const int sink_hi = is_stream ? n_init : 0;
 
@@ -497,7 +592,7 @@ void attn_kernel(AttnParams P) {
 #pragma unroll
     for (int gg = 0; gg < 2; ++gg) {
       const int ar = arow0 + 16 * (2 * hf + gg);
-      const int key_hi = min(ar, skm1);
+      const int key_hi = is_full ? skm1 : min(ar, skm1);
       const int band_lo = is_stream ? ar - n_local + 1 : 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -684,7 +779,7 @@ void attn_kernel(AttnParams P) {
       f[v] = __builtin_amdgcn_exp2f(mw[v] - mt);
       lt += lw[v] * f[v];
     }
-    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    const float inv = lt > 0.0f ? vfac / lt : 0.0f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) f[v] *= inv;
 

@@ -37,13 +37,20 @@ struct F16 {
   }
 };
 
-// 16-bit to fp16, saturating at the fp16 finite range.
-template <typename T>
-__device__ inline _Float16 to_f16_sat(uint16_t b) {
-  float f = T::to_float(b);
-  f = fminf(fmaxf(f, -65504.0f), 65504.0f);
+// fp32 to fp16 after multiplying by sc (a power of two): finite values
+// saturate at the fp16 finite range, Inf and NaN pass through unchanged.
+__device__ inline _Float16 to_f16_scaled(float f, float sc) {
+  f *= sc;
+  f = __builtin_isfinite(f) ? fminf(fmaxf(f, -65504.0f), 65504.0f) : f;
   return static_cast<_Float16>(f);
 }
+
+// |f| for finite f, 0 for Inf / NaN (the magnitude a scale must bring into
+// fp16 range; non-finite values keep their meaning at any scale).
+__device__ inline float finite_abs(float f) { return __builtin_isfinite(f) ? fabsf(f) : 0.0f; }
+
+// Largest finite fp16 magnitude.
+constexpr float kF16Max = 65504.0f;
 
 __device__ inline u32x4 zero_u32x4() { return u32x4{0u, 0u, 0u, 0u}; }
 

@@ -229,7 +229,12 @@ __global__ __launch_bounds__(256) void score_topk_kernel(ScoreParams P) {
         const int c = cb + t + 256 * j;
         if (c < ncand)
 #pragma unroll
-          for (int r = 0; r < R; ++r) sc[r * ncand + c] = float(acc[j][r]) * P.scale;
+          for (int r = 0; r < R; ++r) {
+            // forced ids score +inf: always inside the top-k
+            const bool forced = ((P.flags & kSelectForceFirst) && c == 0) ||
+                                ((P.flags & kSelectForceDiag) && c == bq0 + r);
+            sc[r * ncand + c] = forced ? __builtin_inff() : float(acc[j][r]) * P.scale;
+          }
       }
     }
   };

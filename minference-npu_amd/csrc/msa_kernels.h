@@ -29,8 +29,15 @@ struct ScoreParams {
   int n_qb, n_kb, topk_max, batch, n_slots;
   int s_q, s_k;  // row i of the query is absolute position s_k - s_q + i
   float scale;
+  int flags;     // kSelectForceFirst | kSelectForceDiag
   int16_t slot_topk[kMaxHeads];
 };
+
+// Selector options: block 0 / the query block's own (diagonal, q-frame)
+// block always selected, inside the top-k (their scores count as +inf; ties
+// among forced ids go to the lower id).
+constexpr int kSelectForceFirst = 1;
+constexpr int kSelectForceDiag = 2;
 
 // 32-bit fields throughout: the kernel reads these with scalar loads, which
 // have no 16-bit form on gfx950.
@@ -75,6 +82,7 @@ struct AttnParams {
   const uint16_t* gkt;
   const uint16_t* gvt;
   int vs_slots, vs_cap, nv_pad;
+  const int32_t* vexp;  // [batch * kv_heads]: staged V = V * 2^-vexp (stage_kernel)
   int32_t head_order[kMaxHeads];
   HeadArg hd[kMaxHeads];
 };
@@ -135,6 +143,14 @@ struct StageParams {
   const int32_t* rows;
   const int32_t* rows_cnt;
   int rows_stride, n_slots;
+  // V range handling.  Plain mode: every V tile writes the largest finite |V|
+  // it holds to tmax[b * kv_heads + kvh][tile] (s_pad / 64 tiles); then
+  // vscale_kernel sets vexp[b * kv_heads + kvh] = e, the smallest e >= 0 with
+  // max |V| * 2^-e <= 65504, and restages the head's V times 2^-e when e > 0
+  // (exact for normal results).  Gather mode stages V times 2^-vexp of the
+  // slot's kv head.  The attention kernel multiplies its output by 2^e.
+  float* tmax;
+  int32_t* vexp;
   int16_t slot_kvh[kMaxHeads];
 };
 
@@ -184,6 +200,7 @@ hipError_t launch_score(const ScoreParams& p, int D, hipStream_t st);
 int score_rows_for(int n_kb);
 size_t score_smem_bytes(int R, int D, int n_kb);
 hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st);
+hipError_t launch_vscale(const StageParams& p, int dtype, int D, hipStream_t st);
 hipError_t launch_decode(const DecodeParams& p, int dtype, int out_dtype, int D, hipStream_t st);
 hipError_t launch_attention(const AttnParams& p, int dtype, int out_dtype, int D,
                             hipStream_t st);

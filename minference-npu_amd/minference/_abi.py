@@ -39,11 +39,15 @@ MSA_KIND_DENSE = 0
 MSA_KIND_STREAM = 1
 MSA_KIND_BLOCK = 2
 MSA_KIND_VS = 3
+MSA_KIND_FULL = 4
 MSA_VS_MAX_SEQ = 131072
+
+MSA_SELECT_FORCE_FIRST = 1
+MSA_SELECT_FORCE_DIAG = 2
 
 MSA_MAX_HEADS = 128
 MSA_BLOCK = 64
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _DTYPE_CODE = {
     torch.bfloat16: MSA_DTYPE_BF16,
@@ -57,6 +61,7 @@ EXPORTED_SYMBOLS = (
     "msa_status_str",
     "msa_estimate_workspace_bytes",
     "msa_block_estimate",
+    "msa_block_estimate_ex",
     "msa_attention_workspace_bytes",
     "msa_layer_attention",
     "msa_stage_kv",
@@ -151,6 +156,14 @@ def load_library() -> ctypes.CDLL:
             ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
             ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
             ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.msa_block_estimate_ex.restype = ctypes.c_int
+        lib.msa_block_estimate_ex.argtypes = [
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_float, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
             ctypes.c_size_t, ctypes.c_void_p,
         ]
         lib.msa_attention_workspace_bytes.restype = ctypes.c_size_t
@@ -312,8 +325,10 @@ def block_estimate(
     idx: torch.Tensor,
     cnt: torch.Tensor,
     ws: Optional[torch.Tensor] = None,
+    flags: int = 0,
 ) -> None:
-    """Launch msa_block_estimate on the current stream (no sync)."""
+    """Launch msa_block_estimate on the current stream (no sync); with
+    ``flags`` (MSA_SELECT_*) msa_block_estimate_ex."""
     lib = load_library()
     n_slots = len(slot_heads)
     if len(slot_topk) != n_slots:
@@ -324,12 +339,17 @@ def block_estimate(
     if ws is None or ws.numel() < need:
         ws = workspace(need, q.device)
     qd, kd = tensor4(q), tensor4(k)
-    st = lib.msa_block_estimate(
-        ctypes.byref(qd), ctypes.byref(kd), heads_arr, topk_arr, n_slots, MSA_BLOCK,
-        int(topk_max),
-        float(score_scale), idx.data_ptr(), cnt.data_ptr(), ws.data_ptr(), ws.numel(),
-        current_stream_handle(q.device),
-    )
+    stream = current_stream_handle(q.device)
+    if flags:
+        st = lib.msa_block_estimate_ex(
+            ctypes.byref(qd), ctypes.byref(kd), heads_arr, topk_arr, n_slots, MSA_BLOCK,
+            int(topk_max), float(score_scale), int(flags), idx.data_ptr(), cnt.data_ptr(),
+            ws.data_ptr(), ws.numel(), stream)
+    else:
+        st = lib.msa_block_estimate(
+            ctypes.byref(qd), ctypes.byref(kd), heads_arr, topk_arr, n_slots, MSA_BLOCK,
+            int(topk_max), float(score_scale), idx.data_ptr(), cnt.data_ptr(), ws.data_ptr(),
+            ws.numel(), stream)
     check(st)
 
 

@@ -27,23 +27,21 @@ def dense_attention(
     causal: bool = True,
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Dense causal attention, ``[B, H, S, D]`` in and out.
+    """Dense attention, ``[B, H, S, D]`` in and out.
 
-    Query i sees key j iff j <= i + (S_k - S_q).  ``scale`` defaults to
-    1/sqrt(D) of the unpadded head_dim (reference :210-211).  Only the causal
-    prefill form is implemented; the non-causal one-row form is
-    ``decode_dense``.
+    causal=True: query i sees key j iff j <= i + (S_k - S_q) (S_q <= S_k).
+    causal=False: every query sees every key, any S_q and S_k (reference
+    :221-230).  ``scale`` defaults to 1/sqrt(D) of the unpadded head_dim
+    (reference :210-211).
     """
-    if not causal:
-        raise NotImplementedError("dense_attention(causal=False) is not part of the MI355X prefill "
-                                  "path; use decode_dense for one query row")
     check_bnsd(q, k, v)
-    check_supported(q, k, v)
+    check_supported(q, k, v, allow_longer_q=not causal)
     q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
     result = make_out(q, out)
     s = dense_scale(q.shape[-1]) if scale is None else float(scale)
+    kind = _abi.MSA_KIND_DENSE if causal else _abi.MSA_KIND_FULL
     for h0, h1 in head_chunks(q.shape[1]):
-        heads = [(_abi.MSA_KIND_DENSE, 0, 0, -1, s)] * (h1 - h0)
+        heads = [(kind, 0, 0, -1, s)] * (h1 - h0)
         _abi.layer_attention(q[:, h0:h1], k[:, h0:h1], v[:, h0:h1], result[:, h0:h1], heads)
     return result
 

@@ -36,7 +36,15 @@ def _check_block_size(block_size: int) -> None:
         )
 
 
-def _estimate(q: torch.Tensor, k: torch.Tensor, topk: int):
+def select_flags(force_first: bool = False, force_diag: bool = False) -> int:
+    """Selector flags: block 0 / the query block's own block always kept,
+    inside the top-k (an option of this build; the reference selector has
+    none)."""
+    return ((_abi.MSA_SELECT_FORCE_FIRST if force_first else 0)
+            | (_abi.MSA_SELECT_FORCE_DIAG if force_diag else 0))
+
+
+def _estimate(q: torch.Tensor, k: torch.Tensor, topk: int, flags: int = 0):
     """Run the estimator for every head of q.
 
     Returns a list of (h0, h1, idx, cnt) per head chunk of at most
@@ -51,7 +59,8 @@ def _estimate(q: torch.Tensor, k: torch.Tensor, topk: int):
         idx = torch.empty((B, n, n_qb, topk), dtype=torch.int32, device=q.device)
         cnt = torch.empty((B, n, n_qb), dtype=torch.int32, device=q.device)
         _abi.block_estimate(
-            q[:, h0:h1], k[:, h0:h1], list(range(n)), [topk] * n, topk, scale, idx, cnt
+            q[:, h0:h1], k[:, h0:h1], list(range(n)), [topk] * n, topk, scale, idx, cnt,
+            flags=flags,
         )
         chunks.append((h0, h1, idx, cnt))
     return chunks
@@ -64,6 +73,8 @@ def select_block_sparse_topk_indices(
     block_size: int = _DEFAULT_BLOCK_SIZE,
     *,
     return_counts: bool = False,
+    force_first: bool = False,
+    force_diag: bool = False,
 ):
     """Selected K-block ids per query block, ``[B, H, n_q_blocks, topk]`` int64.
 
@@ -76,6 +87,8 @@ def select_block_sparse_topk_indices(
     With ``return_counts=True`` also returns the per-row counts of leading ids
     some row of the query block attends: min(topk, bq+1), plus, when
     S_q < S_k, the surplus ids that lie before the block's last absolute row.
+    ``force_first`` / ``force_diag`` (not in the reference) keep block 0 /
+    the query block's own block in every row, inside the top-k.
     """
     check_bnsd(q, k)
     check_supported(q, k)
@@ -83,7 +96,7 @@ def select_block_sparse_topk_indices(
     q, k = kernel_view(q), kernel_view(k)
     n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
     topk = min(max(1, int(topk_blocks)), n_kb)
-    chunks = _estimate(q, k, topk)
+    chunks = _estimate(q, k, topk, select_flags(force_first, force_diag))
     idx = torch.cat([c[2] for c in chunks], dim=1).long()
     if return_counts:
         return idx, torch.cat([c[3] for c in chunks], dim=1).long()
@@ -168,6 +181,8 @@ def block_sparse_attention(
     block_size: int = _DEFAULT_BLOCK_SIZE,
     *,
     out: Optional[torch.Tensor] = None,
+    force_first: bool = False,
+    force_diag: bool = False,
 ) -> torch.Tensor:
     """Block-sparse causal attention.
 
@@ -177,6 +192,9 @@ def block_sparse_attention(
                      number of K blocks, as in the reference).
         block_size:  must be 64.
         out:         optional output (q's dtype or float32).
+        force_first, force_diag: keep block 0 / the diagonal block in every
+                     selection (options of this build, off by default: the
+                     reference's selector is the plain top-k).
 
     Returns ``[B, H, S, D]`` in q's dtype (or ``out``).
     """
@@ -186,6 +204,6 @@ def block_sparse_attention(
     q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
     n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
     topk = min(max(1, int(topk_blocks)), n_kb)
-    chunks = _estimate(q, k, topk)
+    chunks = _estimate(q, k, topk, select_flags(force_first, force_diag))
     result = make_out(q, out)
     return _run(q, k, v, chunks, topk, result)

@@ -51,7 +51,8 @@ def check_bnsd(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor] = Non
         assert v.shape == k.shape, f"v shape {tuple(v.shape)} != k shape {tuple(k.shape)}"
 
 
-def check_supported(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor] = None) -> None:
+def check_supported(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor] = None,
+                    allow_longer_q: bool = False) -> None:
     tensors = (q, k) if v is None else (q, k, v)
     _abi.require_device(*tensors)
     for t in tensors:
@@ -66,7 +67,7 @@ def check_supported(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor] 
             f"head_dim={q.shape[-1]} is not supported by the MI355X kernels "
             f"(supported: {SUPPORTED_HEAD_DIMS})"
         )
-    if q.shape[2] > k.shape[2]:
+    if q.shape[2] > k.shape[2] and not allow_longer_q:
         raise ValueError(
             f"prefill attention requires S_q <= S_k, got S_q={q.shape[2]}, S_k={k.shape[2]}"
         )

@@ -24,7 +24,8 @@ something other than its own formula):
                         n_local >= S equals causal dense; LSE-merge identity
   block_sparse_from_indices : full top-k equals causal dense; Q = 0 closed form;
                         per-row brute force over the expanded token set
-  dense_causal        : torch scaled_dot_product_attention(is_causal=True) in fp64
+  dense_causal        : torch scaled_dot_product_attention in fp64 (is_causal
+                        True and False)
   rope_rotate_half    : HF Phi-3's apply_rotary_pos_emb on CPU torch in bf16 / fp16
                         (the call the reference makes), bit for bit, full and
                         partial rotary; in fp64 a norm-preserving rotation of
@@ -186,7 +187,8 @@ def block_scores(q_pool: np.ndarray, k_pool: np.ndarray, scale: float) -> np.nda
     return np.where(causal, s, np.float32(-np.inf)).astype(np.float32)
 
 
-def select_topk(scores: np.ndarray, topk: int):
+def select_topk(scores: np.ndarray, topk: int, force_first: bool = False,
+                force_diag: bool = False):
     """Per query block: the ``topk`` largest scores, ties -> lower block id.
 
     Returns (idx, cnt).  idx[..., bq, :cnt] are the selected causal ids
@@ -195,8 +197,19 @@ def select_topk(scores: np.ndarray, topk: int):
     -inf future ids chosen by torch.topk internals (:262-263); they are never
     attended (token causal mask, :281-284), and here they are the next
     future ids bq+1, bq+2, ... in ascending order.
+
+    force_first / force_diag (this build's selector option, not the
+    reference's): block 0 / block bq rank above every scored block (their
+    scores count as +inf), inside the top-k; between them the lower id wins.
     """
     *lead, n_bq, n_bk = scores.shape
+    if force_first or force_diag:
+        scores = np.array(scores, dtype=np.float32, copy=True)
+        if force_first:
+            scores[..., :, 0] = np.inf
+        if force_diag:
+            d = np.arange(min(n_bq, n_bk))
+            scores[..., d, d] = np.inf
     topk = min(int(topk), n_bk)
     flat = scores.reshape(-1, n_bq, n_bk)
     idx = np.empty((flat.shape[0], n_bq, topk), dtype=np.int64)
@@ -217,13 +230,15 @@ def select_topk(scores: np.ndarray, topk: int):
 
 def select_block_sparse_topk_indices(q: np.ndarray, k: np.ndarray, topk_blocks: int,
                                      dtype: str, scale: float | None = None,
-                                     block: int = BLOCK):
+                                     block: int = BLOCK, force_first: bool = False,
+                                     force_diag: bool = False):
     """Full selector on [..., S, D] inputs (block_sparse_kernel_npu.py:230-263)."""
     if scale is None:
         scale = sparse_scale(q.shape[-1])
     qp = pool_blocks(q, dtype, block)
     kp = pool_blocks(k, dtype, block)
-    return select_topk(block_scores(qp, kp, scale), max(1, int(topk_blocks)))
+    return select_topk(block_scores(qp, kp, scale), max(1, int(topk_blocks)),
+                       force_first, force_diag)
 
 
 def attend_count(idx: np.ndarray, s_q: int, s_k: int, block: int = BLOCK) -> np.ndarray:
@@ -471,8 +486,10 @@ def vertical_slash_from_indices(q, k, v, v_idx, s_idx, scale: float | None = Non
     return out
 
 
-def dense_causal(q, k, v, scale: float | None = None, acc=np.float64) -> np.ndarray:
-    """Causal dense attention j <= i + (S_k - S_q) (attention.py:166-189)."""
+def dense_causal(q, k, v, scale: float | None = None, acc=np.float64,
+                 causal: bool = True) -> np.ndarray:
+    """Dense attention (attention.py:166-189): causal j <= i + (S_k - S_q), or
+    with causal=False every key for every query (any S_q, S_k)."""
     if scale is None:
         scale = dense_scale(q.shape[-1])
     B, H, s_q, D = q.shape
@@ -480,6 +497,8 @@ def dense_causal(q, k, v, scale: float | None = None, acc=np.float64) -> np.ndar
     kvg = H // k.shape[1]
     a = np.arange(s_k - s_q, s_k)[:, None]
     vis = np.arange(s_k)[None, :] <= a
+    if not causal:
+        vis = np.ones((s_q, s_k), dtype=bool)
     out = np.zeros((B, H, s_q, D), dtype=acc)
     for b, h in _heads(q):
         out[b, h] = masked_attention(q[b, h], k[b, h // kvg], v[b, h // kvg], vis, scale, acc)

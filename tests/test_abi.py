@@ -46,10 +46,14 @@ def test_workspace_sizes():
     # estimator: pooled Q + pooled K^T in fp32
     assert _abi.estimate_workspace_bytes(1, 32, 16384, 16384, 96) == 32 * 512 * 96 * 4
     assert _abi.estimate_workspace_bytes(1, 1, 100, 100, 64) == 1024  # 2*2*64*4 rounded to 256
-    # attention: staged K and V operands (16-bit) padded to 64 keys, then
-    # 256 bytes of work-queue counters
-    assert _abi.attention_workspace_bytes(1, 32, 65536, 96) == 2 * 32 * 96 * 65536 * 2 + 256
-    assert _abi.attention_workspace_bytes(1, 1, 65, 64) == 2 * 64 * 128 * 2 + 256
+    # attention: staged K and V operands (16-bit) padded to 64 keys, the V
+    # maxima per 64-key tile (fp32) and the V exponent per kv head (int32),
+    # each rounded up to 256 bytes, then 256 bytes of work-queue counters
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    staged = 2 * 32 * 96 * 65536 * 2
+    assert _abi.attention_workspace_bytes(1, 32, 65536, 96) == \
+        up(up(staged + 32 * 1024 * 4) + 32 * 4) + 256
+    assert _abi.attention_workspace_bytes(1, 1, 65, 64) == up(up(2 * 64 * 128 * 2 + 2 * 4) + 4) + 256
     assert _abi.attention_workspace_bytes(0, 1, 65, 64) == 0
 
 
@@ -123,6 +127,28 @@ def test_attention_validation(mutate, expected):
          "ws": FAKE, "wsb": 1 << 40}
     mutate(a)
     assert attn(a["q"], a["k"], a["v"], a["o"], a["hd"], a["n"], ws=a["ws"], wsb=a["wsb"]) == expected
+
+
+def test_attention_full_kind_allows_longer_queries():
+    """S_q > S_k is refused for causal kinds and accepted for MSA_KIND_FULL
+    heads (the call then fails later, on the deliberately small workspace)."""
+    q, kv = t4([1, 4, 512, 96]), t4([1, 4, 256, 96])
+    assert attn(q, kv, kv, q, heads(4), 4, wsb=100) == _abi.MSA_E_SEQ
+    assert attn(q, kv, kv, q, heads(4, kind=_abi.MSA_KIND_DENSE), 4, wsb=100) == _abi.MSA_E_SEQ
+    assert attn(q, kv, kv, q, heads(4, kind=_abi.MSA_KIND_FULL), 4, wsb=100) == _abi.MSA_E_WORKSPACE
+    mixed = heads(4, kind=_abi.MSA_KIND_FULL)
+    mixed[2].kind = _abi.MSA_KIND_STREAM
+    assert attn(q, kv, kv, q, mixed, 4, wsb=100) == _abi.MSA_E_SEQ
+
+
+def test_estimate_ex_flags_validated():
+    lib = _abi.load_library()
+    q = t4(SHAPE)
+    ha = (ctypes.c_int32 * 1)(0)
+    for flags, want in [(4, _abi.MSA_E_TOPK), (-1, _abi.MSA_E_TOPK), (3, _abi.MSA_E_WORKSPACE)]:
+        st = lib.msa_block_estimate_ex(ctypes.byref(q), ctypes.byref(q), ha, None, 1, 64, 2,
+                                       0.088, flags, FAKE, FAKE, FAKE, 100, None)
+        assert st == want, flags
 
 
 def test_attention_block_slot_range():

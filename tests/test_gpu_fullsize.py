@@ -88,6 +88,50 @@ def test_cfg2_block_ids_bit_exact_and_rows(gpu_device):
         assert err < TOL, (h, err)
 
 
+def test_cfg2_as_worded_forced_first_and_diagonal(gpu_device):
+    """BASELINE config 2 as its text states it: top-100 of the 64-blocks with
+    the diagonal and the first block always included (the selector option
+    FORCE_FIRST | FORCE_DIAG, inside the top-k).  All 32 heads x 256 query
+    blocks bit-exact with the oracle; then block_sparse_attention with the
+    option against the oracle on sampled rows."""
+    from minference import block_sparse_attention
+    from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
+
+    H, S, D, topk = 32, 16384, 96, 100
+    q, k, v = device_qkv(gpu_device, H, S, D, seed=2)
+    print(f"[cfg2 forced] estimator H={H} S={S} topk={topk}", flush=True)
+    idx, cnt = select_block_sparse_topk_indices(q, k, topk, return_counts=True,
+                                                force_first=True, force_diag=True)
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    ridx, rcnt = O.select_block_sparse_topk_indices(qn, kn, topk, "bf16", force_first=True,
+                                                    force_diag=True)
+    gi = idx.cpu().numpy()
+    assert np.array_equal(cnt.cpu().numpy(), rcnt)
+    assert np.array_equal(gi, ridx), f"{(gi != ridx).sum()} block ids differ"
+    for bq in range(S // 64):
+        row = gi[:, :, bq, :rcnt[0, 0, bq]]
+        assert (row == 0).any(-1).all() and (row == bq).any(-1).all()
+    # the option changes selections where the plain top-k left block 0 or bq out
+    plain, _ = O.select_block_sparse_topk_indices(qn, kn, topk, "bf16")
+    print(f"[cfg2 forced] rows changed by the option: "
+          f"{int((plain != ridx).any(-1).sum())} of {H * (S // 64)}", flush=True)
+
+    out = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    block_sparse_attention(q, k, v, topk, out=out, force_first=True, force_diag=True)
+    og = out.cpu().numpy()
+    scale = O.sparse_scale(D)
+    rows = rows_for(S, extra=(64 * 99, 64 * 100 + 5, 64 * 200 + 17))
+    for h in range(1, H, 6):
+        def vis(r, h=h):
+            bq = r // 64
+            ids = ridx[0, h, bq, :rcnt[0, h, bq]]
+            js = np.concatenate([np.arange(64 * b, 64 * b + 64) for b in ids])
+            return js[js <= r]
+        ref = oracle_rows(qn[0, h], kn[0, h], vn[0, h], rows, vis, scale)
+        err = np.abs(og[0, h, rows] - ref).max()
+        assert err < TOL, (h, err)
+
+
 def test_cfg1_rope_then_stream_all_rows(gpu_device):
     from minference import streaming_forward
     from minference.ops.rope import apply_rotary_pos_emb

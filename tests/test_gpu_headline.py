@@ -1,0 +1,116 @@
+"""Parity of the exact launch the benchmark times (its default workload).
+
+bench.py's headline step: S = 65536, 32 heads x 96, bf16, 16 stream_llm(128,
+4096) + 16 block_sparse(top-100) heads assigned by the seed-0 shuffle, Q/K/V
+from the bench's own generator (RoPE, K rows 0-3 x8), estimator + K/V staging
++ one staged attention launch with the plan's kind-interleaved, cost-balanced
+item order.  Checked here:
+  * block ids of all 16 block heads bit-exact with the oracle;
+  * sampled rows of every head (tile boundaries, the sink edge, the band
+    start, the last rows) within 2e-3 of the oracle, in fp32 output and in
+    the bf16 output the bench writes (plus one bf16 rounding);
+  * every row of every head through a constant-V launch (the output of a
+    softmax-weighted mean of a constant is that constant).
+Reference semantics: minference/ops/streaming_kernel_npu.py:94-146,
+minference/ops/block_sparse_kernel_npu.py:230-263, 325-348."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+S, H, D = 65536, 32, 96
+
+
+def _rows(n_init, n_local):
+    base = {0, 1, 63, 64, 65, 127, 128, 129, 191, 192, n_init - 1, n_init, n_local - 1, n_local,
+            n_local + 1, n_local + n_init - 1, n_local + n_init, n_local + 63, n_local + 64,
+            8191, 8192, S // 2 - 1, S // 2, S - 65, S - 64, S - 63, S - 2, S - 1}
+    return sorted(r for r in base if 0 <= r < S)
+
+
+def test_headline_launch_matches_oracle(gpu_device):
+    import bench
+    from minference import _abi
+    from minference.modules.minference_forward import build_layer_plan
+    from minference.ops.common import sparse_scale
+
+    print("[headline] building the bench's layer", flush=True)
+    pats, counts = bench.layer_patterns("headline", H, seed=0)
+    assert counts == (16, 16, 0)
+    plan = build_layer_plan(pats, H, D, S)
+    q, k, v = bench.make_inputs(S, H, D, 0, gpu_device)
+    n_qb = math.ceil(S / 64)
+    n_slots = len(plan.block_heads)
+    idx = torch.empty((1, n_slots, n_qb, plan.topk_max), dtype=torch.int32, device=gpu_device)
+    cnt = torch.empty((1, n_slots, n_qb), dtype=torch.int32, device=gpu_device)
+    ws = _abi.workspace(_abi.attention_workspace_bytes(1, H, S, D), gpu_device)
+    _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max, sparse_scale(D),
+                        idx, cnt)
+    _abi.stage_kv(k, v, ws)
+    out16 = torch.empty_like(q)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    for out in (out16, out32):
+        _abi.layer_attention(q, k, v, out, plan.heads, idx=idx, cnt=cnt, idx_slots=n_slots,
+                             topk_max=plan.topk_max, ws=ws, staged=True)
+    torch.cuda.synchronize()
+
+    print("[headline] oracle block ids", flush=True)
+    qn = q.float().cpu().numpy()[0]
+    kn = k.float().cpu().numpy()[0]
+    vn = v.float().cpu().numpy()[0]
+    bh = list(plan.block_heads)
+    ridx, rcnt = O.select_block_sparse_topk_indices(qn[bh], kn[bh], 100, "bf16", sparse_scale(D))
+    got_idx = idx.cpu().numpy()[0]
+    assert np.array_equal(cnt.cpu().numpy()[0], rcnt)
+    assert np.array_equal(got_idx, ridx), f"{(got_idx != ridx).sum()} block ids differ"
+
+    print("[headline] sampled rows of every head", flush=True)
+    o32 = out32.cpu().numpy()[0]
+    o16 = out16.float().cpu().numpy()[0]
+    sc = sparse_scale(D)
+    worst = 0.0
+    for h in range(H):
+        kind, p1, p2, slot, _ = plan.heads[h]
+        if kind == _abi.MSA_KIND_STREAM:
+            rows = _rows(p1, p2)
+
+            def vis(r, n_init=p1, n_local=p2):
+                j = np.arange(r + 1)
+                return j[(j > r - n_local) | (j < n_init)]
+        else:
+            assert kind == _abi.MSA_KIND_BLOCK
+            rows = _rows(128, 4096)
+
+            def vis(r, s=slot):
+                bq = r // 64
+                ids = ridx[s, bq, :rcnt[s, bq]]
+                j = (ids[:, None] * 64 + np.arange(64)[None, :]).ravel()
+                return j[j <= r]
+        for r in rows:
+            js = vis(r)
+            lg = kn[h, js].astype(np.float64) @ qn[h, r].astype(np.float64) * sc
+            p = np.exp(lg - lg.max())
+            ref = (p / p.sum()) @ vn[h, js].astype(np.float64)
+            err = np.abs(o32[h, r] - ref).max()
+            worst = max(worst, err)
+            assert err < TOL, (h, kind, r, err)
+            assert (np.abs(o16[h, r] - ref) <= TOL + np.abs(ref) * 2.0 ** -8).all(), (h, r)
+    print(f"[headline] worst sampled error {worst:.3e}", flush=True)
+
+    print("[headline] constant V, every row", flush=True)
+    c = (torch.arange(H, device=gpu_device, dtype=torch.float32) * 0.25 + 0.5)
+    vc = c.view(1, H, 1, 1).expand(1, H, S, D).to(torch.bfloat16).contiguous()
+    _abi.stage_kv(k, vc, ws)
+    _abi.layer_attention(q, k, vc, out32, plan.heads, idx=idx, cnt=cnt, idx_slots=n_slots,
+                         topk_max=plan.topk_max, ws=ws, staged=True)
+    dev = (out32 - c.view(1, H, 1, 1)).abs().amax(dim=(0, 2, 3)) / c
+    assert float(dev.max()) < 1e-3, dev.cpu().tolist()

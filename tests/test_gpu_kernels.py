@@ -205,6 +205,65 @@ def test_dense_vs_oracle(gpu_device, s_q, s_k, D, dtype):
     assert_close_f32(out32, ref, what="dense")
 
 
+@pytest.mark.parametrize("s_q,s_k,D,dtype", [(256, 256, 96, torch.bfloat16),
+                                              (100, 700, 96, torch.bfloat16),
+                                              (700, 100, 64, torch.float16),
+                                              (1000, 1000, 128, torch.bfloat16),
+                                              (65, 3000, 96, torch.bfloat16)])
+def test_dense_noncausal_vs_oracle(gpu_device, s_q, s_k, D, dtype):
+    """dense_attention(causal=False) (reference backend_npu/attention.py:221-230):
+    every key visible to every query, S_q > S_k included."""
+    from minference import dense_attention
+
+    print(f"[dense non-causal] {s_q} {s_k} {D} {dtype}", flush=True)
+    q, k, v = make_qkv(1, 3, s_q, s_k, D, dtype, seed=s_q + s_k, use_rope=False)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    dense_attention(dq, dk, dv, causal=False, out=out32)
+    ref = O.dense_causal(np32(q), np32(k), np32(v), causal=False)
+    assert_close_f32(out32, ref, what="dense non-causal")
+    out = dense_attention(dq, dk, dv, causal=False)
+    assert out.dtype == dtype
+    assert_close_lowp(out, ref, what="dense non-causal lowp")
+
+
+FORCED_CASES = [
+    # (S, D, topk, dtype, force_first, force_diag)
+    (4096 + 17, 96, 16, torch.bfloat16, True, True),
+    (4096, 96, 100, torch.bfloat16, True, True),
+    (2048, 128, 7, torch.float16, False, True),
+    (3000, 64, 4, torch.bfloat16, True, False),
+    (1024, 96, 1, torch.bfloat16, True, True),
+    (1024, 96, 2, torch.bfloat16, False, True),
+]
+
+
+@pytest.mark.parametrize("case", FORCED_CASES, ids=[str(c) for c in FORCED_CASES])
+def test_estimator_forced_bit_exact(gpu_device, case):
+    """The selector option that always keeps block 0 and/or the diagonal
+    block (inside the top-k): ids bit-exact with the oracle."""
+    from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
+
+    S, D, topk, dtype, first, diag = case
+    q, k, _ = make_qkv(1, 4, S, S, D, dtype, seed=S + topk, sink_scale=8.0)
+    idx, cnt = select_block_sparse_topk_indices(*to_dev(gpu_device, q, k), topk,
+                                                return_counts=True, force_first=first,
+                                                force_diag=diag)
+    ridx, rcnt = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, dtype_tag(dtype),
+                                                    force_first=first, force_diag=diag)
+    got = idx.cpu().numpy()
+    assert np.array_equal(cnt.cpu().numpy(), rcnt)
+    assert np.array_equal(got, ridx), f"{(got != ridx).sum()} ids differ"
+    nb = ridx.shape[-2]
+    for bq in range(nb):
+        c = rcnt[0, 0, bq]
+        row = set(got[0, 0, bq, :c].tolist())
+        if first:
+            assert 0 in row
+        if diag and not (first and c == 1 and bq > 0):
+            assert bq in row
+
+
 @pytest.mark.parametrize("factor", [4.0, 12.0, 40.0])
 @pytest.mark.parametrize("kind", ["dense", "stream", "block"])
 def test_late_outlier_keys(gpu_device, kind, factor):

@@ -142,6 +142,64 @@ def test_selector_known_answer_ties_to_lower_id():
         assert list(idx[0, 0, bq, c:]) == list(range(bq + 1, bq + 1 + 3 - c))
 
 
+def test_selector_forced_known_answer():
+    """Decreasing pooled scores (K block b = (12 - b) * e0, Q = e0): the plain
+    top-k of row bq is its first k causal blocks; with the diagonal forced the
+    row keeps bq and the first k-1; with block 0 forced nothing changes (it is
+    already first); top-1 with both flags keeps block 0 (lower id)."""
+    S, D = 64 * 12, 64
+    k = torch.zeros(1, 1, S, D)
+    for b in range(12):
+        k[0, 0, 64 * b:64 * b + 64, 0] = float(12 - b)
+    q = torch.zeros(1, 1, S, D)
+    q[..., 0] = 1.0
+    qn, kn = q.numpy(), k.numpy()
+    plain, _ = O.select_block_sparse_topk_indices(qn, kn, 4, "bf16")
+    diag, cd = O.select_block_sparse_topk_indices(qn, kn, 4, "bf16", force_diag=True)
+    first, _ = O.select_block_sparse_topk_indices(qn, kn, 4, "bf16", force_first=True)
+    both1, _ = O.select_block_sparse_topk_indices(qn, kn, 1, "bf16", force_first=True,
+                                                  force_diag=True)
+    for bq in range(12):
+        c = min(4, bq + 1)
+        assert list(plain[0, 0, bq, :c]) == list(range(c))
+        assert list(first[0, 0, bq, :c]) == list(range(c))
+        want = list(range(c)) if bq < 4 else [0, 1, 2, bq]
+        assert list(diag[0, 0, bq, :c]) == want and cd[0, 0, bq] == c
+        assert list(both1[0, 0, bq, :1]) == [0]
+
+
+@pytest.mark.parametrize("first,diag,topk", [(True, True, 5), (False, True, 3), (True, False, 1),
+                                             (True, True, 2)])
+def test_selector_forced_bruteforce(first, diag, topk):
+    """Forced selection = the forced ids plus the brute-force top-(k - |forced|)
+    of the other causal blocks (ties -> lower id), written without the +inf
+    device the oracle uses."""
+    S = 64 * 9 + 17
+    q, k, _ = make_qkv(B=1, H=2, S_q=S, D=32, dtype=torch.bfloat16, seed=41)
+    scale = O.sparse_scale(32)
+    idx, cnt = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, "bf16", scale,
+                                                  force_first=first, force_diag=diag)
+    nb = -(-S // 64)
+    for h in range(2):
+        qp = O.pool_blocks(np32(q)[0, h], "bf16").astype(np.float64)
+        kp = O.pool_blocks(np32(k)[0, h], "bf16").astype(np.float64)
+        for bq in range(nb):
+            forced = []
+            if first:
+                forced.append(0)
+            if diag and bq not in forced:
+                forced.append(bq)
+            kk = min(topk, bq + 1)
+            forced = sorted(forced)[:kk]
+            rest = [b for b in range(bq + 1) if b not in forced]
+            sc = {b: float(np.float32(np.float32(math.fsum(qp[bq] * kp[b])) * np.float32(scale)))
+                  for b in rest}
+            rest.sort(key=lambda b: (-sc[b], b))
+            want = sorted(forced + rest[:kk - len(forced)])
+            assert cnt[0, h, bq] == kk
+            assert list(idx[0, h, bq, :kk]) == want, (h, bq)
+
+
 @pytest.mark.parametrize("topk,S", [(1, 256), (2, 256), (4, 512), (100, 256)])
 def test_selector_invariants(topk, S):
     """Reference tests/test_block_sparse_kernel.py:186-211: sorted, clamped,
@@ -363,6 +421,17 @@ def test_block_q0_closed_form_and_bruteforce():
         ref = (p / p.sum()) @ vn[js]
         assert np.abs(out[i] - ref).max() < 1e-12
     assert nb == 7
+
+
+@pytest.mark.parametrize("s_q,s_k", [(256, 256), (100, 300), (300, 100)])
+def test_dense_noncausal_vs_torch_sdpa(s_q, s_k):
+    """causal=False (attention.py:181-186, :221-230): every key for every
+    query, S_q > S_k included."""
+    q, k, v = make_qkv(B=1, H=2, S_q=s_q, S_k=s_k, D=64, dtype=torch.float32, seed=3,
+                       use_rope=False)
+    out = O.dense_causal(np32(q), np32(k), np32(v), causal=False)
+    ref = F.scaled_dot_product_attention(q.double(), k.double(), v.double(), scale=64 ** -0.5)
+    assert np.abs(out - ref.numpy()).max() < 1e-12
 
 
 @pytest.mark.parametrize("s_q,s_k", [(256, 256), (100, 300)])
