@@ -25,10 +25,13 @@
 //   v_mfma_f32_32x32x16_f16.  K and V are staged once per layer in exact
 //   operand order (V as fp16), so every operand is one contiguous 1 KB load.
 //   The exponentials are taken with each row's running max straight off
-//   QK; only when some P exceeds 2^8 (the row max grew by more than 8 in
-//   log2 units) does a rare path recompute the half's scores, reduce the row
-//   maxima over the four lanes of each row with permlane swaps and rescale
-//   O.  Row sums accumulate per lane and reduce once at the end.
+//   QK, biased so that a row's maximum has P = 2^7 (P, O and the row sums
+//   all carry that factor, which cancels; it keeps small P out of fp16's
+//   subnormal range); only when some P exceeds 2^15 (the row max grew by
+//   more than 8 in log2 units) does a rare path recompute the half's scores,
+//   reduce the row maxima over the four lanes of each row with permlane
+//   swaps and rescale O.  Row sums accumulate per lane and reduce once at
+//   the end.
 //   Tiles that need no mask run first; boundary tiles (diagonal, band start,
 //   partial sink, S_k end) run last with the elementwise mask.
 
@@ -46,6 +49,14 @@ constexpr int KIND_STREAM = 1;
 constexpr int KIND_BLOCK = 2;
 constexpr int KIND_VS = 3;
 constexpr int KIND_FULL = 4;  // dense without the causal mask
+
+// P = 2^(s*c - m) with m = (row max)*c - kPBias: a row's largest P is 2^7,
+// and the rescale triggers above 2^kPSlackBits times that (2^15 < 65504, so
+// every P handed to the fp16 PV product is finite).  The bias moves the
+// fp16 subnormal range of P 7 bits further from the row maximum: a P of
+// 2^-21 of the maximum still rounds with fp16's full relative precision.
+constexpr float kPBias = 7.0f;
+constexpr float kPCheck = 32768.0f;  // 2^(kPBias + 8)
 
 // ---------------------------------------------------------------------------
 // Per-layer staging of K and V into MFMA operand order, zero padded to
@@ -544,9 +555,9 @@ void attn_kernel(AttnParams P) {
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[db][rb][i] = 0.0f;
-  // Running max per row in scaled log2 units, group layout (each group's
-  // value in all 4 lane rows).  It only moves when some P would exceed 2^8,
-  // so the O rescale is rare.
+  // Running (biased) max per row in scaled log2 units, group layout (each
+  // group's value in all 4 lane rows).  It only moves when some P would
+  // exceed 2^15, so the O rescale is rare.
   float m_g[4] = {-1e30f, -1e30f, -1e30f, -1e30f};
   float l_g[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // per-lane partial row sums, group layout
   const float c_log2 = hd.scale_log2;
@@ -609,7 +620,7 @@ void attn_kernel(AttnParams P) {
   };
   // P = 2^(s*c - m) in place, with the current running max, and ps[gg] =
   // the lane's sum of its four P of group gg (its share of the row sum).
-  // Returns true when some sum exceeds 2^8; every P is at most its sum
+  // Returns true when some sum exceeds 2^15; every P is at most its sum
   // (P >= 0), so otherwise no P is large enough to need a rescale.
   auto exp_half = [&](f32x4 (&s)[2], int hf, float (&ps)[2]) INLINE -> bool {
 #pragma unroll
@@ -619,7 +630,7 @@ void attn_kernel(AttnParams P) {
         s[gg][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[gg][i], c_log2, -m_g[2 * hf + gg]));
       ps[gg] = (s[gg][0] + s[gg][1]) + (s[gg][2] + s[gg][3]);
     }
-    return __ballot(fmaxf(ps[0], ps[1]) > 256.0f) != 0;
+    return __ballot(fmaxf(ps[0], ps[1]) > kPCheck) != 0;
   };
   // Rare path: recompute the half's scores, raise the running max to the
   // row max, rescale the half's O and row sums, and redo the exponentials.
@@ -634,8 +645,8 @@ void attn_kernel(AttnParams P) {
     swap16(a, bb);
     float g0 = fmaxf(a, bb), g1 = g0;  // [group 2h, 2h, 2h+1, 2h+1] by lane row
     swap32(g0, g1);                    // g0: group 2h in every lane row, g1: group 2h+1
-    const float n0 = fmaxf(m_g[2 * hf], g0 * c_log2);
-    const float n1 = fmaxf(m_g[2 * hf + 1], g1 * c_log2);
+    const float n0 = fmaxf(m_g[2 * hf], g0 * c_log2 - kPBias);
+    const float n1 = fmaxf(m_g[2 * hf + 1], g1 * c_log2 - kPBias);
     const float al0 = __builtin_amdgcn_exp2f(m_g[2 * hf] - n0);
     const float al1 = __builtin_amdgcn_exp2f(m_g[2 * hf + 1] - n1);
     m_g[2 * hf] = n0;
