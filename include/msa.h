@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MSA_ABI_VERSION 6
+#define MSA_ABI_VERSION 7
 
 /* status codes (negative: validation, nothing launched) */
 #define MSA_OK 0
@@ -44,6 +44,7 @@ extern "C" {
 #define MSA_E_WORKSPACE (-9)   /* workspace missing or too small */
 #define MSA_E_SEQ (-10)        /* S_q > S_k (causal kinds), S_q == 0, or too long */
 #define MSA_E_SLOTS (-11)      /* sparse head without an index slot, or bad index lists */
+#define MSA_E_SCRATCH (-12)    /* more than the fixed scratch of a no-allocation entry point */
 
 /* element types */
 #define MSA_DTYPE_BF16 1
@@ -278,6 +279,22 @@ size_t msa_decode_workspace_bytes(int64_t batch, int64_t heads, int64_t s_k, int
 int msa_decode_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
                          const msa_tensor4* o, float scale, void* workspace,
                          size_t workspace_bytes, msa_stream_t stream);
+
+/* msa_decode_attention without a workspace argument: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * split-K partials go to a fixed per-GPU device array of
+ * MSA_DECODE_SCRATCH_BYTES inside the library (held by each GPU it runs on
+ * until the process ends); the call allocates nothing.  A call whose partials
+ * would not fit (msa_decode_workspace_bytes > MSA_DECODE_SCRATCH_BYTES; at
+ * D = 128 that is B * H above about 7800) returns MSA_E_SCRATCH.  Every call
+ * on one GPU shares that array: calls that overlap on one GPU (different
+ * streams, or host threads without ordering) race.  Same arguments, checks
+ * and results as msa_decode_attention. */
+#define MSA_DECODE_SCRATCH_BYTES (4u << 20)
+int msa_decode_attention_noalloc(const msa_tensor4* q, const msa_tensor4* k,
+                                 const msa_tensor4* v, const msa_tensor4* o, float scale,
+                                 msa_stream_t stream);
 
 /* Rotary position embedding of one layer's query and key heads, one launch.
  * Replaces the apply_rotary_pos_emb call of the patched forward

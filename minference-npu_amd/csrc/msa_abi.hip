@@ -4,6 +4,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string.h>
 
 #include "../../include/msa.h"
@@ -79,6 +80,7 @@ const char* msa_status_str(int status) {
     case MSA_E_WORKSPACE: return "workspace missing or too small";
     case MSA_E_SEQ: return "sequence lengths must satisfy 0 < S_q <= S_k <= 2^20 (S_q > S_k only for full heads)";
     case MSA_E_SLOTS: return "sparse head without a valid index slot, or bad idx/cnt or vertical_and_slash lists";
+    case MSA_E_SCRATCH: return "the call needs more than the fixed scratch of a no-allocation entry point (MSA_DECODE_SCRATCH_BYTES)";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
@@ -763,6 +765,57 @@ int msa_decode_attention(const msa_tensor4* q, const msa_tensor4* k, const msa_t
   dp.ml = dp.part + B * H * dp.n_split * D;
   const hipError_t e = launch_decode(dp, q->dtype, o->dtype, D, reinterpret_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSA_OK : int(e);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// decode without allocation
+// ---------------------------------------------------------------------------
+// The split-K partials of msa_decode_attention_noalloc live in this array
+// (each GPU holds its own copy until the process ends).  Host code must not
+// pass `scratch` itself to a kernel: that name is a host-side stand-in.  Its
+// device address is looked up once per device and kept in g_scratch.
+static __device__ __align__(256) unsigned char scratch[MSA_DECODE_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// Device address of the current device's scratch; MSA_OK or a status.
+int current_scratch(void** out) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return int(e);
+  if (dev < 0 || dev >= kMaxDevices) return int(hipErrorInvalidDevice);
+  std::call_once(g_scratch_once[dev], [dev] {
+    g_scratch_err[dev] = hipGetSymbolAddress(&g_scratch[dev], HIP_SYMBOL(scratch));
+  });
+  if (g_scratch_err[dev] != hipSuccess) return int(g_scratch_err[dev]);
+  *out = g_scratch[dev];
+  return MSA_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int msa_decode_attention_noalloc(const msa_tensor4* q, const msa_tensor4* k,
+                                 const msa_tensor4* v, const msa_tensor4* o, float scale,
+                                 msa_stream_t stream) {
+  // the same partials as msa_decode_attention; refuse what does not fit
+  // before touching the device
+  if (q && k && q->size[0] > 0 && q->size[1] > 0 && k->size[2] > 0 && q->size[3] > 0 &&
+      q->size[3] <= 1024) {
+    const size_t need = msa_decode_workspace_bytes(q->size[0], q->size[1], k->size[2],
+                                                   int32_t(q->size[3]));
+    if (need > size_t(MSA_DECODE_SCRATCH_BYTES)) return MSA_E_SCRATCH;
+  }
+  void* ws = nullptr;
+  const int st = current_scratch(&ws);
+  if (st != MSA_OK) return st;
+  return msa_decode_attention(q, k, v, o, scale, ws, MSA_DECODE_SCRATCH_BYTES, stream);
 }
 
 int msa_rope_qk(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* cos,

@@ -30,6 +30,8 @@ MSA_E_HEADS = -8
 MSA_E_WORKSPACE = -9
 MSA_E_SEQ = -10
 MSA_E_SLOTS = -11
+MSA_E_SCRATCH = -12
+MSA_DECODE_SCRATCH_BYTES = 4 << 20
 
 MSA_DTYPE_BF16 = 1
 MSA_DTYPE_FP16 = 2
@@ -47,7 +49,7 @@ MSA_SELECT_FORCE_DIAG = 2
 
 MSA_MAX_HEADS = 128
 MSA_BLOCK = 64
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _DTYPE_CODE = {
     torch.bfloat16: MSA_DTYPE_BF16,
@@ -68,6 +70,7 @@ EXPORTED_SYMBOLS = (
     "msa_layer_attention_staged",
     "msa_decode_workspace_bytes",
     "msa_decode_attention",
+    "msa_decode_attention_noalloc",
     "msa_vs_workspace_bytes",
     "msa_layer_attention_ex",
     "msa_vs_estimate_workspace_bytes",
@@ -195,6 +198,12 @@ def load_library() -> ctypes.CDLL:
             ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
             ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
+        lib.msa_decode_attention_noalloc.restype = ctypes.c_int
+        lib.msa_decode_attention_noalloc.argtypes = [
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.c_float, ctypes.c_void_p,
+        ]
         lib.msa_vs_estimate_workspace_bytes.restype = ctypes.c_size_t
         lib.msa_vs_estimate_workspace_bytes.argtypes = [
             ctypes.c_int64, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
@@ -298,6 +307,17 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: tor
     check(load_library().msa_decode_attention(
         ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ctypes.byref(od), float(scale),
         ws.data_ptr(), ws.numel(), current_stream_handle(q.device)))
+
+
+def decode_attention_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                             out: torch.Tensor, scale: float) -> None:
+    """Launch msa_decode_attention_noalloc on the current stream: the same
+    decode as decode_attention with the partials in the library's fixed
+    per-GPU scratch (no workspace, nothing allocated)."""
+    qd, kd, vd, od = tensor4(q), tensor4(k), tensor4(v), tensor4(out)
+    check(load_library().msa_decode_attention_noalloc(
+        ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ctypes.byref(od), float(scale),
+        current_stream_handle(q.device)))
 
 
 def rope_qk(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,

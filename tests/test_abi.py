@@ -36,10 +36,23 @@ def test_library_exports_every_header_symbol():
 def test_abi_version_and_status_strings():
     lib = _abi.load_library()
     assert lib.msa_abi_version() == _abi.ABI_VERSION
-    for code in range(-11, 1):
+    for code in range(-12, 1):
         s = _abi.status_str(code)
         assert s and s != "unknown status"
     assert _abi.status_str(-99) == "unknown status"
+
+
+def test_decode_noalloc_refuses_oversize_before_any_device_call():
+    """The no-allocation decode rejects partials larger than its fixed
+    scratch (fake pointers: nothing is dereferenced or launched)."""
+    lib = _abi.load_library()
+    bh = 20000  # one split per head: 20000 * 130 * 4 bytes > 4 MiB at D = 128
+    assert _abi.decode_workspace_bytes(1, bh, 4096, 128) > _abi.MSA_DECODE_SCRATCH_BYTES
+    q, kv = t4([1, bh, 1, 128]), t4([1, bh, 4096, 128])
+    st = lib.msa_decode_attention_noalloc(ctypes.byref(q), ctypes.byref(kv), ctypes.byref(kv),
+                                          ctypes.byref(q), 0.088, None)
+    assert st == _abi.MSA_E_SCRATCH
+    assert "scratch" in _abi.status_str(st)
 
 
 def test_workspace_sizes():
