@@ -15,9 +15,9 @@ RoPE theta 1e4 on Q and K, K rows 0-3 scaled 8x (attention sinks).
 Printed JSON line: value = algorithmic TFLOP/s of the whole step; roofline =
 the attention kernel alone (HIP events on the launch stream) against the
 bf16 MFMA peak; dense = same-GPU dense attention on the same tensors
-(PyTorch SDPA flash and this build's dense kind); cpu_baseline = the oracle's
-stream_llm restatement of the reference CPU path timed on
-the host cores; decode = one decode step against the layer's K/V cache;
+(PyTorch SDPA flash and this build's dense kind); cpu_baseline = the
+reference's CPU path (its torch ops, restated in oracle/cpu_reference.py) for
+BASELINE configs 1 (stream_llm) and 2 (block_sparse) timed on the host cores; decode = one decode step against the layer's K/V cache;
 rope = the fused RoPE kernel on the layer's q and k against HF's eager one.
 """
 
@@ -94,8 +94,8 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
     ap.add_argument("--no-rope", action="store_true", help="skip the RoPE measurement")
-    ap.add_argument("--cpu-heads", type=int, default=16,
-                    help="heads of BASELINE config 1 timed on the CPU (scaled to 32)")
+    ap.add_argument("--cpu-block-heads", type=int, default=2,
+                    help="heads of BASELINE config 2 timed on the CPU per repeat (scaled to 32)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 launches) to calibrate the "
                          "FETCH_SIZE / WRITE_SIZE counters, then exit")
@@ -171,59 +171,104 @@ def profiled_traffic(workload):
     return None
 
 
-def cpu_model():
+def cpu_info():
+    """CPU model, physical cores of the host, CPUs this process may run on,
+    and the threads torch uses."""
+    import torch
+
+    model, cores = platform.processor() or "unknown", set()
+    phys = core = None
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    return ln.split(":", 1)[1].strip()
+                key, _, val = ln.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name":
+                    model = val
+                elif key == "physical id":
+                    phys = val
+                elif key == "core id":
+                    core = val
+                elif not key and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
     except OSError:
         pass
-    return platform.processor() or "unknown"
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"cpu_model": model, "physical_cores": len(cores) or None,
+            "logical_cpus": os.cpu_count(), "usable_cpus": usable,
+            "threads": torch.get_num_threads()}
 
 
-def cpu_baseline(n_heads_sample):
-    """BASELINE config 1 on the host: stream_llm, B=1, 32 heads, S=4096,
-    D=96, fp32, n_init=64, n_local=1024, through the oracle's restatement of
-    the reference CPU path (streaming_kernel_npu.py:94-146, same chunking).
-    Warmup 1 head, then 3 timed repeats over ``n_heads_sample`` heads, scaled
-    to 32 heads."""
-    import numpy as np
+def _time_cpu(fn, repeats=3):
+    fn()  # warmup 1
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return times
+
+
+def cpu_baseline(block_heads_sample):
+    """The reference's CPU path timed on the host (warmup 1, 3 repeats, as
+    benchmarks/probe_block_sparse_heads.py:18-31), through the torch-CPU fp32
+    restatement in oracle/cpu_reference.py (the reference's own ops at its
+    padded D = 128):
+      stream_llm, B=1, 32 heads, S=4096, D=96, fp32,
+        n_init 64, n_local 1024, all 32 heads per repeat;
+      block_sparse top-100 at S=16384, bf16 inputs, one
+        head at a time (the as-written [1,32,S,S] fp32 logits are 34 GB);
+        ``block_heads_sample`` heads per repeat, scaled to 32 heads.
+    value / unit are config 1's algorithmic TFLOP/s."""
     import torch
 
-    import oracle as O
-    from msa_data import make_qkv, np32
+    from msa_data import make_qkv
+    from oracle import cpu_reference as R
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    info = cpu_info()
     S, D, n_init, n_local = 4096, 96, 64, 1024
-    q, k, v = make_qkv(1, n_heads_sample, S, S, D, torch.float32, seed=0)
-    q, k, v = np32(q), np32(k), np32(v)
-    O.streaming_attention(q[:, :1], k[:, :1], v[:, :1], n_init, n_local, acc=np.float32)
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        O.streaming_attention(q, k, v, n_init, n_local, acc=np.float32)
-        times.append(time.perf_counter() - t0)
-    per_layer = (sum(times) / len(times)) * 32 / n_heads_sample
-    flops = 32 * stream_pairs(S, n_init, n_local) * 4 * D
+    q, k, v = make_qkv(1, 32, S, S, D, torch.float32, seed=0)
+    with torch.no_grad():
+        t1 = _time_cpu(lambda: R.streaming_reference(q, k, v, n_init, n_local))
+    per1 = sum(t1) / len(t1)
+    flop1 = 32 * stream_pairs(S, n_init, n_local) * 4 * D
+    del q, k, v
+
+    S2, topk, nh = 16384, 100, max(1, int(block_heads_sample))
+    q, k, v = make_qkv(1, nh, S2, S2, D, torch.bfloat16, seed=2, sink_scale=8.0)
+    with torch.no_grad():
+        t2 = _time_cpu(lambda: R.block_sparse_reference(q, k, v, topk))
+    scale2 = 32 / nh
+    per2 = sum(t2) / len(t2) * scale2
+    flop2 = 32 * block_tiles(S2, topk) * 4 * BLOCK * BLOCK * D
+    del q, k, v
     return {
-        "value": round(flops / per_layer / 1e12, 6),
+        "value": round(flop1 / per1 / 1e12, 6),
         "unit": "TFLOP/s",
-        "cores": int(threads),
+        "cores": info["threads"],
         "kind": "port",
-        "sample": (f"BASELINE config 1 (stream_llm S=4096 n_init=64 n_local=1024 D=96 fp32) via the "
-                   f"oracle's numpy restatement of the reference CPU path; {n_heads_sample} of 32 "
-                   f"heads x 3 repeats, scaled to 32 heads"),
-        "ms_per_layer": round(per_layer * 1e3, 2),
-        "ms_min_max": [round(min(times) * 32 / n_heads_sample * 1e3, 2),
-                       round(max(times) * 32 / n_heads_sample * 1e3, 2)],
-        "cpu_model": cpu_model(),
-        "logical_cpus": os.cpu_count(),
+        "sample": ("BASELINE config 1 (stream_llm S=4096 n_init=64 n_local=1024, 32 heads, fp32) "
+                   "through a torch-CPU fp32 restatement of the reference CPU path "
+                   "(_streaming_pytorch_ref after the D 96->128 pad: chunked full-row logits, "
+                   "masked softmax), warmup 1 + 3 repeats of the whole layer"),
+        "ms_per_layer": round(per1 * 1e3, 2),
+        "ms_min_max": [round(min(t1) * 1e3, 2), round(max(t1) * 1e3, 2)],
+        "block_cfg2": {
+            "value": round(flop2 / per2 / 1e12, 6), "unit": "TFLOP/s",
+            "ms_per_layer": round(per2 * 1e3, 1),
+            "ms_min_max": [round(min(t2) * scale2 * 1e3, 1), round(max(t2) * scale2 * 1e3, 1)],
+            "sample": (f"BASELINE config 2 (block_sparse top-100, S=16384, bf16) through the "
+                       f"torch-CPU restatement of _block_sparse_pytorch_ref (selector, token mask, "
+                       f"fp32 masked softmax over S x S, D padded to 128), one head at a time; "
+                       f"{nh} of 32 heads x 3 repeats, scaled to 32 heads"),
+        },
+        **info,
     }
 
 
@@ -387,7 +432,7 @@ def main():
     if not args.no_dense:
         result["dense"] = dense_baselines(q, k, v, S, H, D, ms_step)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_heads)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_block_heads)
     print(json.dumps(result), flush=True)
 
 
