@@ -91,7 +91,14 @@ size_t msa_estimate_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_q,
                                     int32_t head_dim) {
   if (batch <= 0 || n_slots <= 0 || s_q <= 0 || s_k <= 0 || head_dim <= 0) return 0;
   const int64_t sb = batch * n_slots;
-  const int64_t bytes = sb * (cdiv(s_q, MSA_BLOCK) + cdiv(s_k, MSA_BLOCK)) * head_dim * 4;
+  // pooled Q in fp64 (read through the scalar cache; rows padded to the
+  // scoring row group), pooled K^T in fp32
+  const int64_t n_qb_pad = cdiv(cdiv(s_q, MSA_BLOCK), kScoreRowPad) * kScoreRowPad;
+  const int64_t n_kb = cdiv(s_k, MSA_BLOCK);
+  int64_t bytes = sb * (n_qb_pad * 8 + n_kb * 4) * head_dim;
+  // the pooled scores of every row, fp32 (the reference's [B, H, n_bq, n_bk]
+  // score tensor)
+  bytes += sb * n_qb_pad * n_kb * 4;
   return size_t((bytes + 255) / 256 * 256);
 }
 
@@ -133,8 +140,9 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
 
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   const int64_t sb = q->size[0] * n_slots;
-  float* q_pool = static_cast<float*>(workspace);
-  float* k_poolT = q_pool + sb * n_qb * D;
+  const int n_qb_pad = int(cdiv(n_qb, kScoreRowPad) * kScoreRowPad);
+  double* q_pool = static_cast<double*>(workspace);
+  float* k_poolT = reinterpret_cast<float*>(q_pool + sb * n_qb_pad * D);
 
   PoolParams pp;
   memset(&pp, 0, sizeof(pp));
@@ -146,6 +154,7 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
   pp.s_k = k->size[2];
   pp.n_qb = n_qb;
   pp.n_kb = n_kb;
+  pp.n_qb_pad = n_qb_pad;
   pp.batch = int(q->size[0]);
   pp.n_slots = n_slots;
   pp.kv_group = int(q->size[1] / k->size[1]);
@@ -159,10 +168,12 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
   memset(&sp, 0, sizeof(sp));
   sp.q_pool = q_pool;
   sp.k_poolT = k_poolT;
+  sp.scores = k_poolT + sb * D * n_kb;
   sp.idx = idx;
   sp.cnt = cnt;
   sp.n_qb = n_qb;
   sp.n_kb = n_kb;
+  sp.n_qb_pad = n_qb_pad;
   sp.topk_max = topk_max;
   sp.batch = int(q->size[0]);
   sp.n_slots = n_slots;

@@ -20,31 +20,36 @@
 namespace msa {
 
 // ---------------------------------------------------------------------------
-// Pooling: one workgroup per (block, slot*batch, {q,k}).
-// q_pool layout [SB][n_qb][D]  (row major, fp32)
-// k_poolT layout [SB][D][n_kb] (transposed so the scorer reads it coalesced)
+// Pooling: one workgroup per (kPoolBlocks consecutive blocks, slot*batch, {q,k}).
+// Thread (bg, c) sums 16-byte chunk c of the 64 rows of block blk0 + bg in
+// fp64, eight rows' loads in flight.
+// q_pool layout [SB][n_qb_pad][D] (row major, fp64: the scorer reads it as
+//                                  scalars; rows n_qb .. n_qb_pad-1 unused)
+// k_poolT layout [SB][D][n_kb] (transposed so the scorer reads it coalesced;
+//                               written through LDS, kPoolBlocks ids per run)
 // ---------------------------------------------------------------------------
+constexpr int kPoolBlocks = 16;
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void pool_kernel(PoolParams P) {
-  constexpr int KCH = D / 8;            // 16-byte chunks per row
-  constexpr int ROWS_PER_PASS = 256 / KCH;  // thread rows covered per pass
-  __shared__ double part[ROWS_PER_PASS][D];
+  constexpr int KCH = D / 8;  // 16-byte chunks per row
+  constexpr int G = kPoolBlocks;
+  static_assert(G * KCH <= 256, "one thread per (block, chunk)");
+  __shared__ float tr[G][D + 1];
 
-  const int blk = blockIdx.x;
   const int sb = blockIdx.y;  // slot-major: sb = b * n_slots + s
   const bool is_k = blockIdx.z == 1;
   const int b = sb / P.n_slots;
   const int s = sb - b * P.n_slots;
   const int head = P.slot_heads[s];
-
   const int64_t S = is_k ? P.s_k : P.s_q;
   const int nb = is_k ? P.n_kb : P.n_qb;
-  if (blk >= nb) return;
+  const int blk0 = blockIdx.x * G;
+  if (blk0 >= nb) return;  // uniform over the workgroup
   const uint16_t* base;
   int64_t ss;
   if (is_k) {
-    const int kvh = head / P.kv_group;
-    base = reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + kvh * P.k_sh;
+    base = reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + (head / P.kv_group) * P.k_sh;
     ss = P.k_ss;
   } else {
     base = reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + head * P.q_sh;
@@ -52,43 +57,66 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams P) {
   }
 
   const int t = threadIdx.x;
-  const int c = t % KCH;
-  const int r0 = t / KCH;
+  const int bg = t / KCH;
+  const int c = t - bg * KCH;
+  const int blk = blk0 + bg;
+  const bool active = bg < G && blk < nb;
   double acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0;
-  if (r0 < ROWS_PER_PASS) {
-    for (int r = r0; r < kBlock; r += ROWS_PER_PASS) {
-      const int64_t row = int64_t(blk) * kBlock + r;
-      if (row < S) {
-        u32x4 v = load16(base + row * ss + c * 8);
+  if (active) {
+    const int64_t row0 = int64_t(blk) * kBlock;
+    const int rows = int(min(int64_t(kBlock), S - row0));  // rows past S pool as zeros
+    const uint16_t* p = base + row0 * ss + c * 8;
+    for (int r0 = 0; r0 < kBlock; r0 += 8) {
+      u32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = r0 + u < rows ? load16(p + (r0 + u) * ss) : zero_u32x4();
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          acc[2 * e] += double(T::to_float(uint16_t(v[e] & 0xffffu)));
-          acc[2 * e + 1] += double(T::to_float(uint16_t(v[e] >> 16)));
+          acc[2 * e] += double(T::to_float(uint16_t(v[u][e] & 0xffffu)));
+          acc[2 * e + 1] += double(T::to_float(uint16_t(v[u][e] >> 16)));
         }
-      }
     }
+  }
+  // mean in fp32 (sum / 64 is exact), then rounded to the input dtype
+  float pooled[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) part[r0][c * 8 + e] = acc[e];
+  for (int e = 0; e < 8; ++e) pooled[e] = T::to_float(T::from_float(float(acc[e]) * (1.0f / 64.0f)));
+  if (!is_k) {
+    if (active) {
+      double* dst = P.q_pool + (int64_t(sb) * P.n_qb_pad + blk) * D + c * 8;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        *reinterpret_cast<double2*>(dst + e) = make_double2(pooled[e], pooled[e + 1]);
+    }
+    return;
+  }
+  if (bg < G) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tr[bg][c * 8 + e] = pooled[e];
   }
   __syncthreads();
-  if (t < D) {
-    double sum = 0.0;
-    for (int r = 0; r < ROWS_PER_PASS; ++r) sum += part[r][t];
-    // mean in fp32 (sum / 64 is exact), then rounded to the input dtype
-    const float mean = float(sum) * (1.0f / 64.0f);
-    const float pooled = T::to_float(T::from_float(mean));
-    if (is_k) {
-      P.k_poolT[(int64_t(sb) * D + t) * P.n_kb + blk] = pooled;
-    } else {
-      P.q_pool[(int64_t(sb) * P.n_qb + blk) * D + t] = pooled;
-    }
+  const int nvalid = min(G, nb - blk0);
+  float* kT = P.k_poolT + int64_t(sb) * D * P.n_kb + blk0;
+  for (int i = t; i < D * G; i += 256) {
+    const int d = i / G, g = i - d * G;
+    if (g < nvalid) kT[int64_t(d) * P.n_kb + g] = tr[g][d];
   }
 }
 
 // ---------------------------------------------------------------------------
-// Scoring + top-k: one workgroup of 4 waves per (R consecutive q blocks, sb).
+// Scoring + top-k: one workgroup of 4 waves per (R consecutive q blocks, sb),
+// heaviest (last) groups first.  Each thread scores whole candidate columns
+// for all R rows: fp64 FMAs in d order, the pooled Q values (uniform over
+// the wave) coming through the scalar cache as SGPR operands, the pooled K
+// column from global memory.  Then each wave selects the top-k of its rows:
+// the k-th largest order key by a bitwise search (keys of KPL x 64
+// candidates in registers; KPL = 0 reads them from LDS), stopping as soon as
+// a threshold splits off exactly k keys, then an ordered compaction, equal
+// keys going to the lower id.
 // ---------------------------------------------------------------------------
 __device__ inline uint32_t order_key(float f) {
   f = f + 0.0f;  // -0 -> +0 so that equal scores compare equal
@@ -96,164 +124,125 @@ __device__ inline uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ inline int wave_excl_prefix(int v, int lane) {
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  return x - v;
+// Sum of v over the 64 lanes (every lane active): inclusive scan within the
+// 16-lane rows by DPP row shifts, then the row totals by row broadcasts;
+// lane 63 holds the total.
+__device__ inline int wave_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
-// Selects the k largest scores of sc[0..n) (ties -> lower index) and writes
-// their indices ascending to out[0..k).  n > k.  hist: 256 ints private to
-// the wave.
-__device__ void wave_topk(const float* sc, int n, int k, int* hist, int32_t* out, int lane) {
-  uint32_t prefix = 0u, pmask = 0u;
-  int krem = k;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = lane; i < 256; i += 64) hist[i] = 0;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    for (int c = lane; c < n; c += 64) {
-      const uint32_t u = order_key(sc[c]);
-      if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    // lane l owns the bins 255-4l .. 252-4l (descending)
-    int h[4];
-    int lsum = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      h[e] = hist[255 - 4 * lane - e];
-      lsum += h[e];
-    }
-    const int above = wave_excl_prefix(lsum, lane);
-    // the digit lives in the lane where above < krem <= above + lsum
-    const bool mine = (above < krem) && (krem <= above + lsum);
-    const unsigned long long who = __ballot(mine);
-    const int src = who ? __ffsll(who) - 1 : 0;
-    int digit = 0, newk = 0;
-    if (mine) {
-      int acc = above;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (acc + h[e] >= krem) {
-          digit = 255 - 4 * lane - e;
-          newk = krem - acc;
-          break;
-        }
-        acc += h[e];
-      }
-    }
-    digit = __shfl(digit, src, 64);
-    krem = __shfl(newk, src, 64);
-    prefix |= uint32_t(digit) << shift;
-    pmask |= 255u << shift;
-  }
-  // prefix is the k-th largest key; krem of its equal keys are taken, lowest ids first
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+// Selection of one row: writes the ids of the topk largest keys (equal keys
+// to the lower id) ascending to out.  keys(j) = key of candidate 64 j + lane
+// (0 past the row), nj key chunks (N > 0: at most N, loop unrolled so that
+// register-held keys are indexed statically); T = the k-th largest key or any
+// value with exactly topk keys >= T; need_eq = topk - #(keys > T).
+template <int N, typename KeyFn>
+__device__ inline void emit_topk(KeyFn keys, int nj, uint32_t T, int need_eq, int32_t* out,
+                                 int lane) {
+  const unsigned long long below = (1ull << lane) - 1ull;
   int written = 0, eq_seen = 0;
-  const unsigned long long lt = (1ull << lane) - 1ull;
-  for (int base = 0; base < n; base += 64) {
-    const int c = base + lane;
-    const bool valid = c < n;
-    const uint32_t u = valid ? order_key(sc[c]) : 0u;
-    const bool gt = valid && u > prefix;
-    const bool eq = valid && u == prefix;
+  auto one = [&](int j) {
+    const uint32_t k = keys(j);
+    const bool eq = k == T;
     const unsigned long long eqm = __ballot(eq);
-    const int eq_rank = eq_seen + __popcll(eqm & lt);
-    const bool sel = gt || (eq && eq_rank < krem);
+    const bool sel = k > T || (eq && eq_seen + __popcll(eqm & below) < need_eq);
     const unsigned long long selm = __ballot(sel);
-    const int pos = written + __popcll(selm & lt);
-    if (sel && pos < k) out[pos] = c;
+    if (sel) out[written + __popcll(selm & below)] = 64 * j + lane;
     written += __popcll(selm);
     eq_seen += __popcll(eqm);
+  };
+  if constexpr (N > 0) {
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (j < nj) one(j);
+  } else {
+    for (int j = 0; j < nj; ++j) one(j);
   }
 }
 
-template <int D, int R>
+template <int D, int R, int KPL>
 __global__ __launch_bounds__(256) void score_topk_kernel(ScoreParams P) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  double* qp = reinterpret_cast<double*>(smem);                  // [R][D]
-  int* hist = reinterpret_cast<int*>(qp + R * D);                // [4][256]
-  float* sc = reinterpret_cast<float*>(hist + 4 * 256);          // [R][ncand]
+  static_assert(R == 16, "one 16-row fp64 MFMA tile of query blocks, 4 rows per wave");
+  constexpr int NK = D / 4;  // k-steps of the 16x16x4 fp64 MFMA
 
   const int sb = blockIdx.y;
-  const int bq0 = blockIdx.x * R;
+  const int n_groups = (P.n_qb + R - 1) / R;
+  const int bq0 = (n_groups - 1 - int(blockIdx.x)) * R;
   const int nrows = min(R, P.n_qb - bq0);
   const int ncand = min(bq0 + nrows, P.n_kb);  // causal candidates of the last row
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int w = t >> 6;
+  const int l16 = lane & 15;
+  const int lq = lane >> 4;
+  // row scores of this group: workspace rows [n_qb_pad][n_kb] of the slot
+  float* sc = P.scores + (int64_t(sb) * P.n_qb_pad + bq0) * P.n_kb;
 
-  for (int i = t; i < R * D; i += 256) {
-    const int r = i / D, d = i - r * D;
-    qp[i] = (r < nrows) ? double(P.q_pool[(int64_t(sb) * P.n_qb + bq0 + r) * D + d]) : 0.0;
+  // A operands: pooled Q row bq0 + l16, dims 4s + lq (rows past n_qb are
+  // padding, read and never stored)
+  double qa[NK];
+  {
+    const double* qrow = P.q_pool + (int64_t(sb) * P.n_qb_pad + bq0 + l16) * D + lq;
+#pragma unroll
+    for (int s = 0; s < NK; ++s) qa[s] = qrow[4 * s];
   }
-  __syncthreads();
-
-  // Each thread scores NC columns (stride 256) at once, NC chosen from the
-  // candidate count: the pooled-K loads of a d-chunk are issued together and
-  // every pooled-Q value read from LDS serves all NC columns.  Per (row,
-  // column) the fp64 FMAs run in d order.
-  const float* kT = P.k_poolT + int64_t(sb) * D * P.n_kb;
-  auto score = [&](auto nc) {
-    constexpr int NC = decltype(nc)::value, DC = 8;
-    for (int cb = 0; cb < ncand; cb += 256 * NC) {
-      double acc[NC][R];
+  // candidate tiles of 16 ids, two at a time per wave (independent MFMA
+  // chains): wave w takes tiles w + 8 m and w + 8 m + 4.  Output element i
+  // of a lane: row lq + 4 i, candidate 16 tile + l16 (the accumulator layout
+  // of v_mfma_f64_16x16x4f64, checked on gfx950).
+  const float* kT = P.k_poolT + int64_t(sb) * D * P.n_kb + int64_t(lq) * P.n_kb;
+  const int n_tiles = (ncand + 15) >> 4;
+  auto store = [&](const f64x4& acc, int c) {
+    if (c < ncand) {
 #pragma unroll
-      for (int j = 0; j < NC; ++j)
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[j][r] = 0.0;
-      for (int d0 = 0; d0 < D; d0 += DC) {
-        float kv[NC][DC];
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          const int c = min(cb + t + 256 * j, ncand - 1);
-#pragma unroll
-          for (int u = 0; u < DC; ++u) kv[j][u] = kT[int64_t(d0 + u) * P.n_kb + c];
-        }
-#pragma unroll
-        for (int u = 0; u < DC; ++u)
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            const double qv = qp[r * D + d0 + u];
-#pragma unroll
-            for (int j = 0; j < NC; ++j) acc[j][r] = fma(qv, double(kv[j][u]), acc[j][r]);
-          }
-      }
-#pragma unroll
-      for (int j = 0; j < NC; ++j) {
-        const int c = cb + t + 256 * j;
-        if (c < ncand)
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            // forced ids score +inf: always inside the top-k
-            const bool forced = ((P.flags & kSelectForceFirst) && c == 0) ||
-                                ((P.flags & kSelectForceDiag) && c == bq0 + r);
-            sc[r * ncand + c] = forced ? __builtin_inff() : float(acc[j][r]) * P.scale;
-          }
+      for (int i = 0; i < 4; ++i) {
+        const int r = lq + 4 * i;
+        // forced ids score +inf: always inside the top-k
+        const bool forced = ((P.flags & kSelectForceFirst) && c == 0) ||
+                            ((P.flags & kSelectForceDiag) && c == bq0 + r);
+        sc[int64_t(r) * P.n_kb + c] = forced ? __builtin_inff() : float(acc[i]) * P.scale;
       }
     }
   };
-  if (ncand > 512) score(std::integral_constant<int, 4>());
-  else if (ncand > 256) score(std::integral_constant<int, 2>());
-  else score(std::integral_constant<int, 1>());
+  for (int ct = w; ct < n_tiles; ct += 8) {
+    const int c0 = ct * 16 + l16;
+    const int c1 = c0 + 64;  // tile ct + 4 (may lie past the last tile: clamped, not stored)
+    const float* col0 = kT + min(c0, ncand - 1);
+    const float* col1 = kT + min(c1, ncand - 1);
+    float k0[NK], k1[NK];
+#pragma unroll
+    for (int s = 0; s < NK; ++s) {
+      k0[s] = col0[int64_t(4 * s) * P.n_kb];
+      k1[s] = col1[int64_t(4 * s) * P.n_kb];
+    }
+    f64x4 a0 = {0.0, 0.0, 0.0, 0.0}, a1 = a0;
+#pragma unroll
+    for (int s = 0; s < NK; ++s) {
+      a0 = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[s], double(k0[s]), a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[s], double(k1[s]), a1, 0, 0, 0);
+    }
+    store(a0, c0);
+    if (ct + 4 < n_tiles) store(a1, c1);
+  }
   __syncthreads();
 
+  // ---- top-k, rows 4w .. 4w+3 of the group
   const int topk = P.slot_topk[sb % P.n_slots];
-  for (int r = w; r < nrows; r += 4) {
+  auto finish_row = [&](int r, bool selected_all) {
     const int bq = bq0 + r;
     const int n = min(bq + 1, P.n_kb);
     const int cnt = min(topk, n);
     int32_t* out = P.idx + (int64_t(sb) * P.n_qb + bq) * P.topk_max;
-    if (n <= topk) {
+    if (selected_all)
       for (int c = lane; c < n; c += 64) out[c] = c;
-    } else {
-      wave_topk(sc + r * ncand, n, topk, hist + w * 256, out, lane);
-    }
     // Surplus slots (the reference's -inf picks, which torch.topk fills with
     // q-frame future ids): the next ids bq+1, bq+2, ...  The token mask is
     // in the absolute frame (row i at s_k - s_q + i), so with s_q < s_k some
@@ -264,6 +253,94 @@ __global__ __launch_bounds__(256) void score_topk_kernel(ScoreParams P) {
     const int a1 = P.s_k - P.s_q + min(64 * bq + 63, P.s_q - 1);
     const int n_sur = max(0, min(topk - cnt, (a1 >> 6) - bq));
     if (lane == 0) P.cnt[int64_t(sb) * P.n_qb + bq] = cnt + n_sur;
+  };
+  if constexpr (KPL > 0) {
+    // the four rows' searches interleaved (independent reduction chains);
+    // rows that need no search (n <= topk or past the group) stay done
+    uint32_t keys[4][KPL];
+    uint32_t T[4];
+    bool done[4];
+    int nj[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * w + i;
+      const int n = r < nrows ? min(bq0 + r + 1, P.n_kb) : 0;
+      nj[i] = (n + 63) >> 6;
+      done[i] = n <= topk;
+      T[i] = 0u;
+      const float* row = sc + int64_t(r) * P.n_kb;
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        const int c = 64 * j + lane;
+        keys[i][j] = (!done[i] && c < n) ? order_key(row[c]) : 0u;
+      }
+    }
+    for (int bit = 31; bit >= 0; --bit) {
+      if (done[0] && done[1] && done[2] && done[3]) break;
+      int ge[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t cand = T[i] | (1u << bit);
+        int mine = 0;
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) mine += keys[i][j] >= cand ? 1 : 0;
+        ge[i] = wave_sum(mine);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (!done[i]) {
+          if (ge[i] >= topk) T[i] = T[i] | (1u << bit);
+          if (ge[i] == topk) done[i] = true;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * w + i;
+      if (r >= nrows) continue;
+      const int n = min(bq0 + r + 1, P.n_kb);
+      if (n > topk) {
+        int gt = 0;
+        if (T[i] != 0xffffffffu) {
+#pragma unroll
+          for (int j = 0; j < KPL; ++j) gt += keys[i][j] > T[i] ? 1 : 0;
+          gt = wave_sum(gt);
+        }
+        int32_t* out = P.idx + (int64_t(sb) * P.n_qb + bq0 + r) * P.topk_max;
+        const uint32_t(&kr)[KPL] = keys[i];
+        emit_topk<KPL>([&](int j) { return kr[j]; }, nj[i], T[i], topk - gt, out, lane);
+      }
+      finish_row(r, n <= topk);
+    }
+  } else {
+    // long key axes: one row at a time, keys read from the workspace
+    for (int r = 4 * w; r < min(4 * w + 4, nrows); ++r) {
+      const int n = min(bq0 + r + 1, P.n_kb);
+      if (n > topk) {
+        const float* row = sc + int64_t(r) * P.n_kb;
+        auto key_at = [&](int j) -> uint32_t {
+          const int c = 64 * j + lane;
+          return c < n ? order_key(row[c]) : 0u;
+        };
+        const int nj = (n + 63) >> 6;
+        auto count_ge = [&](uint32_t thr) -> int {
+          int mine = 0;
+          for (int j = 0; j < nj; ++j) mine += key_at(j) >= thr ? 1 : 0;
+          return wave_sum(mine);
+        };
+        uint32_t T = 0u;
+        for (int bit = 31; bit >= 0; --bit) {
+          const uint32_t cand = T | (1u << bit);
+          const int ge = count_ge(cand);
+          if (ge >= topk) T = cand;
+          if (ge == topk) break;
+        }
+        const int need_eq = topk - (T == 0xffffffffu ? 0 : count_ge(T + 1u));
+        emit_topk<0>(key_at, nj, T, need_eq,
+                  P.idx + (int64_t(sb) * P.n_qb + bq0 + r) * P.topk_max, lane);
+      }
+      finish_row(r, n <= topk);
+    }
   }
 }
 
@@ -272,7 +349,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(ScoreParams P) {
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 static hipError_t launch_pool_t(const PoolParams& p, hipStream_t st) {
-  dim3 grid(max(p.n_qb, p.n_kb), p.batch * p.n_slots, 2);
+  dim3 grid((max(p.n_qb, p.n_kb) + kPoolBlocks - 1) / kPoolBlocks, p.batch * p.n_slots, 2);
   hipLaunchKernelGGL((pool_kernel<T, D>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
@@ -288,46 +365,31 @@ hipError_t launch_pool(const PoolParams& p, int dtype, int D, hipStream_t st) {
   return launch_pool_t<F16, 128>(p, st);
 }
 
-int score_rows_for(int n_kb) {
-  if (n_kb <= 2048) return 8;
-  if (n_kb <= 4096) return 4;
-  if (n_kb <= 8192) return 2;
-  if (n_kb <= 16384) return 1;
-  return 0;
-}
+// Query blocks per scoring workgroup (one 16-row MFMA tile); the row scores
+// go to the estimator workspace.
+int score_rows_for(int n_kb) { return n_kb <= 16384 ? 16 : 0; }
 
-size_t score_smem_bytes(int R, int D, int n_kb) {
-  return size_t(R) * D * sizeof(double) + 4 * 256 * sizeof(int) +
-         size_t(R) * size_t(n_kb) * sizeof(float);
-}
-
-template <int D, int R>
+template <int D, int R, int KPL>
 static hipError_t launch_score_t(const ScoreParams& p, hipStream_t st) {
-  const size_t smem = score_smem_bytes(R, D, p.n_kb);
-  auto kern = score_topk_kernel<D, R>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(smem));
-  if (e != hipSuccess) return e;
   dim3 grid((p.n_qb + R - 1) / R, p.batch * p.n_slots);
-  hipLaunchKernelGGL(kern, grid, dim3(256), smem, st, p);
+  hipLaunchKernelGGL((score_topk_kernel<D, R, KPL>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
+// keys per lane held in registers for the selection: KPL * 64 >= n_kb
 template <int D>
-static hipError_t launch_score_d(const ScoreParams& p, int R, hipStream_t st) {
-  switch (R) {
-    case 8: return launch_score_t<D, 8>(p, st);
-    case 4: return launch_score_t<D, 4>(p, st);
-    case 2: return launch_score_t<D, 2>(p, st);
-    default: return launch_score_t<D, 1>(p, st);
-  }
+static hipError_t launch_score_d(const ScoreParams& p, hipStream_t st) {
+  if (p.n_kb <= 256) return launch_score_t<D, 16, 4>(p, st);
+  if (p.n_kb <= 512) return launch_score_t<D, 16, 8>(p, st);
+  if (p.n_kb <= 1024) return launch_score_t<D, 16, 16>(p, st);
+  if (p.n_kb <= 2048) return launch_score_t<D, 16, 32>(p, st);
+  return launch_score_t<D, 16, 0>(p, st);
 }
 
 hipError_t launch_score(const ScoreParams& p, int D, hipStream_t st) {
-  const int R = score_rows_for(p.n_kb);
-  if (D == 64) return launch_score_d<64>(p, R, st);
-  if (D == 96) return launch_score_d<96>(p, R, st);
-  return launch_score_d<128>(p, R, st);
+  if (D == 64) return launch_score_d<64>(p, st);
+  if (D == 96) return launch_score_d<96>(p, st);
+  return launch_score_d<128>(p, st);
 }
 
 }  // namespace msa

@@ -14,19 +14,20 @@ struct PoolParams {
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t s_q, s_k;
-  int n_qb, n_kb;
+  int n_qb, n_kb, n_qb_pad;  // n_qb_pad: n_qb rounded up to kScoreRowPad
   int batch, n_slots, kv_group;
-  float* q_pool;   // [batch*n_slots][n_qb][D]
+  double* q_pool;  // [batch*n_slots][n_qb_pad][D] (pooled values, exact in fp64)
   float* k_poolT;  // [batch*n_slots][D][n_kb]
   int16_t slot_heads[kMaxHeads];  // head of q for each slot (kernel-argument copy)
 };
 
 struct ScoreParams {
-  const float* q_pool;
+  const double* q_pool;  // [batch*n_slots][n_qb_pad][D]
   const float* k_poolT;
+  float* scores;  // [batch*n_slots][n_qb_pad][n_kb]: pooled scores of every row
   int32_t* idx;  // [batch*n_slots][n_qb][topk_max]
   int32_t* cnt;  // [batch*n_slots][n_qb]
-  int n_qb, n_kb, topk_max, batch, n_slots;
+  int n_qb, n_kb, n_qb_pad, topk_max, batch, n_slots;
   int s_q, s_k;  // row i of the query is absolute position s_k - s_q + i
   float scale;
   int flags;     // kSelectForceFirst | kSelectForceDiag
@@ -37,6 +38,8 @@ struct ScoreParams {
 // block always selected, inside the top-k (their scores count as +inf; ties
 // among forced ids go to the lower id).
 constexpr int kSelectForceFirst = 1;
+// Pooled-Q rows are padded to a multiple of the largest scoring row group.
+constexpr int kScoreRowPad = 16;
 constexpr int kSelectForceDiag = 2;
 
 // 32-bit fields throughout: the kernel reads these with scalar loads, which
@@ -198,7 +201,6 @@ constexpr int kDecodeMaxSplit = 2048;
 hipError_t launch_pool(const PoolParams& p, int dtype, int D, hipStream_t st);
 hipError_t launch_score(const ScoreParams& p, int D, hipStream_t st);
 int score_rows_for(int n_kb);
-size_t score_smem_bytes(int R, int D, int n_kb);
 hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st);
 hipError_t launch_vscale(const StageParams& p, int dtype, int D, hipStream_t st);
 hipError_t launch_decode(const DecodeParams& p, int dtype, int out_dtype, int D, hipStream_t st);

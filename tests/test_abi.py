@@ -56,9 +56,12 @@ def test_decode_noalloc_refuses_oversize_before_any_device_call():
 
 
 def test_workspace_sizes():
-    # estimator: pooled Q + pooled K^T in fp32
-    assert _abi.estimate_workspace_bytes(1, 32, 16384, 16384, 96) == 32 * 512 * 96 * 4
-    assert _abi.estimate_workspace_bytes(1, 1, 100, 100, 64) == 1024  # 2*2*64*4 rounded to 256
+    # estimator: pooled Q in fp64 (rows padded to 16), pooled K^T in fp32 and
+    # the fp32 pooled scores of every (padded) row, rounded up to 256 bytes
+    assert _abi.estimate_workspace_bytes(1, 32, 16384, 16384, 96) == \
+        32 * (256 * 96 * (8 + 4) + 256 * 256 * 4)
+    assert _abi.estimate_workspace_bytes(1, 1, 100, 100, 64) == \
+        (16 * 64 * 8 + 2 * 64 * 4 + 16 * 2 * 4 + 255) // 256 * 256
     # attention: staged K and V operands (16-bit) padded to 64 keys, the V
     # maxima per 64-key tile (fp32) and the V exponent per kv head (int32),
     # each rounded up to 256 bytes, then 256 bytes of work-queue counters

@@ -72,6 +72,21 @@ def test_estimator_bit_exact(gpu_device, case):
     assert np.array_equal(got_i, ridx), f"{(got_i != ridx).sum()} ids differ"
 
 
+def test_estimator_long_key_axis(gpu_device):
+    """More than 2048 key blocks (S = 200000): the selection reads its keys
+    from LDS instead of registers; ids bit-exact with the oracle."""
+    from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
+
+    S, topk = 200000, 160
+    print(f"[estimator] S={S} topk={topk}", flush=True)
+    q, k, _ = make_qkv(1, 2, S, S, 64, torch.bfloat16, seed=11, sink_scale=8.0)
+    idx, cnt = select_block_sparse_topk_indices(*to_dev(gpu_device, q, k), topk, return_counts=True)
+    ridx, rcnt = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, "bf16")
+    got = idx.cpu().numpy()
+    assert np.array_equal(cnt.cpu().numpy(), rcnt)
+    assert np.array_equal(got, ridx), f"{(got != ridx).sum()} ids differ"
+
+
 def test_estimator_ties_to_lower_id(gpu_device):
     from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
 
