@@ -2,10 +2,13 @@
 """Sparse prefill attention benchmark: one Phi-3-mini layer on one MI355X.
 
 A step = the whole sparse attention of one layer, all heads, inputs resident
-in HBM: one estimator launch (block top-k for the block_sparse heads), one K/V
-staging launch on a side stream under the estimator (as the patched forward
-runs them), and one attention launch after both.  QKV projection, RoPE and o_proj are
-outside the step (the reference's per-layer attention, BASELINE.json metric).
+in HBM, launched as the patched forward launches it (launch_block_layer): the
+block estimator (block top-k for the block_sparse heads) on a side stream
+beside the K/V staging launch; the attention launch of the stream_llm /
+dense heads as soon as the staging is done; then, after the estimator, the
+attention launch of the block heads (one attention launch after both when
+every head is block_sparse).  QKV projection, RoPE and o_proj are outside the
+step (the reference's per-layer attention, BASELINE.json metric).
 
 Default workload ("headline"): S = 65536, 32 heads x 96, bf16, every head
 sparse, 16 stream_llm(n_init 128, n_local 4096) + 16 block_sparse(top-100)
@@ -13,8 +16,8 @@ heads (seeded head assignment).  Q, K, V ~ N(0,1) from a seeded generator,
 RoPE theta 1e4 on Q and K, K rows 0-3 scaled 8x (attention sinks).
 
 Printed JSON line: value = algorithmic TFLOP/s of the whole step; roofline =
-the attention kernel alone (HIP events on the launch stream) against the
-bf16 MFMA peak; dense = same-GPU dense attention on the same tensors
+the attention kernel alone (the sum of its launches' durations, HIP events on
+the launch stream) against the bf16 MFMA peak; dense = same-GPU dense attention on the same tensors
 (PyTorch SDPA flash and this build's dense kind); cpu_baseline = the
 reference's CPU path (its torch ops, restated in oracle/cpu_reference.py) for
 BASELINE configs 1 (stream_llm) and 2 (block_sparse) timed on the host cores; decode = one decode step against the layer's K/V cache;
@@ -294,7 +297,7 @@ def main():
     import torch
 
     from minference import _abi
-    from minference.modules.minference_forward import build_layer_plan
+    from minference.modules.minference_forward import build_layer_plan, launch_block_layer
     from minference.ops.common import sparse_scale
 
     dev = torch.device("cuda:0")
@@ -322,56 +325,55 @@ def main():
     sel_flags = ((_abi.MSA_SELECT_FORCE_FIRST if force_first else 0)
                  | (_abi.MSA_SELECT_FORCE_DIAG if force_diag else 0))
 
-    def launch_est():
-        if n_slots:
-            _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max,
-                                s_sparse, idx, cnt, ws_est, flags=sel_flags)
-
-    def launch_stage():
-        _abi.stage_kv(k, v, ws_att)
-
-    def launch_attn():
-        _abi.layer_attention(q, k, v, out, plan.heads, idx=idx if n_slots else None,
-                             cnt=cnt if n_slots else None, idx_slots=n_slots,
-                             topk_max=plan.topk_max, ws=ws_att, staged=True)
-
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
-    side = _side_stream(dev)
+    names = ("start", "est0", "est1", "stage0", "stage1", "attn0", "attn0_end", "attn1",
+             "attn1_end")
+    ev = [{n: torch.cuda.Event(enable_timing=True) for n in names} for _ in range(args.steps)]
+    if not n_slots:
+        idx = cnt = None
 
     def step(e=None):
-        # as the patched forward runs a layer: K/V staging on the side stream
-        # under the estimator, then the attention launch after both
+        # the product's schedule (launch_block_layer): the estimator on the
+        # side stream beside the staging; the heads that need no block ids
+        # start when the staging is done
+        if n_slots:
+            launch_block_layer(q, k, v, plan, out, idx, cnt, ws_att, ws_est, sel_flags,
+                               mark=(lambda n, st: e[n].record(st)) if e else None)
+            return
         if e:
-            e[0].record(stream)
-        side.wait_stream(stream)
-        with torch.cuda.stream(side):
-            if e:
-                e[4].record(side)
-            launch_stage()
-            if e:
-                e[5].record(side)
-        launch_est()
+            e["start"].record(stream)
+            e["stage0"].record(stream)
+        _abi.stage_kv(k, v, ws_att)
         if e:
-            e[1].record(stream)
-        stream.wait_stream(side)
+            e["stage1"].record(stream)
+            e["attn0"].record(stream)
+        _abi.layer_attention(q, k, v, out, plan.heads, ws=ws_att, staged=True)
         if e:
-            e[2].record(stream)
-        launch_attn()
-        if e:
-            e[3].record(stream)
+            e["attn0_end"].record(stream)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(ev[i])
+        step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
-    t_est = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
-    t_stage = sum(e[4].elapsed_time(e[5]) for e in ev) / args.steps
-    t_attn = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    # the per-launch breakdown: K more steps with events at the phase
+    # boundaries (outside the timed loop: each timing event adds a little)
+    for i in range(args.steps):
+        step(ev[i])
+    torch.cuda.synchronize()
+    split = bool(n_slots) and len(plan.block_heads) < H
+
+    def avg(a, b):
+        return sum(e[a].elapsed_time(e[b]) for e in ev) / args.steps
+
+    t_est = avg("est0", "est1") if n_slots else 0.0
+    t_stage = avg("stage0", "stage1")
+    t_launch = [avg("attn0", "attn0_end")] + ([avg("attn1", "attn1_end")] if split else [])
+    t_attn = sum(t_launch)
+    t_pre = avg("start", "attn0")
 
     flop_stream = n_stream * stream_pairs(S, n_init, n_local) * 4 * D
     flop_block = n_block * block_tiles(S, topk) * 4 * BLOCK * BLOCK * D
@@ -412,7 +414,10 @@ def main():
         "algorithmic_flop": flop,
         "kernels_ms": {"estimator": round(t_est, 4), "stage_kv": round(t_stage, 4),
                        "attention": round(t_attn, 4)},
-        "stage_overlaps_estimator": True,
+        "attention_launches_ms": [round(t, 4) for t in t_launch],
+        "schedule": ("estimator beside the staging; other heads, then block heads"
+                     if split else "estimator beside the staging" if n_slots else "sequential"),
+        "ms_before_first_attention": round(t_pre, 4),
         "estimator_gbps": round(est_bytes / (t_est * 1e-3) / 1e9, 1) if n_slots else None,
         "roofline": {
             "bound": "mfma",
@@ -646,9 +651,12 @@ def vs_bench(args, dev):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(ev[i])
+        step()
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    for i in range(args.steps):  # the breakdown, outside the timed loop
+        step(ev[i])
+    torch.cuda.synchronize()
     t_est = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
     t_stage = sum(e[4].elapsed_time(e[5]) for e in ev) / args.steps
     t_attn = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MSA_ABI_VERSION 7
+#define MSA_ABI_VERSION 8
 
 /* status codes (negative: validation, nothing launched) */
 #define MSA_OK 0
@@ -57,6 +57,7 @@ extern "C" {
 #define MSA_KIND_BLOCK 2  /* "block_sparse" */
 #define MSA_KIND_VS 3     /* "vertical_and_slash" */
 #define MSA_KIND_FULL 4   /* dense without the causal mask (dense_attention(causal=False)) */
+#define MSA_KIND_SKIP 5   /* left to another launch: rows neither read nor written */
 
 /* msa_block_estimate_ex flags */
 #define MSA_SELECT_FORCE_FIRST 1 /* block 0 always selected */
@@ -165,7 +166,9 @@ size_t msa_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t s_
  * dtype) or fp32.  Rows with no visible key are written as 0.
  * MSA_KIND_FULL heads see every key (dense_attention(causal=False),
  * minference/backend_npu/attention.py:221-230); S_q > S_k is accepted only
- * when every head is MSA_KIND_FULL. */
+ * when every head is MSA_KIND_FULL (or MSA_KIND_SKIP).  MSA_KIND_SKIP heads
+ * are left out of the launch: their output rows are not written, their
+ * descriptors' other fields are not read. */
 int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k,
                         const msa_tensor4* v, const msa_tensor4* o,
                         const msa_head_desc* heads, int32_t n_heads,

@@ -504,6 +504,7 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   int n_vs = 0;
   for (int h = 0; h < n_heads; ++h) {
     const msa_head_desc& hd = heads[h];
+    if (hd.kind == MSA_KIND_SKIP) continue;
     if (hd.kind != MSA_KIND_DENSE && hd.kind != MSA_KIND_STREAM && hd.kind != MSA_KIND_BLOCK &&
         hd.kind != MSA_KIND_VS && hd.kind != MSA_KIND_FULL)
       return MSA_E_HEADS;
@@ -596,10 +597,13 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
     if (BH <= kMaxHeads) {
       int pairs[kMaxHeads];
       HeadWork work[kMaxHeads];
-      for (int i = 0; i < BH; ++i) pairs[i] = i;
-      interleave_kinds(pairs, BH, heads, int(H));
-      for (int i = 0; i < BH; ++i) work[i] = head_work(heads[pairs[i] % H], n_kb, topk_max);
-      order_items(ap, pairs, work, BH);
+      int n = 0;
+      for (int i = 0; i < BH; ++i)
+        if (heads[i % H].kind != MSA_KIND_SKIP) pairs[n++] = i;
+      if (n == 0) return MSA_OK;
+      interleave_kinds(pairs, n, heads, int(H));
+      for (int i = 0; i < n; ++i) work[i] = head_work(heads[pairs[i] % H], n_kb, topk_max);
+      order_items(ap, pairs, work, n);
     } else {
       ap.n_hl = 0;  // every pair, plain order
     }
@@ -656,7 +660,7 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
     if (hd.kind == MSA_KIND_VS) {
       vs_pairs[n_v] = i;
       vs_work[n_v++] = head_work(hd, n_kb, topk_max);
-    } else {
+    } else if (hd.kind != MSA_KIND_SKIP) {
       other[n_o++] = i;
     }
   }

@@ -49,6 +49,7 @@ constexpr int KIND_STREAM = 1;
 constexpr int KIND_BLOCK = 2;
 constexpr int KIND_VS = 3;
 constexpr int KIND_FULL = 4;  // dense without the causal mask
+constexpr int KIND_SKIP = 5;  // computed by another launch
 
 // P = 2^(s*c - m) with m = (row max)*c - kPBias: a row's largest P is 2^7,
 // and the rescale triggers above 2^kPSlackBits times that (2^15 < 65504, so
@@ -841,8 +842,12 @@ void attn_kernel(AttnParams P) {
     const int hl = g / P.n_qb;
     item_body(int(P.head_order[hl]), P.n_qb - 1 - (g - hl * P.n_qb));
   } else {
+    // plain order: every (batch, head) pair; the host lists no item of a
+    // skipped head in the other modes
     const int BH = P.batch * P.heads;
-    item_body(int(blockIdx.x) % BH, P.n_qb - 1 - int(blockIdx.x) / BH);
+    const int hh = int(blockIdx.x) % BH;
+    if (P.hd[hh % P.heads].kind == KIND_SKIP) return;
+    item_body(hh, P.n_qb - 1 - int(blockIdx.x) / BH);
   }
 }
 

@@ -42,6 +42,7 @@ MSA_KIND_STREAM = 1
 MSA_KIND_BLOCK = 2
 MSA_KIND_VS = 3
 MSA_KIND_FULL = 4
+MSA_KIND_SKIP = 5
 MSA_VS_MAX_SEQ = 131072
 
 MSA_SELECT_FORCE_FIRST = 1
@@ -49,7 +50,7 @@ MSA_SELECT_FORCE_DIAG = 2
 
 MSA_MAX_HEADS = 128
 MSA_BLOCK = 64
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _DTYPE_CODE = {
     torch.bfloat16: MSA_DTYPE_BF16,

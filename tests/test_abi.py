@@ -303,3 +303,18 @@ def test_python_ops_refuse_cpu_tensors():
     cos = torch.zeros(1, 128, 96, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
         apply_rotary_pos_emb(q, q, cos, cos)
+
+
+def test_skip_kind_is_exempt_from_head_checks():
+    """MSA_KIND_SKIP heads are left out of a launch: their other fields are
+    not checked, and they do not count as causal heads for S_q > S_k (each
+    call then fails later, on the deliberately small workspace)."""
+    q, kv = t4([1, 4, 512, 96]), t4([1, 4, 256, 96])
+    hd = heads(4, kind=_abi.MSA_KIND_FULL)
+    hd[1].kind = _abi.MSA_KIND_SKIP
+    hd[1].scale = 0.0
+    hd[1].slot = 99
+    assert attn(q, kv, kv, q, hd, 4, wsb=100) == _abi.MSA_E_WORKSPACE
+    hd[2].kind = _abi.MSA_KIND_STREAM
+    assert attn(q, kv, kv, q, hd, 4, wsb=100) == _abi.MSA_E_SEQ
+
