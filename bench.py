@@ -158,8 +158,9 @@ def make_inputs(S, H, D, seed, device):
 
 
 def profiled_traffic(workload):
-    """HBM bytes per attention launch measured by two rocprofv3 --pmc runs
-    (FETCH_SIZE, WRITE_SIZE; calibrated on a device copy), from profiles/."""
+    """HBM bytes of the attention kernel per step (its launches of the layer)
+    measured by two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE; calibrated
+    on a device copy), from profiles/."""
     name = TRAFFIC_PROFILE.get(workload)
     if not name:
         return None
@@ -167,7 +168,7 @@ def profiled_traffic(workload):
     try:
         with open(path) as f:
             for ln in f:
-                if ln.startswith("attn_kernel traffic_bytes_per_launch:"):
+                if ln.startswith("attn_kernel traffic_bytes_per_step:"):
                     return int(ln.split(":")[1])
     except OSError:
         pass

@@ -37,7 +37,7 @@ extern "C" {
 #define MSA_E_RANK (-2)        /* shape mismatch between q/k/v/o */
 #define MSA_E_DTYPE (-3)       /* unsupported or mismatched dtype */
 #define MSA_E_HEAD_DIM (-4)    /* D not in {64, 96, 128} */
-#define MSA_E_ALIGN (-5)       /* D stride != 1 or rows not 16-byte aligned */
+#define MSA_E_ALIGN (-5)       /* D stride != 1, rows not 16-byte aligned or row stride >= 2^24 */
 #define MSA_E_BLOCK (-6)       /* block size other than 64 */
 #define MSA_E_TOPK (-7)        /* topk < 1 or topk > n_kv_blocks */
 #define MSA_E_HEADS (-8)       /* bad head count / head index / kind */

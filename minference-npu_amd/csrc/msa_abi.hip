@@ -28,10 +28,13 @@ int elem_size(int dtype) {
 
 bool head_dim_ok(int64_t d) { return d == 64 || d == 96 || d == 128; }
 
-// D contiguous, every row and the base 16-byte aligned.
+// D contiguous, every row and the base 16-byte aligned, row stride below
+// 2^24 elements (the attention kernel addresses a query block's 64 rows
+// with 32-bit byte offsets).
 bool aligned(const msa_tensor4* t) {
   const int es = elem_size(t->dtype);
   if (es == 0 || t->stride[3] != 1) return false;
+  if (t->stride[2] < 0 || t->stride[2] >= (int64_t(1) << 24)) return false;
   if ((reinterpret_cast<uintptr_t>(t->data) & 15u) != 0) return false;
   for (int i = 0; i < 3; ++i)
     if (t->size[i] > 1 && ((t->stride[i] * es) & 15) != 0) return false;
@@ -73,7 +76,7 @@ const char* msa_status_str(int status) {
     case MSA_E_RANK: return "shape mismatch between q, k, v and o";
     case MSA_E_DTYPE: return "unsupported or mismatched dtype (q/k/v must be bf16 or fp16; o same or fp32)";
     case MSA_E_HEAD_DIM: return "head_dim must be 64, 96 or 128";
-    case MSA_E_ALIGN: return "head_dim stride must be 1 and rows 16-byte aligned";
+    case MSA_E_ALIGN: return "head_dim stride must be 1, rows 16-byte aligned and the row stride below 2^24";
     case MSA_E_BLOCK: return "block size must be 64";
     case MSA_E_TOPK: return "topk must be in [1, n_kv_blocks]";
     case MSA_E_HEADS: return "bad head count, head index or head kind";

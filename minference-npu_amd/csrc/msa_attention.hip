@@ -417,112 +417,154 @@ void attn_kernel(AttnParams P) {
   //   that range's counter, then of the other XCDs' ranges once its own is
   //   empty, and exits when every range is empty.
   //   other kinds: workgroup i is item i / 8 of XCD i % 8's range (ranges
-  //   cut by estimated cost); without a list, item i in plain order.
+  //   cut by estimated cost); without a list, item i in plain order.  (A
+  //   persistent grid over these items, resident workgroups taking items of
+  //   their XCD's range with a static stride and requesting the next item's
+  //   first tiles before the output merge, ran 12-15 % slower than one item
+  //   per workgroup.)
   __shared__ int s_item;
   const int xcd = blockIdx.x & 7;
-  auto item_body = [&](const int hh, const int bq) INLINE {
-  const int b = hh / P.heads;
-  const int h = hh - b * P.heads;
-  const int kvh = h / P.kv_group;
-  const HeadArg hd = P.hd[h];
-  const int kind = hd.kind;
 
-  const int q0 = bq * kBlock;
-  const int nrows = min(kBlock, P.s_q - q0);
-  const int off = P.s_k - P.s_q;
-  const int a0 = q0 + off;
-  const int a1 = q0 + nrows - 1 + off;
-  const int last_tile = min(a1 >> 6, P.n_kb - 1);
-  const int n_init = hd.p1;
-  const int n_local = hd.p2;
-  // tile t needs no mask for the causal / S_k bounds iff t < F
-  const int Fe = min(min((a0 + 1) >> 6, P.s_k >> 6), last_tile + 1);
-
-  TileSeq seq;
-  seq.n_kb = P.n_kb;
-  seq.list = nullptr;
-  seq.any = reinterpret_cast<const int32_t*>(P.q);
+  // ---- state of the current work item (wave-uniform)
+  int b = 0, h = 0, q0 = 0, a0 = 0, n_init = 0, n_local = 0, kind = KIND_DENSE;
+  float c_log2 = 0.0f, vfac = 1.0f;
   int64_t vs_base = 0;  // list row of a vertical_and_slash item
-  if constexpr (VS) {
-    // full tiles (no mask), then partial tiles, then gathered vertical tiles
-    // (ids n_kb + g), every entry with its key mask
-    vs_base = ((int64_t(b) * P.vs_slots + hd.slot) * P.n_qb + bq);
-    const int nf = load_uniform(P.vs_cnt + 2 * vs_base);
-    const int nt = load_uniform(P.vs_cnt + 2 * vs_base + 1);
-    vs_base *= P.vs_cap;
-    seq.list = P.vs_ids + vs_base;
-    seq.n_kb = P.n_kb + P.nv_pad / kBlock;
-    seq.set({0, nf, 0, 0, 0}, {nf, nt, 0, 0, 0}, 1);
-  } else if (kind == KIND_BLOCK) {
-    // canonical list: ascending causal ids, so the boundary ids come last
-    const int64_t base = (int64_t(b) * P.idx_slots + hd.slot) * P.n_qb + bq;
-    const int cnt = max(0, min(load_uniform(P.cnt + base), P.topk_max));
-    const int32_t* list = P.idx + base * P.topk_max;
-    int nf = cnt;
-    while (nf > 0 && load_uniform(list + nf - 1) >= Fe) --nf;
-    seq.list = list;
-    seq.set({0, nf, 0, 0, 0}, {nf, cnt, 0, 0, 0}, 1);
-  } else if (kind == KIND_STREAM) {
-    const int lo = min(max(a0 - n_local + 1, 0) >> 6, last_tile + 1);
-    const int nsink = min((min(max(n_init, 0), P.s_k) + 63) >> 6, lo);
-    const int sf = max(0, min(nsink, min(n_init >> 6, Fe)));  // sink tiles below n_init
-    int bf0 = a1 - n_local + 1;                                 // band tiles in every row's band
-    bf0 = bf0 <= 0 ? 0 : (bf0 + 63) >> 6;
-    bf0 = min(max(bf0, lo), last_tile + 1);
-    const int fb_hi = max(bf0, Fe);
-    // full sink, full band | partial sink, band tiles cut by the window
-    // start, diagonal / S_k boundary
-    seq.set({0, bf0, sf, lo, fb_hi}, {sf, fb_hi, nsink, bf0, last_tile + 1}, 2);
-  } else if (kind == KIND_FULL) {
-    const int ff = P.s_k >> 6;  // tiles whose keys are all below S_k
-    seq.set({0, ff, 0, 0, 0}, {ff, P.n_kb, 0, 0, 0}, 1);
-  } else {
-    seq.set({0, Fe, 0, 0, 0}, {Fe, last_tile + 1, 0, 0, 0}, 1);
-  }
+  TileSeq seq;
+  __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.kt), short(0), 0, 0x00020000);
+  __amdgpu_buffer_rsrc_t vrs = krs, gkrs = krs, gvrs = krs;
+  __amdgpu_buffer_rsrc_t qrs = krs;  // the item's 64 query rows (rows past S_q out of range)
+  int total = 0, mpos = 0, arow0 = 0, sink_hi = 0;
+  bool is_full = false, is_stream = false;
+  const int skm1 = P.s_k - 1;
 
-  const int64_t bk = int64_t(b) * (P.heads / P.kv_group) + kvh;
-  // staged V is V * 2^-vexp (stage_kernel); the output takes the 2^vexp back
-  const float vfac = __builtin_amdgcn_ldexpf(1.0f, load_uniform(P.vexp + bk));
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(P.kt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(P.vt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
-  // gathered vertical operands of a vertical_and_slash slot (tiles n_kb + g)
-  __amdgpu_buffer_rsrc_t gkrs = krs, gvrs = vrs;
-  if constexpr (VS) {
-    const int64_t gb = (int64_t(b) * P.vs_slots + hd.slot) * P.nv_pad * D;
-    gkrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.gkt + gb), short(0),
-                                             P.nv_pad * D * 2, 0x00020000);
-    gvrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.gvt + gb), short(0),
-                                             P.nv_pad * D * 2, 0x00020000);
-  }
+  auto init_item = [&](const int hh, const int bq) INLINE {
+    b = hh / P.heads;
+    h = hh - b * P.heads;
+    const int kvh = h / P.kv_group;
+    const int hd_slot = P.hd[h].slot;
+    kind = P.hd[h].kind;
+    q0 = bq * kBlock;
+    const int nrows = min(kBlock, P.s_q - q0);
+    const int off = P.s_k - P.s_q;
+    a0 = q0 + off;
+    const int a1 = q0 + nrows - 1 + off;
+    const int last_tile = min(a1 >> 6, P.n_kb - 1);
+    n_init = P.hd[h].p1;
+    n_local = P.hd[h].p2;
+    // tile t needs no mask for the causal / S_k bounds iff t < F
+    const int Fe = min(min((a0 + 1) >> 6, P.s_k >> 6), last_tile + 1);
+
+    seq.n_kb = P.n_kb;
+    seq.list = nullptr;
+    seq.any = reinterpret_cast<const int32_t*>(P.q);
+    if constexpr (VS) {
+      // full tiles (no mask), then partial tiles, then gathered vertical tiles
+      // (ids n_kb + g), every entry with its key mask
+      vs_base = ((int64_t(b) * P.vs_slots + hd_slot) * P.n_qb + bq);
+      const int nf = load_uniform(P.vs_cnt + 2 * vs_base);
+      const int nt = load_uniform(P.vs_cnt + 2 * vs_base + 1);
+      vs_base *= P.vs_cap;
+      seq.list = P.vs_ids + vs_base;
+      seq.n_kb = P.n_kb + P.nv_pad / kBlock;
+      seq.set({0, nf, 0, 0, 0}, {nf, nt, 0, 0, 0}, 1);
+    } else if (kind == KIND_BLOCK) {
+      // canonical list: ascending causal ids, so the boundary ids come last
+      const int64_t base = (int64_t(b) * P.idx_slots + hd_slot) * P.n_qb + bq;
+      const int cnt = max(0, min(load_uniform(P.cnt + base), P.topk_max));
+      const int32_t* list = P.idx + base * P.topk_max;
+      int nf = cnt;
+      while (nf > 0 && load_uniform(list + nf - 1) >= Fe) --nf;
+      seq.list = list;
+      seq.set({0, nf, 0, 0, 0}, {nf, cnt, 0, 0, 0}, 1);
+    } else if (kind == KIND_STREAM) {
+      const int lo = min(max(a0 - n_local + 1, 0) >> 6, last_tile + 1);
+      const int nsink = min((min(max(n_init, 0), P.s_k) + 63) >> 6, lo);
+      const int sf = max(0, min(nsink, min(n_init >> 6, Fe)));  // sink tiles below n_init
+      int bf0 = a1 - n_local + 1;                                 // band tiles in every row's band
+      bf0 = bf0 <= 0 ? 0 : (bf0 + 63) >> 6;
+      bf0 = min(max(bf0, lo), last_tile + 1);
+      const int fb_hi = max(bf0, Fe);
+      // full sink, full band | partial sink, band tiles cut by the window
+      // start, diagonal / S_k boundary
+      seq.set({0, bf0, sf, lo, fb_hi}, {sf, fb_hi, nsink, bf0, last_tile + 1}, 2);
+    } else if (kind == KIND_FULL) {
+      const int ff = P.s_k >> 6;  // tiles whose keys are all below S_k
+      seq.set({0, ff, 0, 0, 0}, {ff, P.n_kb, 0, 0, 0}, 1);
+    } else {
+      seq.set({0, Fe, 0, 0, 0}, {Fe, last_tile + 1, 0, 0, 0}, 1);
+    }
+    total = seq.total;
+    mpos = min(seq.mpos, total);
+
+    const int64_t bk = int64_t(b) * (P.heads / P.kv_group) + kvh;
+    // staged V is V * 2^-vexp (stage_kernel); the output takes the 2^vexp back
+    vfac = __builtin_amdgcn_ldexpf(1.0f, load_uniform(P.vexp + bk));
+    krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.kt + bk * P.s_pad * D),
+                                            short(0), P.s_pad * D * 2, 0x00020000);
+    vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.vt + bk * P.s_pad * D),
+                                            short(0), P.s_pad * D * 2, 0x00020000);
+    // gathered vertical operands of a vertical_and_slash slot (tiles n_kb + g)
+    if constexpr (VS) {
+      const int64_t gb = (int64_t(b) * P.vs_slots + hd_slot) * P.nv_pad * D;
+      gkrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.gkt + gb), short(0),
+                                               P.nv_pad * D * 2, 0x00020000);
+      gvrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.gvt + gb), short(0),
+                                               P.nv_pad * D * 2, 0x00020000);
+    }
+    // the item's rows of Q: row q0 + r at byte r * q_ss * 2; rows past S_q lie
+    // beyond the record count and load as zeros
+    qrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb +
+                              int64_t(h) * P.q_sh + int64_t(q0) * P.q_ss),
+        short(0), int(nrows * P.q_ss * 2), 0x00020000);
+    c_log2 = P.hd[h].scale_log2;
+    arow0 = a0 + lc;  // absolute position of this lane's row in group 0
+    is_full = kind == KIND_FULL;
+    is_stream = kind == KIND_STREAM;
+    sink_hi = is_stream ? n_init : 0;
+  };
 
   // ---- Q as the B operand: lane (lc, lr) of group g, k-step ks holds
-  // Q[q0 + 16g + lc][32ks + 8lr .. +7]
+  // Q[q0 + 16g + lc][32ks + 8lr .. +7]; rows past S_q are zero
   u32x4 qb[4][NKS];
-  {
-    const uint16_t* qbase =
-        reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + int64_t(h) * P.q_sh;
-    // rows past S_q load row S_q - 1 and are zeroed after the load, so the
-    // loads issue back to back with no branch between them
+  auto load_q = [&]() INLINE {
+    if constexpr (VS) {
+      // vertical_and_slash: plain loads of row min(row, S_q - 1), rows past
+      // S_q zeroed after the load (fewer registers in this variant)
+      const uint16_t* qbase =
+          reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + int64_t(h) * P.q_sh;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int row = q0 + 16 * g + lc;
-      const int64_t roff = int64_t(min(row, P.s_q - 1)) * P.q_ss;
+      for (int g = 0; g < 4; ++g) {
+        const int row = q0 + 16 * g + lc;
+        const int64_t roff = int64_t(min(row, P.s_q - 1)) * P.q_ss;
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) qb[g][ks] = load16(qbase + roff + 32 * ks + 8 * lr);
+        for (int ks = 0; ks < NKS; ++ks) qb[g][ks] = load16(qbase + roff + 32 * ks + 8 * lr);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+          qb[g][ks] = q0 + 16 * g + lc < P.s_q ? qb[g][ks] : zero_u32x4();
+      return;
     }
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t roff = uint32_t((16 * g + lc) * P.q_ss * 2 + 16 * lr);
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks)
-        qb[g][ks] = q0 + 16 * g + lc < P.s_q ? qb[g][ks] : zero_u32x4();
-  }
+        qb[g][ks] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(qrs, roff, 64 * ks, 0));
+    }
+  };
 
   // K and V chunk operands of tile t: wave w reads chunk 4t + w of the staged
   // operands, each MFMA operand as one contiguous 1 KB (lane l: 16 bytes).
+  // drop: the position lies past the item's last tile; the lane offset is
+  // then out of the buffer's range, so the load returns zeros without a
+  // memory access (the loop's instruction stream stays the same).
   const uint32_t lane_off = 16u * lane;
-  auto load_k = [&](int t, u32x4 (&kr)[NKS]) INLINE {
+  auto load_k = [&](int t, u32x4 (&kr)[NKS], bool drop) INLINE {
     __amdgpu_buffer_rsrc_t rs = krs;
     if constexpr (VS) {
       const bool gat = t >= P.n_kb;
@@ -530,12 +572,13 @@ void attn_kernel(AttnParams P) {
       t = gat ? t - P.n_kb : t;
     }
     const int soff = (4 * t + w) * S::CHUNK_BYTES;
+    const uint32_t vo = lane_off | (drop ? 0x80000000u : 0u);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
       kr[ks] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, soff + 1024 * ks, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, soff + 1024 * ks, 0));
   };
-  auto load_v = [&](int t, u32x4 (&vr)[NDB]) INLINE {
+  auto load_v = [&](int t, u32x4 (&vr)[NDB], bool drop) INLINE {
     __amdgpu_buffer_rsrc_t rs = vrs;
     if constexpr (VS) {
       const bool gat = t >= P.n_kb;
@@ -543,30 +586,32 @@ void attn_kernel(AttnParams P) {
       t = gat ? t - P.n_kb : t;
     }
     const int soff = (4 * t + w) * S::CHUNK_BYTES;
+    const uint32_t vo = lane_off | (drop ? 0x80000000u : 0u);
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
       vr[db] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, soff + 1024 * db, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, soff + 1024 * db, 0));
   };
 
   f32x16 o[NDB][2];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][rb][i] = 0.0f;
   // Running (biased) max per row in scaled log2 units, group layout (each
   // group's value in all 4 lane rows).  It only moves when some P would
   // exceed 2^15, so the O rescale is rare.
-  float m_g[4] = {-1e30f, -1e30f, -1e30f, -1e30f};
-  float l_g[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // per-lane partial row sums, group layout
-  const float c_log2 = hd.scale_log2;
-  const int arow0 = a0 + lc;  // absolute position of this lane's row in group 0
-  const int skm1 = P.s_k - 1;
-  const bool is_full = kind == KIND_FULL;
-  const bool is_stream = kind == KIND_STREAM;
-  const int sink_hi = is_stream ? n_init : 0;
+  float m_g[4];
+  float l_g[4];  // per-lane partial row sums, group layout
+  auto reset_acc = [&]() INLINE {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][rb][i] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      m_g[g] = -1e30f;
+      l_g[g] = 0.0f;
+    }
+  };
 
   // A step works on two 32-row halves h (groups 2h, 2h+1 = PV row block h) so
   // that the softmax of one half overlaps the MFMAs of the other.
@@ -687,15 +732,13 @@ void attn_kernel(AttnParams P) {
   // Pipeline over positions p: two register sets alternate (A: even p, B:
   // odd p).  The K operands of position p+2 are requested as soon as QK of p
   // has consumed the set, the V operands once PV has.  Loads are issued
-  // unconditionally (past the end they repeat the last tile), so every path
+  // unconditionally (past the item's end they are dropped), so every path
   // through the loop has the same loads in flight and the waits stay exact.
   // The tile number of p+3 is looked up one step before its loads.  Tiles
   // that need no mask and boundary tiles run as two separate loops (the mask
   // is a compile-time switch, so no branch splits a step's instruction
   // stream); each loop runs whole (A, B) pairs, with a single step before or
   // after it when its range starts or ends on the other set.
-  const int total = seq.total;
-  const int mpos = min(seq.mpos, total);
   u32x4 kA[NKS], vA[NDB], kB[NKS], vB[NDB];
   // key masks of vertical_and_slash tiles travel with their tile numbers
   // (looked up three positions ahead, like the tiles)
@@ -703,13 +746,21 @@ void attn_kernel(AttnParams P) {
     if constexpr (VS) return load_uniform(P.vs_masks + vs_base + max(min(q, total - 1), 0));
     return 0ull;
   };
-  int tA = seq.tile(0), tB = seq.tile(1);
-  uint64_t mA = mask_at(0), mB = mask_at(1), mn = mask_at(2);
-  load_k(tA, kA);
-  load_v(tA, vA);
-  load_k(tB, kB);
-  load_v(tB, vB);
-  int tn = seq.tile(2);
+  int tA = 0, tB = 0, tn = 0;
+  uint64_t mA = 0, mB = 0, mn = 0;
+  // the first two positions' operands of the item (and the third's tile)
+  auto start_tiles = [&]() INLINE {
+    tA = seq.tile(0);
+    tB = seq.tile(1);
+    mA = mask_at(0);
+    mB = mask_at(1);
+    mn = mask_at(2);
+    load_k(tA, kA, !VS && total < 1);
+    load_v(tA, vA, !VS && total < 1);
+    load_k(tB, kB, !VS && total < 2);
+    load_v(tB, vB, !VS && total < 2);
+    tn = seq.tile(2);
+  };
   // one step: QK of both halves; half 0's softmax under half 1's QK, half
   // 1's softmax under half 0's PV; K is reloaded once the rare path can no
   // longer need it
@@ -718,6 +769,9 @@ void attn_kernel(AttnParams P) {
     constexpr bool MT = decltype(masked)::value;
     const int tnn = seq.tile(p + 3);
     const uint64_t mnn = mask_at(p + 3);
+    // (vertical_and_slash items walk long lists: the per-step test costs
+    // more there than the two loads it saves per item)
+    const bool drop = !VS && p + 2 >= total;
     f32x4 sa[2], sb[2];
     float pa[2], pb[2];
     qk_half(kr, 0, sa);
@@ -727,9 +781,9 @@ void attn_kernel(AttnParams P) {
     pv_half(sa, pa, 0, vr);
     if constexpr (MT) mask_half(sb, 1, tcur, mcur);
     if (exp_half(sb, 1, pb)) rescale_half(kr, sb, pb, 1, tcur, mcur, MT);
-    load_k(tn, kr);
+    load_k(tn, kr, drop);
     pv_half(sb, pb, 1, vr);
-    load_v(tn, vr);
+    load_v(tn, vr, drop);
     tcur = tn;
     tn = tnn;
     mcur = mn;
@@ -744,85 +798,91 @@ void attn_kernel(AttnParams P) {
     }
     if (p < p1) step(masked, kA, vA, tA, mA, p);
   };
-  run(std::integral_constant<bool, false>(), 0, mpos);
-  run(std::integral_constant<bool, true>(), mpos, total);
+  auto body = [&]() INLINE {
+    run(std::integral_constant<bool, false>(), 0, mpos);
+    run(std::integral_constant<bool, true>(), mpos, total);
+  };
 
   // ---- merge the four chunk partials of each row; wave 0 writes the rows
-  // block layout: lane rows 1, 3 hold group 2rb+1.  Chosen by an exact blend
+  // of the item (batch ib, head ih, first row iq0; iv = 2^vexp of its head).
+  // Block layout: lane rows 1, 3 hold group 2rb+1.  Chosen by an exact blend
   // (the maxima are finite) rather than a select, which the compiler turns
   // into a lane-indexed load from a private copy of m_g.
-  float m_b[2], l_b[2];
-  const float odd = float(lr & 1);
+  auto merge_store = [&](const int ib, const int ih, const int iq0, const float iv) INLINE {
+    float m_b[2], l_b[2];
+    const float odd = float(lr & 1);
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-    m_b[rb] = __builtin_fmaf(odd, m_g[2 * rb + 1], (1.0f - odd) * m_g[2 * rb]);
-  lanes_to_blocks(reduce_rows(l_g[0], l_g[1], l_g[2], l_g[3], RowSum()), l_b);
-  if (w > 0) {
-    float* slot = lds + (w - 1) * S::SLOT;
+    for (int rb = 0; rb < 2; ++rb)
+      m_b[rb] = __builtin_fmaf(odd, m_g[2 * rb + 1], (1.0f - odd) * m_g[2 * rb]);
+    lanes_to_blocks(reduce_rows(l_g[0], l_g[1], l_g[2], l_g[3], RowSum()), l_b);
+    if (w > 0) {
+      float* slot = lds + (w - 1) * S::SLOT;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+      for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+        for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) slot[((db * 2 + rb) * 16 + i) * 64 + lane] = o[db][rb][i];
+          for (int i = 0; i < 16; ++i) slot[((db * 2 + rb) * 16 + i) * 64 + lane] = o[db][rb][i];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      slot[(S::NO + rb) * 64 + lane] = m_b[rb];
-      slot[(S::NO + 2 + rb) * 64 + lane] = l_b[rb];
+      for (int rb = 0; rb < 2; ++rb) {
+        slot[(S::NO + rb) * 64 + lane] = m_b[rb];
+        slot[(S::NO + 2 + rb) * 64 + lane] = l_b[rb];
+      }
     }
-  }
-  __syncthreads();
-  if (w == 0) {
+    __syncthreads();
+    if (w == 0) {
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    float mw[4], lw[4];
-    mw[0] = m_b[rb];
-    lw[0] = l_b[rb];
+      for (int rb = 0; rb < 2; ++rb) {
+        float mw[4], lw[4];
+        mw[0] = m_b[rb];
+        lw[0] = l_b[rb];
 #pragma unroll
-    for (int v = 1; v < 4; ++v) {
-      mw[v] = lds[(v - 1) * S::SLOT + (S::NO + rb) * 64 + lane];
-      lw[v] = lds[(v - 1) * S::SLOT + (S::NO + 2 + rb) * 64 + lane];
-    }
-    const float mt = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
-    float f[4];
-    float lt = 0.0f;
+        for (int v = 1; v < 4; ++v) {
+          mw[v] = lds[(v - 1) * S::SLOT + (S::NO + rb) * 64 + lane];
+          lw[v] = lds[(v - 1) * S::SLOT + (S::NO + 2 + rb) * 64 + lane];
+        }
+        const float mt = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+        float f[4];
+        float lt = 0.0f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      f[v] = __builtin_amdgcn_exp2f(mw[v] - mt);
-      lt += lw[v] * f[v];
-    }
-    const float inv = lt > 0.0f ? vfac / lt : 0.0f;
+        for (int v = 0; v < 4; ++v) {
+          f[v] = __builtin_amdgcn_exp2f(mw[v] - mt);
+          lt += lw[v] * f[v];
+        }
+        const float inv = lt > 0.0f ? iv / lt : 0.0f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) f[v] *= inv;
+        for (int v = 0; v < 4; ++v) f[v] *= inv;
 
-    const int row = q0 + 32 * rb + (lane & 31);
-    if (row < P.s_q) {
-      const int64_t obase = b * P.o_sb + int64_t(h) * P.o_sh + int64_t(row) * P.o_ss;
+        const int row = iq0 + 32 * rb + (lane & 31);
+        if (row < P.s_q) {
+          const int64_t obase = ib * P.o_sb + int64_t(ih) * P.o_sh + int64_t(row) * P.o_ss;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
+          for (int db = 0; db < NDB; ++db) {
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          float v4[4];
+            for (int qd = 0; qd < 4; ++qd) {
+              float v4[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = 4 * qd + e;
-            const int r = (db * 2 + rb) * 16 + i;
-            float acc = o[db][rb][i] * f[0];
+              for (int e = 0; e < 4; ++e) {
+                const int i = 4 * qd + e;
+                const int r = (db * 2 + rb) * 16 + i;
+                float acc = o[db][rb][i] * f[0];
 #pragma unroll
-            for (int v = 1; v < 4; ++v) acc += lds[(v - 1) * S::SLOT + r * 64 + lane] * f[v];
-            v4[e] = acc;
-          }
-          const int d = 32 * db + 8 * qd + 4 * (lane >> 5);
-          if constexpr (OUT_F32) {
-            store_out4<float>(reinterpret_cast<float*>(P.o) + obase + d, v4[0], v4[1], v4[2], v4[3]);
-          } else {
-            store_out4_16<T>(reinterpret_cast<uint16_t*>(P.o) + obase + d, v4[0], v4[1], v4[2], v4[3]);
+                for (int v = 1; v < 4; ++v) acc += lds[(v - 1) * S::SLOT + r * 64 + lane] * f[v];
+                v4[e] = acc;
+              }
+              const int d = 32 * db + 8 * qd + 4 * (lane >> 5);
+              if constexpr (OUT_F32) {
+                store_out4<float>(reinterpret_cast<float*>(P.o) + obase + d, v4[0], v4[1], v4[2],
+                                  v4[3]);
+              } else {
+                store_out4_16<T>(reinterpret_cast<uint16_t*>(P.o) + obase + d, v4[0], v4[1],
+                                 v4[2], v4[3]);
+              }
+            }
           }
         }
       }
-    }
-  }
-  }  // w == 0
+    }  // w == 0
   };
 
   if constexpr (VS) {
@@ -833,21 +893,36 @@ void attn_kernel(AttnParams P) {
       __syncthreads();
       if (g < 0) break;
       const int hl = g / P.n_qb;
-      item_body(int(P.head_order[hl]), P.n_qb - 1 - (g - hl * P.n_qb));
+      init_item(int(P.head_order[hl]), P.n_qb - 1 - (g - hl * P.n_qb));
+      load_q();
+      reset_acc();
+      start_tiles();
+      body();
+      merge_store(b, h, q0, vfac);
     }
-  } else if (P.n_hl) {
-    const int r = int(blockIdx.x) >> 3;
-    if (r >= P.xcd_count[xcd]) return;
-    const int g = P.xcd_start[xcd] + r;
-    const int hl = g / P.n_qb;
-    item_body(int(P.head_order[hl]), P.n_qb - 1 - (g - hl * P.n_qb));
   } else {
-    // plain order: every (batch, head) pair; the host lists no item of a
-    // skipped head in the other modes
-    const int BH = P.batch * P.heads;
-    const int hh = int(blockIdx.x) % BH;
-    if (P.hd[hh % P.heads].kind == KIND_SKIP) return;
-    item_body(hh, P.n_qb - 1 - int(blockIdx.x) / BH);
+    int hh, bq;
+    if (P.n_hl) {
+      const int r = int(blockIdx.x) >> 3;
+      if (r >= P.xcd_count[xcd]) return;
+      const int g = P.xcd_start[xcd] + r;
+      const int hl = g / P.n_qb;
+      hh = int(P.head_order[hl]);
+      bq = P.n_qb - 1 - (g - hl * P.n_qb);
+    } else {
+      // plain order: every (batch, head) pair; the host lists no item of a
+      // skipped head in the other modes
+      const int BH = P.batch * P.heads;
+      hh = int(blockIdx.x) % BH;
+      if (P.hd[hh % P.heads].kind == KIND_SKIP) return;
+      bq = P.n_qb - 1 - int(blockIdx.x) / BH;
+    }
+    init_item(hh, bq);
+    load_q();
+    reset_acc();
+    start_tiles();
+    body();
+    merge_store(b, h, q0, vfac);
   }
 }
 

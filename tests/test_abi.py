@@ -127,6 +127,8 @@ SHAPE = [1, 4, 256, 96]
         (lambda a: a.__setitem__("k", t4(SHAPE, strides=[4 * 256 * 96, 256 * 96, 96, 2])), _abi.MSA_E_ALIGN),
         (lambda a: a.__setitem__("q", t4(SHAPE, strides=[4 * 256 * 100, 256 * 100, 100, 1])), _abi.MSA_E_ALIGN),
         (lambda a: a.__setitem__("q", t4(SHAPE, data=FAKE + 2)), _abi.MSA_E_ALIGN),
+        (lambda a: a.__setitem__("q", t4(SHAPE, strides=[4 * 256 << 24, 256 << 24, 1 << 24, 1])),
+         _abi.MSA_E_ALIGN),
         (lambda a: a.__setitem__("q", t4([1, 4, 512, 96])) or a.__setitem__("o", t4([1, 4, 512, 96])), _abi.MSA_E_SEQ),
         (lambda a: a.__setitem__("n", 3), _abi.MSA_E_HEADS),
         (lambda a: a.__setitem__("hd", heads(4, kind=7)), _abi.MSA_E_HEADS),
