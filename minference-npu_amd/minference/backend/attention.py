@@ -13,7 +13,7 @@ from typing import Optional
 import torch
 
 from .. import _abi
-from ..ops.common import check_bnsd, check_supported, dense_scale, head_chunks, kernel_view, make_out
+from ..ops.common import check_bnsd, check_supported, dense_scale, head_chunks, padded_call
 
 __all__ = ["dense_attention", "prefill_dense", "decode_dense"]
 
@@ -36,14 +36,15 @@ def dense_attention(
     """
     check_bnsd(q, k, v)
     check_supported(q, k, v, allow_longer_q=not causal)
-    q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
-    result = make_out(q, out)
     s = dense_scale(q.shape[-1]) if scale is None else float(scale)
     kind = _abi.MSA_KIND_DENSE if causal else _abi.MSA_KIND_FULL
-    for h0, h1 in head_chunks(q.shape[1]):
-        heads = [(kind, 0, 0, -1, s)] * (h1 - h0)
-        _abi.layer_attention(q[:, h0:h1], k[:, h0:h1], v[:, h0:h1], result[:, h0:h1], heads)
-    return result
+
+    def run(q, k, v, result):
+        for h0, h1 in head_chunks(q.shape[1]):
+            heads = [(kind, 0, 0, -1, s)] * (h1 - h0)
+            _abi.layer_attention(q[:, h0:h1], k[:, h0:h1], v[:, h0:h1], result[:, h0:h1], heads)
+
+    return padded_call(q, k, v, out, run)
 
 
 def prefill_dense(q, k, v, *, scale: Optional[float] = None, causal: bool = True):
@@ -77,8 +78,6 @@ def decode_dense(
         raise NotImplementedError("decode_dense takes one query row; use dense_attention for "
                                   "q_len > 1")
     check_supported(q, k_cache, v_cache)
-    q, k_cache, v_cache = kernel_view(q), kernel_view(k_cache), kernel_view(v_cache)
-    result = make_out(q, out)
     s = dense_scale(q.shape[-1]) if scale is None else float(scale)
-    _abi.decode_attention(q, k_cache, v_cache, result, s)
-    return result
+    return padded_call(q, k_cache, v_cache, out,
+                       lambda q, k, v, r: _abi.decode_attention(q, k, v, r, s))

@@ -26,7 +26,7 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import torch
 
 from .. import _abi
-from ..ops.common import dense_scale, sparse_scale
+from ..ops.common import dense_scale, require_kernel_head_dim, sparse_scale
 from ..ops.rope import apply_rotary_pos_emb as apply_rotary_pos_emb_gpu, rope_supported
 from ..ops.vertical_slash_kernel import vs_sizes
 
@@ -178,6 +178,7 @@ def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan:
     out any [B, H, S_q, D] view with D contiguous (bf16/fp16 or fp32).
     """
     _abi.require_device(q, k, v)
+    require_kernel_head_dim(q.shape[-1], "the patched attention forward")
     B, H, S_q, _ = q.shape
     if H > _abi.MSA_MAX_HEADS:
         raise NotImplementedError(

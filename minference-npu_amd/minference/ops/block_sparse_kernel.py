@@ -18,7 +18,8 @@ from typing import Optional, Tuple
 import torch
 
 from .. import _abi
-from .common import check_bnsd, check_supported, head_chunks, kernel_view, make_out, sparse_scale
+from .common import (check_bnsd, check_supported, head_chunks, kernel_head_dim, kernel_view,
+                     pad_head_dim, padded_call, sparse_scale)
 
 __all__ = [
     "block_sparse_attention",
@@ -44,15 +45,15 @@ def select_flags(force_first: bool = False, force_diag: bool = False) -> int:
             | (_abi.MSA_SELECT_FORCE_DIAG if force_diag else 0))
 
 
-def _estimate(q: torch.Tensor, k: torch.Tensor, topk: int, flags: int = 0):
-    """Run the estimator for every head of q.
+def _estimate(q: torch.Tensor, k: torch.Tensor, topk: int, scale: float, flags: int = 0):
+    """Run the estimator for every head of q (kernel views at the kernel
+    head dim; ``scale`` from the original head_dim).
 
     Returns a list of (h0, h1, idx, cnt) per head chunk of at most
     MSA_MAX_HEADS heads, idx/cnt int32 contiguous [B, h1-h0, n_qb(, topk)].
     """
     B, H, S_q, _ = q.shape
     n_qb = math.ceil(S_q / _abi.MSA_BLOCK)
-    scale = sparse_scale(q.shape[-1])
     chunks = []
     for h0, h1 in head_chunks(H):
         n = h1 - h0
@@ -93,10 +94,12 @@ def select_block_sparse_topk_indices(
     check_bnsd(q, k)
     check_supported(q, k)
     _check_block_size(block_size)
-    q, k = kernel_view(q), kernel_view(k)
+    scale = sparse_scale(q.shape[-1])
+    dk = kernel_head_dim(q.shape[-1])
+    q, k = kernel_view(pad_head_dim(q, dk)), kernel_view(pad_head_dim(k, dk))
     n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
     topk = min(max(1, int(topk_blocks)), n_kb)
-    chunks = _estimate(q, k, topk, select_flags(force_first, force_diag))
+    chunks = _estimate(q, k, topk, scale, select_flags(force_first, force_diag))
     idx = torch.cat([c[2] for c in chunks], dim=1).long()
     if return_counts:
         return idx, torch.cat([c[3] for c in chunks], dim=1).long()
@@ -130,15 +133,14 @@ def block_sparse_attention_with_indices(
             "block_indices shape must be [B,H,n_q_blocks,topk_blocks]; "
             f"got {tuple(block_indices.shape)} for q={tuple(q.shape)} block_size={block_size}"
         )
-    q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
     n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
     idx, cnt = canonical_block_lists(block_indices.to(q.device), n_kb)
     topk = idx.shape[-1]
     chunks = []
     for h0, h1 in head_chunks(H):
         chunks.append((h0, h1, idx[:, h0:h1].contiguous(), cnt[:, h0:h1].contiguous()))
-    result = make_out(q, out)
-    return _run(q, k, v, chunks, topk, result)
+    scale = sparse_scale(q.shape[-1])
+    return padded_call(q, k, v, out, lambda q, k, v, r: _run(q, k, v, chunks, topk, scale, r))
 
 
 def canonical_block_lists(block_indices: torch.Tensor, n_kb: int):
@@ -161,8 +163,7 @@ def canonical_block_lists(block_indices: torch.Tensor, n_kb: int):
     return ids.to(torch.int32).contiguous(), cnt.to(torch.int32).contiguous()
 
 
-def _run(q, k, v, chunks, topk, result):
-    scale = sparse_scale(q.shape[-1])
+def _run(q, k, v, chunks, topk, scale, result):
     for h0, h1, idx, cnt in chunks:
         n = h1 - h0
         heads = [(_abi.MSA_KIND_BLOCK, topk, 0, s, scale) for s in range(n)]
@@ -201,9 +202,12 @@ def block_sparse_attention(
     check_bnsd(q, k, v)
     check_supported(q, k, v)
     _check_block_size(block_size)
-    q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
     n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
     topk = min(max(1, int(topk_blocks)), n_kb)
-    chunks = _estimate(q, k, topk, select_flags(force_first, force_diag))
-    result = make_out(q, out)
-    return _run(q, k, v, chunks, topk, result)
+    scale = sparse_scale(q.shape[-1])
+    flags = select_flags(force_first, force_diag)
+
+    def run(q, k, v, result):
+        _run(q, k, v, _estimate(q, k, topk, scale, flags), topk, scale, result)
+
+    return padded_call(q, k, v, out, run)

@@ -13,6 +13,8 @@ from .. import _abi
 # (minference/ops/streaming_kernel_npu.py:70-86; block_sparse_kernel_npu.py:56, 95-101).
 ALLOWED_HEAD_DIMS = (16, 32, 64, 128, 256, 512)
 
+# Head dims the HIP kernels are built for; the ops take any head_dim up to the
+# largest of them by zero-padding q, k and v to the next one.
 SUPPORTED_HEAD_DIMS = (64, 96, 128)
 SUPPORTED_DTYPES = (torch.bfloat16, torch.float16)
 
@@ -51,6 +53,57 @@ def check_bnsd(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor] = Non
         assert v.shape == k.shape, f"v shape {tuple(v.shape)} != k shape {tuple(k.shape)}"
 
 
+def kernel_head_dim(d: int) -> int:
+    """The head dim the kernels run at for head_dim ``d``: d itself when the
+    kernels are built for it, else the next built size.  The ops pad q, k and
+    v with zeros to it (no dot product changes; the extra output columns are
+    dropped), as the reference pads to its allowed sizes before its kernels
+    (streaming_kernel_npu.py:377-381, block_sparse_kernel_npu.py:651-656).
+    The scale still follows the reference's rule for the original d."""
+    for cand in SUPPORTED_HEAD_DIMS:
+        if cand >= d:
+            return cand
+    raise NotImplementedError(
+        f"head_dim={d} is not supported by the MI355X kernels (at most "
+        f"{SUPPORTED_HEAD_DIMS[-1]}; the reference pads up to {ALLOWED_HEAD_DIMS[-1]})"
+    )
+
+
+def require_kernel_head_dim(d: int, what: str) -> None:
+    """Paths that do not pad (vertical_and_slash, whose estimator divides by
+    the kernel's sqrt(D); the patched model forward) take the built head
+    dims only."""
+    if d not in SUPPORTED_HEAD_DIMS:
+        raise NotImplementedError(
+            f"{what} runs at head_dim {SUPPORTED_HEAD_DIMS} only, got {d}"
+        )
+
+
+def pad_head_dim(t: torch.Tensor, dk: int) -> torch.Tensor:
+    """t with its last dimension zero-padded to dk (t itself when it is dk)."""
+    if t.shape[-1] == dk:
+        return t
+    return torch.nn.functional.pad(t, (0, dk - t.shape[-1]))
+
+
+def padded_call(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[torch.Tensor],
+                fn) -> torch.Tensor:
+    """Run ``fn(q, k, v, result)`` on views the kernels read in place, at the
+    kernel head dim; returns the op's output (``out`` when given) with the
+    original head_dim."""
+    d = q.shape[-1]
+    dk = kernel_head_dim(d)
+    result = make_out(q, out)
+    if dk == d:
+        fn(kernel_view(q), kernel_view(k), kernel_view(v), result)
+        return result
+    qp, kp, vp = pad_head_dim(q, dk), pad_head_dim(k, dk), pad_head_dim(v, dk)
+    tmp = torch.empty(qp.shape, dtype=result.dtype, device=q.device)
+    fn(qp, kp, vp, tmp)
+    result.copy_(tmp[..., :d])
+    return result
+
+
 def check_supported(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor] = None,
                     allow_longer_q: bool = False) -> None:
     tensors = (q, k) if v is None else (q, k, v)
@@ -62,11 +115,9 @@ def check_supported(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor] 
             )
     if len({t.dtype for t in tensors}) != 1:
         raise ValueError("q, k and v must share one dtype")
-    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
-        raise NotImplementedError(
-            f"head_dim={q.shape[-1]} is not supported by the MI355X kernels "
-            f"(supported: {SUPPORTED_HEAD_DIMS})"
-        )
+    if q.shape[-1] < 1:
+        raise ValueError("head_dim must be positive")
+    kernel_head_dim(q.shape[-1])  # NotImplementedError beyond the largest built size
     if q.shape[2] > k.shape[2] and not allow_longer_q:
         raise ValueError(
             f"prefill attention requires S_q <= S_k, got S_q={q.shape[2]}, S_k={k.shape[2]}"

@@ -14,7 +14,7 @@ from typing import Optional
 import torch
 
 from .. import _abi
-from .common import check_bnsd, check_supported, head_chunks, kernel_view, make_out, sparse_scale
+from .common import check_bnsd, check_supported, head_chunks, padded_call, sparse_scale
 
 __all__ = ["streaming_forward"]
 
@@ -40,16 +40,18 @@ def streaming_forward(
     Query i (absolute position a = S_k - S_q + i) sees key j iff
     j <= a and (j > a - n_local or j < n_init).  When S_k <= n_local this is
     causal dense attention, which is the reference's short circuit (:385-390).
-    The softmax scale is (padded head_dim)**-0.5 as in the reference.
+    The softmax scale is (padded head_dim)**-0.5 as in the reference; a
+    head_dim the kernels are not built for runs zero-padded to the next one.
     """
     check_bnsd(q, k, v)
     check_supported(q, k, v)
-    q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
-    result = make_out(q, out)
     scale = sparse_scale(q.shape[-1])
-    for h0, h1 in head_chunks(q.shape[1]):
-        heads = [(_abi.MSA_KIND_STREAM, int(n_init), int(n_local), -1, scale)] * (h1 - h0)
-        _abi.layer_attention(
-            q[:, h0:h1], k[:, h0:h1], v[:, h0:h1], result[:, h0:h1], heads
-        )
-    return result
+
+    def run(q, k, v, result):
+        for h0, h1 in head_chunks(q.shape[1]):
+            heads = [(_abi.MSA_KIND_STREAM, int(n_init), int(n_local), -1, scale)] * (h1 - h0)
+            _abi.layer_attention(
+                q[:, h0:h1], k[:, h0:h1], v[:, h0:h1], result[:, h0:h1], heads
+            )
+
+    return padded_call(q, k, v, out, run)

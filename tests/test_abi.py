@@ -320,3 +320,30 @@ def test_skip_kind_is_exempt_from_head_checks():
     hd[2].kind = _abi.MSA_KIND_STREAM
     assert attn(q, kv, kv, q, hd, 4, wsb=100) == _abi.MSA_E_SEQ
 
+
+
+def test_head_dim_padding_helpers():
+    """Head dims up to 128 run at the next built size (zero padding); the
+    scale keeps the reference's rule for the original head_dim."""
+    import torch
+
+    from minference.ops import common as C
+
+    assert [C.kernel_head_dim(d) for d in (1, 40, 64, 65, 80, 96, 97, 112, 128)] == \
+        [64, 64, 64, 96, 96, 96, 128, 128, 128]
+    with pytest.raises(NotImplementedError):
+        C.kernel_head_dim(129)
+    # (next allowed of 16/32/64/128/256/512)^-0.5, not of the padded size
+    assert C.sparse_scale(24) == 32 ** -0.5 and C.sparse_scale(80) == 128 ** -0.5
+    t = torch.arange(2 * 3 * 5 * 40, dtype=torch.float32).reshape(2, 3, 5, 40)
+    p = C.pad_head_dim(t, 64)
+    assert p.shape == (2, 3, 5, 64) and torch.equal(p[..., :40], t) and not p[..., 40:].any()
+    assert C.pad_head_dim(t, 40) is t
+    seen = {}
+
+    def fn(q, k, v, r):
+        seen["d"] = q.shape[-1]
+        r.copy_(q + 1)
+
+    out = C.padded_call(t, t, t, None, fn)
+    assert seen["d"] == 64 and out.shape == t.shape and torch.equal(out, t + 1)
