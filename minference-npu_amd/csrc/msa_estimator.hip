@@ -108,15 +108,15 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams P) {
 }
 
 // ---------------------------------------------------------------------------
-// Scoring + top-k: one workgroup of 4 waves per (R consecutive q blocks, sb),
-// heaviest (last) groups first.  Each thread scores whole candidate columns
-// for all R rows: fp64 FMAs in d order, the pooled Q values (uniform over
-// the wave) coming through the scalar cache as SGPR operands, the pooled K
-// column from global memory.  Then each wave selects the top-k of its rows:
-// the k-th largest order key by a bitwise search (keys of KPL x 64
-// candidates in registers; KPL = 0 reads them from LDS), stopping as soon as
-// a threshold splits off exactly k keys, then an ordered compaction, equal
-// keys going to the lower id.
+// Scoring + top-k: one workgroup of 4 waves per (R = 16 consecutive q blocks,
+// sb).  Scores: v_mfma_f64_16x16x4f64 tiles of the 16 rows x 16 candidates,
+// pooled Q (fp64) as the A operand held in registers, pooled K columns loaded
+// coalesced; two independent accumulation chains per wave; every causal
+// score goes to the workspace.  Then each wave selects the top-k of its four
+// rows: the k-th largest order key by a bitwise search (keys of KPL x 64
+// candidates in registers; KPL = 0 reads them from the workspace), stopping
+// as soon as a threshold splits off exactly k keys, then an ordered
+// compaction, equal keys going to the lower id.
 // ---------------------------------------------------------------------------
 __device__ inline uint32_t order_key(float f) {
   f = f + 0.0f;  // -0 -> +0 so that equal scores compare equal
@@ -175,7 +175,12 @@ __global__ __launch_bounds__(256) void score_topk_kernel(ScoreParams P) {
 
   const int sb = blockIdx.y;
   const int n_groups = (P.n_qb + R - 1) / R;
-  const int bq0 = (n_groups - 1 - int(blockIdx.x)) * R;
+  // heaviest (last) groups first; every other set of four slots takes the
+  // groups in the mirrored order, so that the workgroups dispatched to one CU
+  // (ids 256 apart: the same group of four consecutive slots) mix heavy and
+  // light groups instead of four copies of one
+  const int gx = ((sb >> 2) & 1) ? n_groups - 1 - int(blockIdx.x) : int(blockIdx.x);
+  const int bq0 = (n_groups - 1 - gx) * R;
   const int nrows = min(R, P.n_qb - bq0);
   const int ncand = min(bq0 + nrows, P.n_kb);  // causal candidates of the last row
   const int t = threadIdx.x;
