@@ -3,12 +3,10 @@
 
 A step = the whole sparse attention of one layer, all heads, inputs resident
 in HBM, launched as the patched forward launches it (launch_block_layer): the
-block estimator (block top-k for the block_sparse heads) on a side stream
-beside the K/V staging launch; the attention launch of the stream_llm /
-dense heads as soon as the staging is done; then, after the estimator, the
-attention launch of the block heads (one attention launch after both when
-every head is block_sparse).  QKV projection, RoPE and o_proj are outside the
-step (the reference's per-layer attention, BASELINE.json metric).
+block estimator's pooling pass, then its selection pass (block top-k for the
+block_sparse heads) on a side stream beside the K/V staging launch, then one
+attention launch of all heads.  QKV projection, RoPE and o_proj are outside
+the step (the reference's per-layer attention, BASELINE.json metric).
 
 Default workload ("headline"): S = 65536, 32 heads x 96, bf16, every head
 sparse, 16 stream_llm(n_init 128, n_local 4096) + 16 block_sparse(top-100)
@@ -326,16 +324,15 @@ def main():
     sel_flags = ((_abi.MSA_SELECT_FORCE_FIRST if force_first else 0)
                  | (_abi.MSA_SELECT_FORCE_DIAG if force_diag else 0))
 
-    names = ("start", "est0", "est1", "stage0", "stage1", "attn0", "attn0_end", "attn1",
-             "attn1_end")
+    names = ("start", "est0", "est1", "stage0", "stage1", "attn0", "attn0_end")
     ev = [{n: torch.cuda.Event(enable_timing=True) for n in names} for _ in range(args.steps)]
     if not n_slots:
         idx = cnt = None
 
     def step(e=None):
-        # the product's schedule (launch_block_layer): the estimator on the
-        # side stream beside the staging; the heads that need no block ids
-        # start when the staging is done
+        # the product's schedule (launch_block_layer): pooling, then the
+        # selection on the side stream beside the staging, then one attention
+        # launch of all heads
         if n_slots:
             launch_block_layer(q, k, v, plan, out, idx, cnt, ws_att, ws_est, sel_flags,
                                mark=(lambda n, st: e[n].record(st)) if e else None)
@@ -365,15 +362,13 @@ def main():
     for i in range(args.steps):
         step(ev[i])
     torch.cuda.synchronize()
-    split = bool(n_slots) and len(plan.block_heads) < H
 
     def avg(a, b):
         return sum(e[a].elapsed_time(e[b]) for e in ev) / args.steps
 
     t_est = avg("est0", "est1") if n_slots else 0.0
     t_stage = avg("stage0", "stage1")
-    t_launch = [avg("attn0", "attn0_end")] + ([avg("attn1", "attn1_end")] if split else [])
-    t_attn = sum(t_launch)
+    t_attn = avg("attn0", "attn0_end")
     t_pre = avg("start", "attn0")
 
     flop_stream = n_stream * stream_pairs(S, n_init, n_local) * 4 * D
@@ -415,9 +410,8 @@ def main():
         "algorithmic_flop": flop,
         "kernels_ms": {"estimator": round(t_est, 4), "stage_kv": round(t_stage, 4),
                        "attention": round(t_attn, 4)},
-        "attention_launches_ms": [round(t, 4) for t in t_launch],
-        "schedule": ("estimator beside the staging; other heads, then block heads"
-                     if split else "estimator beside the staging" if n_slots else "sequential"),
+        "schedule": ("block pooling; selection beside the staging; one attention launch"
+                     if n_slots else "staging; one attention launch"),
         "ms_before_first_attention": round(t_pre, 4),
         "estimator_gbps": round(est_bytes / (t_est * 1e-3) / 1e9, 1) if n_slots else None,
         "roofline": {

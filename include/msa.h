@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MSA_ABI_VERSION 8
+#define MSA_ABI_VERSION 9
 
 /* status codes (negative: validation, nothing launched) */
 #define MSA_OK 0
@@ -60,8 +60,10 @@ extern "C" {
 #define MSA_KIND_SKIP 5   /* left to another launch: rows neither read nor written */
 
 /* msa_block_estimate_ex flags */
-#define MSA_SELECT_FORCE_FIRST 1 /* block 0 always selected */
-#define MSA_SELECT_FORCE_DIAG 2  /* the query block's own block always selected */
+#define MSA_SELECT_FORCE_FIRST 1   /* block 0 always selected */
+#define MSA_SELECT_FORCE_DIAG 2    /* the query block's own block always selected */
+#define MSA_ESTIMATE_POOL_ONLY 4   /* phase 1 only: pooled Q and K into the workspace */
+#define MSA_ESTIMATE_SELECT_ONLY 8 /* phase 2 only: scores and top-k from that workspace */
 
 #define MSA_VS_MAX_SEQ 131072 /* longest S of a vertical_and_slash head */
 
@@ -136,8 +138,14 @@ int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k,
  * selection, inside the top-k: forced ids rank above every scored id, and
  * between the two the lower id wins (top-k 1 with both flags keeps block 0).
  * The reference selector has no such option; it serves selection rules that
- * always keep the diagonal and first block.  Same counterpart as
- * msa_block_estimate
+ * always keep the diagonal and first block.
+ * The estimator is two passes (pooling, then scoring + top-k); POOL_ONLY and
+ * SELECT_ONLY (one of them at a time) launch one pass, so a caller can run
+ * the pooling first and the selection beside other work.  A SELECT_ONLY call
+ * reads the pooled Q and K that a POOL_ONLY call with the same arguments left
+ * in the same workspace, and must be ordered after it (same stream, or an
+ * event); a POOL_ONLY call leaves idx and cnt untouched.  Same counterpart
+ * as msa_block_estimate
  * (minference/ops/block_sparse_kernel_npu.py:230-263). */
 int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k,
                           const int32_t* slot_heads, const int32_t* slot_topk,

@@ -118,7 +118,12 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
                           int32_t topk_max, float score_scale, int32_t flags, int32_t* idx,
                           int32_t* cnt, void* workspace, size_t workspace_bytes,
                           msa_stream_t stream) {
-  if ((flags & ~(MSA_SELECT_FORCE_FIRST | MSA_SELECT_FORCE_DIAG)) != 0) return MSA_E_TOPK;
+  constexpr int32_t kKnown = MSA_SELECT_FORCE_FIRST | MSA_SELECT_FORCE_DIAG |
+                              MSA_ESTIMATE_POOL_ONLY | MSA_ESTIMATE_SELECT_ONLY;
+  if ((flags & ~kKnown) != 0) return MSA_E_TOPK;
+  const int32_t phase = flags & (MSA_ESTIMATE_POOL_ONLY | MSA_ESTIMATE_SELECT_ONLY);
+  if (phase == (MSA_ESTIMATE_POOL_ONLY | MSA_ESTIMATE_SELECT_ONLY)) return MSA_E_TOPK;
+  flags &= MSA_SELECT_FORCE_FIRST | MSA_SELECT_FORCE_DIAG;
   int st = check_qk(q, k);
   if (st != MSA_OK) return st;
   if (block != MSA_BLOCK) return MSA_E_BLOCK;
@@ -164,8 +169,10 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
   pp.q_pool = q_pool;
   pp.k_poolT = k_poolT;
   for (int s = 0; s < n_slots; ++s) pp.slot_heads[s] = int16_t(slot_heads[s]);
-  hipError_t e = launch_pool(pp, q->dtype, D, hs);
+  hipError_t e = hipSuccess;
+  if (phase != MSA_ESTIMATE_SELECT_ONLY) e = launch_pool(pp, q->dtype, D, hs);
   if (e != hipSuccess) return int(e);
+  if (phase == MSA_ESTIMATE_POOL_ONLY) return MSA_OK;
 
   ScoreParams sp;
   memset(&sp, 0, sizeof(sp));

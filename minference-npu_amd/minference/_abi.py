@@ -47,10 +47,12 @@ MSA_VS_MAX_SEQ = 131072
 
 MSA_SELECT_FORCE_FIRST = 1
 MSA_SELECT_FORCE_DIAG = 2
+MSA_ESTIMATE_POOL_ONLY = 4
+MSA_ESTIMATE_SELECT_ONLY = 8
 
 MSA_MAX_HEADS = 128
 MSA_BLOCK = 64
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _DTYPE_CODE = {
     torch.bfloat16: MSA_DTYPE_BF16,
@@ -349,7 +351,9 @@ def block_estimate(
     flags: int = 0,
 ) -> None:
     """Launch msa_block_estimate on the current stream (no sync); with
-    ``flags`` (MSA_SELECT_*) msa_block_estimate_ex."""
+    ``flags`` (MSA_SELECT_* / MSA_ESTIMATE_*) msa_block_estimate_ex.  The
+    one-pass flags need the caller's workspace (the select pass reads what
+    the pooling pass left in it)."""
     lib = load_library()
     n_slots = len(slot_heads)
     if len(slot_topk) != n_slots:
@@ -358,6 +362,9 @@ def block_estimate(
     topk_arr = (ctypes.c_int32 * max(n_slots, 1))(*[int(t) for t in slot_topk])
     need = estimate_workspace_bytes(q.shape[0], n_slots, q.shape[2], k.shape[2], q.shape[3])
     if ws is None or ws.numel() < need:
+        if flags & (MSA_ESTIMATE_POOL_ONLY | MSA_ESTIMATE_SELECT_ONLY):
+            raise ValueError("a one-pass block estimate needs the caller's workspace "
+                             f"of at least {need} bytes")
         ws = workspace(need, q.device)
     qd, kd = tensor4(q), tensor4(k)
     stream = current_stream_handle(q.device)

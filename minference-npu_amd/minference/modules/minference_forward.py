@@ -170,9 +170,9 @@ def _vs_lists(q: torch.Tensor, k: torch.Tensor, plan: LayerPlan):
 
 def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: LayerPlan,
                         out: torch.Tensor) -> torch.Tensor:
-    """Estimator launches (block_sparse and vertical_and_slash heads) + the
-    attention launches of all heads (launch_block_layer's schedule for a
-    layer with block_sparse heads and no vertical_and_slash heads).
+    """Estimator launches (block_sparse and vertical_and_slash heads) + one
+    attention call for all heads (launch_block_layer's schedule for a layer
+    with block_sparse heads and no vertical_and_slash heads).
 
     q [B, H, S_q, D]; k/v [B, H_kv, S_k, D] (H % H_kv == 0, no repeat_kv copy);
     out any [B, H, S_q, D] view with D contiguous (bf16/fp16 or fp32).
@@ -202,7 +202,9 @@ def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan:
         idx = torch.empty((B, n_slots, n_qb, plan.topk_max), dtype=torch.int32, device=q.device)
         cnt = torch.empty((B, n_slots, n_qb), dtype=torch.int32, device=q.device)
     if not plan.vs_heads:
-        launch_block_layer(q, k, v, plan, out, idx, cnt, ws)
+        est_ws = _abi.workspace(_abi.estimate_workspace_bytes(B, n_slots, S_q, k.shape[2],
+                                                              q.shape[3]), q.device)
+        launch_block_layer(q, k, v, plan, out, idx, cnt, ws, est_ws)
         return out
     # vertical_and_slash heads: K/V staging on the side stream under the
     # estimators, then one attention call for all heads
@@ -221,66 +223,49 @@ def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan:
     return out
 
 
-def _only(plan: LayerPlan, keep) -> List[tuple]:
-    """plan.heads with every head h where not keep(h) set to MSA_KIND_SKIP."""
-    return [hd if keep(h) else (_abi.MSA_KIND_SKIP, 0, 0, -1, hd[4])
-            for h, hd in enumerate(plan.heads)]
-
-
 def launch_block_layer(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: LayerPlan,
                        out: torch.Tensor, idx: torch.Tensor, cnt: torch.Tensor,
-                       ws: torch.Tensor, est_ws: Optional[torch.Tensor] = None,
-                       flags: int = 0, mark=None) -> None:
+                       ws: torch.Tensor, est_ws: torch.Tensor, flags: int = 0,
+                       mark=None) -> None:
     """Launches of a layer with block_sparse heads and no vertical_and_slash
     heads, on the current ("main") stream and the device's side stream:
 
-      side: block estimator
-      main: K/V staging -> attention of the stream_llm / dense heads (block
-            heads MSA_KIND_SKIP) -> wait for side -> attention of the block
-            heads (the others MSA_KIND_SKIP)
+      main: block pooling -> K/V staging -> wait for side -> one attention
+            launch of all heads
+      side: (after the pooling) block scoring + top-k
 
-    The estimator runs beside the staging (both are memory passes that leave
-    bandwidth to each other), and the heads that need no block ids start as
-    soon as the staging is done.  A layer of block heads only makes one
-    attention launch after both.  Every head's rows are computed by the same
-    kernel code as in one launch of all heads, so the output is the same.
-    ``mark(name, stream)``, when given, is called at the phase boundaries
-    ("start", "est0", "est1", "stage0", "stage1", "attn0", "attn0_end",
-    "attn1", "attn1_end"; the benchmark records events there)."""
+    The selection pass (compute-bound) runs beside the staging (HBM-bound);
+    the pooling, also HBM-bound, runs before both.  Every head of the layer
+    is in the one attention grid, whatever the pattern mix.  ``est_ws`` is
+    the estimator workspace both passes share.  ``mark(name, stream)``, when
+    given, is called at the phase boundaries ("start", "est0", "est1",
+    "stage0", "stage1", "attn0", "attn0_end"; the benchmark records events
+    there)."""
     mark = mark or (lambda name, stream: None)
-    H = q.shape[1]
-    n_slots = len(plan.block_heads)
-    block = set(plan.block_heads)
     main = torch.cuda.current_stream(q.device)
     side = _side_stream(q.device)
+    scale = sparse_scale(q.shape[-1])
 
-    def attention(heads):
-        _abi.layer_attention(q, k, v, out, heads, idx=idx, cnt=cnt, idx_slots=n_slots,
-                             topk_max=plan.topk_max, ws=ws, staged=True)
+    def estimate(phase):
+        _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max, scale,
+                            idx, cnt, est_ws, flags=flags | phase)
 
     mark("start", main)
+    mark("est0", main)
+    estimate(_abi.MSA_ESTIMATE_POOL_ONLY)
     side.wait_stream(main)
     with torch.cuda.stream(side):
-        mark("est0", side)
-        _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max,
-                            sparse_scale(q.shape[-1]), idx, cnt, est_ws, flags=flags)
+        estimate(_abi.MSA_ESTIMATE_SELECT_ONLY)
         mark("est1", side)
     mark("stage0", main)
     _abi.stage_kv(k, v, ws)
     mark("stage1", main)
-    if len(block) < H:
-        mark("attn0", main)
-        attention(_only(plan, lambda h: h not in block))
-        mark("attn0_end", main)
-        main.wait_stream(side)
-        mark("attn1", main)
-        attention(_only(plan, lambda h: h in block))
-        mark("attn1_end", main)
-    else:
-        main.wait_stream(side)
-        mark("attn0", main)
-        attention(plan.heads)
-        mark("attn0_end", main)
+    main.wait_stream(side)
+    mark("attn0", main)
+    _abi.layer_attention(q, k, v, out, plan.heads, idx=idx, cnt=cnt,
+                         idx_slots=len(plan.block_heads), topk_max=plan.topk_max, ws=ws,
+                         staged=True)
+    mark("attn0_end", main)
 
 
 _SIDE_STREAMS: Dict[int, "torch.cuda.Stream"] = {}

@@ -163,10 +163,31 @@ def test_estimate_ex_flags_validated():
     lib = _abi.load_library()
     q = t4(SHAPE)
     ha = (ctypes.c_int32 * 1)(0)
-    for flags, want in [(4, _abi.MSA_E_TOPK), (-1, _abi.MSA_E_TOPK), (3, _abi.MSA_E_WORKSPACE)]:
+    both = _abi.MSA_ESTIMATE_POOL_ONLY | _abi.MSA_ESTIMATE_SELECT_ONLY
+    for flags, want in [(16, _abi.MSA_E_TOPK), (-1, _abi.MSA_E_TOPK), (both, _abi.MSA_E_TOPK),
+                        (3, _abi.MSA_E_WORKSPACE),
+                        (_abi.MSA_ESTIMATE_POOL_ONLY, _abi.MSA_E_WORKSPACE),
+                        (_abi.MSA_ESTIMATE_SELECT_ONLY | 3, _abi.MSA_E_WORKSPACE)]:
         st = lib.msa_block_estimate_ex(ctypes.byref(q), ctypes.byref(q), ha, None, 1, 64, 2,
                                        0.088, flags, FAKE, FAKE, FAKE, 100, None)
         assert st == want, flags
+
+
+def test_one_pass_estimate_needs_caller_workspace():
+    """The select pass reads what the pooling pass left in the workspace, so
+    the Python wrapper refuses a one-pass call without a large enough one
+    (instead of allocating a fresh, unfilled workspace)."""
+    import torch
+
+    q = torch.zeros(1, 2, 256, 96, dtype=torch.bfloat16)
+    idx = torch.zeros(1, 1, 4, 2, dtype=torch.int32)
+    cnt = torch.zeros(1, 1, 4, dtype=torch.int32)
+    for phase in (_abi.MSA_ESTIMATE_POOL_ONLY, _abi.MSA_ESTIMATE_SELECT_ONLY):
+        with pytest.raises(ValueError, match="workspace"):
+            _abi.block_estimate(q, q, [0], [2], 2, 0.088, idx, cnt, flags=phase)
+        with pytest.raises(ValueError, match="workspace"):
+            _abi.block_estimate(q, q, [0], [2], 2, 0.088, idx, cnt,
+                                ws=torch.zeros(16, dtype=torch.uint8), flags=phase)
 
 
 def test_attention_block_slot_range():

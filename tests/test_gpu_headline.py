@@ -2,9 +2,10 @@
 
 bench.py's headline step: S = 65536, 32 heads x 96, bf16, 16 stream_llm(128,
 4096) + 16 block_sparse(top-100) heads assigned by the seed-0 shuffle, Q/K/V
-from the bench's own generator (RoPE, K rows 0-3 x8), estimator + K/V staging
-+ one staged attention launch with the plan's kind-interleaved, cost-balanced
-item order.  Checked here:
+from the bench's own generator (RoPE, K rows 0-3 x8), launched by the
+bench's own schedule (launch_block_layer: estimator pooling, selection beside
+the K/V staging, one attention launch with the plan's kind-interleaved,
+cost-balanced item order; the fp32 output by a second launch).  Checked here:
   * block ids of all 16 block heads bit-exact with the oracle;
   * sampled rows of every head (tile boundaries, the sink edge, the band
     start, the last rows) within 2e-3 of the oracle, in fp32 output and in
@@ -40,7 +41,7 @@ def _rows(n_init, n_local):
 def test_headline_launch_matches_oracle(gpu_device):
     import bench
     from minference import _abi
-    from minference.modules.minference_forward import build_layer_plan
+    from minference.modules.minference_forward import build_layer_plan, launch_block_layer
     from minference.ops.common import sparse_scale
 
     print("[headline] building the bench's layer", flush=True)
@@ -53,14 +54,12 @@ def test_headline_launch_matches_oracle(gpu_device):
     idx = torch.empty((1, n_slots, n_qb, plan.topk_max), dtype=torch.int32, device=gpu_device)
     cnt = torch.empty((1, n_slots, n_qb), dtype=torch.int32, device=gpu_device)
     ws = _abi.workspace(_abi.attention_workspace_bytes(1, H, S, D), gpu_device)
-    _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max, sparse_scale(D),
-                        idx, cnt)
-    _abi.stage_kv(k, v, ws)
+    est_ws = _abi.workspace(_abi.estimate_workspace_bytes(1, n_slots, S, S, D), gpu_device)
     out16 = torch.empty_like(q)
     out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
-    for out in (out16, out32):
-        _abi.layer_attention(q, k, v, out, plan.heads, idx=idx, cnt=cnt, idx_slots=n_slots,
-                             topk_max=plan.topk_max, ws=ws, staged=True)
+    launch_block_layer(q, k, v, plan, out16, idx, cnt, ws, est_ws)
+    _abi.layer_attention(q, k, v, out32, plan.heads, idx=idx, cnt=cnt, idx_slots=n_slots,
+                         topk_max=plan.topk_max, ws=ws, staged=True)
     torch.cuda.synchronize()
 
     print("[headline] oracle block ids", flush=True)

@@ -1,11 +1,12 @@
-"""The split layer schedule (launch_block_layer) and MSA_KIND_SKIP heads on
-the GPU.
+"""The layer schedule (launch_block_layer), the estimator's one-pass flags and
+MSA_KIND_SKIP heads on the GPU.
 
-A layer with block_sparse and other heads runs as two attention launches:
-the other heads once the K/V staging is done (the estimator runs beside the
-staging on the side stream), then the block heads.  Every (head, query block) is computed by the same kernel code as in
-one launch of all heads, so the output must equal the single launch's bit for
-bit; its correctness against the oracle is what the other GPU tests check.
+A layer with block_sparse heads runs the estimator's pooling pass, then its
+selection pass on the side stream beside the K/V staging, then one attention
+launch of all heads.  The passes compute what one estimator call computes,
+and the attention launch is the one msa_layer_attention makes, so the ids
+and the output must equal those of the plain calls bit for bit; their
+correctness against the oracle is what the other GPU tests check.
 Semantics mirrored: minference/modules/minference_forward.py:398-487 (the
 reference's per-kind dispatch of one layer)."""
 
@@ -46,11 +47,12 @@ def _single_launch(plan, q, k, v, idx, cnt, out):
 
 
 @pytest.mark.parametrize("case", ["gqa_mixed", "mha_mixed", "block_only"])
-def test_split_schedule_matches_single_launch(gpu_device, case):
-    """launch_block_layer (estimator on the side stream, two attention
-    launches) == one launch of all heads, bit for bit, fp32 and bf16 outputs,
-    twice in a row.  gqa_mixed: kv heads shared by block and stream heads,
-    one kv head holding V beyond the fp16 range."""
+def test_layer_schedule_matches_plain_calls(gpu_device, case):
+    """launch_block_layer (two-pass estimator, the selection on the side
+    stream beside the staging) == msa_block_estimate + msa_layer_attention,
+    bit for bit, fp32 and bf16 outputs, twice in a row.  gqa_mixed: kv heads
+    shared by block and stream heads, one kv head holding V beyond the fp16
+    range."""
     from minference import _abi
     from minference.modules.minference_forward import launch_block_layer
     from minference.ops.common import sparse_scale
@@ -71,16 +73,19 @@ def test_split_schedule_matches_single_launch(gpu_device, case):
     ns = len(plan.block_heads)
     idx = torch.empty((1, ns, n_qb, plan.topk_max), dtype=torch.int32, device=gpu_device)
     cnt = torch.empty((1, ns, n_qb), dtype=torch.int32, device=gpu_device)
-    idx2, cnt2 = torch.empty_like(idx), torch.empty_like(cnt)
+    idx2, cnt2 = torch.full_like(idx, -5), torch.full_like(cnt, -5)
     _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max,
                         sparse_scale(96), idx2, cnt2)
     ws = _abi.workspace(_abi.attention_workspace_bytes(1, k.shape[1], S, 96), gpu_device)
+    est_ws = _abi.workspace(_abi.estimate_workspace_bytes(1, ns, S, S, 96), gpu_device)
     for dt in (torch.float32, torch.bfloat16):
         ref = torch.empty(q.shape, dtype=dt, device=gpu_device)
         _single_launch(plan, q, k, v, idx2, cnt2, ref)
         for rep in range(2):
             out = torch.full(q.shape, float("nan"), dtype=dt, device=gpu_device)
-            launch_block_layer(q, k, v, plan, out, idx, cnt, ws)
+            idx.fill_(-5)
+            cnt.fill_(-5)
+            launch_block_layer(q, k, v, plan, out, idx, cnt, ws, est_ws)
             torch.cuda.synchronize()
             assert torch.equal(idx, idx2) and torch.equal(cnt, cnt2)
             assert torch.equal(out, ref), (case, dt, rep, float((out.float() - ref.float()).abs().max()))
@@ -130,3 +135,42 @@ def test_run_layer_attention_uses_split_schedule(gpu_device):
     _single_launch(plan, q, k, v, idx, cnt, ref)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("flags", [0, 3])
+def test_estimator_passes_match_one_call(gpu_device, flags):
+    """MSA_ESTIMATE_POOL_ONLY then MSA_ESTIMATE_SELECT_ONLY (on another
+    stream, ordered by an event) == one msa_block_estimate_ex call, ids and
+    counts bit for bit, with and without the forced first / diagonal blocks;
+    the pooling pass leaves idx and cnt untouched."""
+    from minference import _abi
+    from minference.modules.minference_forward import _side_stream
+    from minference.ops.common import sparse_scale
+
+    print(f"[schedule] estimator passes flags={flags}", flush=True)
+    S = 2000
+    kinds = ["block_sparse", "stream_llm", "block_sparse", "block_sparse"]
+    plan, q, k, v = _layer(gpu_device, 4, 2, S, kinds, seed=11)
+    n_qb = math.ceil(S / 64)
+    ns = len(plan.block_heads)
+    topk = [3, 6, 5]
+    idx = torch.empty((1, ns, n_qb, 6), dtype=torch.int32, device=gpu_device)
+    cnt = torch.empty((1, ns, n_qb), dtype=torch.int32, device=gpu_device)
+    ref_idx, ref_cnt = torch.full_like(idx, -5), torch.full_like(cnt, -5)
+    sc = sparse_scale(96)
+    _abi.block_estimate(q, k, plan.block_heads, topk, 6, sc, ref_idx, ref_cnt, flags=flags)
+    ws = _abi.workspace(_abi.estimate_workspace_bytes(1, ns, S, S, 96), gpu_device)
+    idx.fill_(-5)
+    cnt.fill_(-5)
+    _abi.block_estimate(q, k, plan.block_heads, topk, 6, sc, idx, cnt, ws,
+                        flags=flags | _abi.MSA_ESTIMATE_POOL_ONLY)
+    torch.cuda.synchronize()
+    assert bool((idx == -5).all()) and bool((cnt == -5).all())
+    side = _side_stream(q.device)
+    side.wait_stream(torch.cuda.current_stream(q.device))
+    with torch.cuda.stream(side):
+        _abi.block_estimate(q, k, plan.block_heads, topk, 6, sc, idx, cnt, ws,
+                            flags=flags | _abi.MSA_ESTIMATE_SELECT_ONLY)
+    torch.cuda.current_stream(q.device).wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, ref_idx) and torch.equal(cnt, ref_cnt)
