@@ -168,8 +168,12 @@ __device__ inline void emit_topk(KeyFn keys, int nj, uint32_t T, int need_eq, in
   }
 }
 
+// Up to 1024 candidates (KPL <= 16) the kernel fits 128 registers, so four
+// workgroups share a CU and a 64K layer's 16 x 64 workgroups are all resident
+// at once.
 template <int D, int R, int KPL>
-__global__ __launch_bounds__(256) void score_topk_kernel(ScoreParams P) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KPL > 16 ? 1 : 4)))
+void score_topk_kernel(ScoreParams P) {
   static_assert(R == 16, "one 16-row fp64 MFMA tile of query blocks, 4 rows per wave");
   constexpr int NK = D / 4;  // k-steps of the 16x16x4 fp64 MFMA
 
