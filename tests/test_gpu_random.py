@@ -2,9 +2,10 @@
 
 Each case draws batch, head counts (MHA, GQA, MQA), head dim, dtype, S_k
 (ragged, down to one key), S_q (full or chunked prefill) and a per-head mix
-of stream_llm (random n_init / n_local), block_sparse (random top-k) and
-dense heads, runs the patched layer's dispatch (run_layer_attention: the
-block estimator and one attention launch) and checks every row of every head
+of stream_llm (random n_init / n_local), block_sparse (random top-k), dense
+and, for full prefills, vertical_and_slash heads (random vertical / slash
+counts), runs the patched layer's dispatch (run_layer_attention: the
+estimators and the attention launches) and checks every row of every head
 against the oracle's per-head layer within 2e-3 (fp32 output), plus the
 block ids of every block_sparse head bit-exact.
 Semantics mirrored: minference/modules/minference_forward.py:398-487 and the
@@ -41,9 +42,14 @@ def _draw(i: int):
     sink = 8.0 if rng.random() < 0.5 else None
     n_kb = math.ceil(S_k / 64)
     pats = {}
+    vs_ok = S_q == S_k
     for h in range(H):
-        kind = rng.choice(["stream_llm", "block_sparse", "dense"], p=[0.4, 0.45, 0.15])
-        if kind == "stream_llm":
+        kind = rng.choice(["stream_llm", "block_sparse", "dense", "vertical_and_slash"],
+                          p=[0.3, 0.35, 0.1, 0.25] if vs_ok else [0.4, 0.45, 0.15, 0.0])
+        if kind == "vertical_and_slash":
+            pats[h] = ["vertical_and_slash", int(rng.integers(1, 1500)), int(rng.integers(1, 3000)),
+                       1.0]
+        elif kind == "stream_llm":
             pats[h] = ["stream_llm", int(rng.integers(0, 300)), int(rng.integers(1, 2000)), 1.0]
         elif kind == "block_sparse":
             pats[h] = ["block_sparse", min(int(rng.integers(1, 40)), n_kb), 0, 1.0]
@@ -70,8 +76,21 @@ def test_random_layer(gpu_device, i):
     run_layer_attention(dq, dk, dv, plan, out)
 
     rep = H // Hkv
+    qn = np32(q)
     kr, vr = np.repeat(np32(k), rep, axis=1), np.repeat(np32(v), rep, axis=1)
-    ref, sel = O.layer_attention(np32(q), kr, vr, [pats[h] for h in range(H)], dtype_tag(dtype))
+    ref = np.zeros(q.shape)
+    sel = {}
+    for h in range(H):
+        ty, p1, p2 = pats[h][:3]
+        sl = slice(h, h + 1)
+        if ty == "vertical_and_slash":
+            vi, si = O.vs_estimate(qn[:, sl], kr[:, sl], p1, p2, dtype_tag(dtype))
+            ref[:, sl] = O.vertical_slash_from_indices(qn[:, sl], kr[:, sl], vr[:, sl], vi, si)
+        else:
+            r, s_h = O.layer_attention(qn[:, sl], kr[:, sl], vr[:, sl], [pats[h]], dtype_tag(dtype))
+            ref[:, sl] = r
+            if 0 in s_h:
+                sel[h] = s_h[0]
     assert_close_f32(out, ref, what=f"random case {i}")
 
     if plan.block_heads:
