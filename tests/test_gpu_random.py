@@ -107,3 +107,82 @@ def test_random_layer(gpu_device, i):
             assert np.array_equal(got_i[:, s, :, :tk], ridx[:, 0]), f"case {i} head {h}: ids differ"
             want_c = O.attend_count(ridx[:, 0], S_q, S_k)
             assert np.array_equal(got_c[:, s], want_c), f"case {i} head {h}: counts differ"
+
+
+def _draw_op(i: int):
+    rng = np.random.default_rng(77000 + i)
+    D = int(rng.choice([2 * int(rng.integers(4, 65)), 64, 96, 128]))  # even: RoPE'd inputs
+    B = int(rng.choice([1, 2]))
+    H = int(rng.integers(1, 5))
+    S_k = int(rng.choice([int(rng.integers(1, 300)), int(rng.integers(300, 2500))]))
+    S_q = S_k if rng.random() < 0.6 else int(rng.integers(1, S_k + 1))
+    dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float16
+    op = str(rng.choice(["stream", "block", "dense", "full"]))
+    if op == "full":  # dense without the causal mask: any S_q
+        S_q = int(rng.integers(1, 2 * S_k + 2))
+    n_init, n_local = int(rng.integers(0, 400)), int(rng.integers(1, 3000))
+    topk = int(rng.integers(1, 60))
+    return B, H, S_q, S_k, D, dtype, op, n_init, n_local, topk
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_op(gpu_device, i):
+    """The op-level entry points (streaming_forward, block_sparse_attention,
+    dense_attention causal and not) at random shapes and head dims up to 128
+    (zero-padded to the built sizes), fp32 outputs against the oracle on the
+    unpadded inputs (ops/streaming_kernel_npu.py:349-397,
+    ops/block_sparse_kernel_npu.py:609-709, backend_npu/attention.py:192-255)."""
+    from minference import block_sparse_attention, dense_attention, streaming_forward
+    from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
+
+    B, H, S_q, S_k, D, dtype, op, n_init, n_local, topk = _draw_op(i)
+    print(f"[random op] case {i}: {op} B={B} H={H} S_q={S_q} S_k={S_k} D={D} {dtype_tag(dtype)} "
+          f"n_init={n_init} n_local={n_local} topk={topk}", flush=True)
+    q, k, v = make_qkv(B, H, S_q, S_k, D, dtype, seed=5000 + i, sink_scale=8.0,
+                       use_rope=S_q <= S_k)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    qn, kn, vn = np32(q), np32(k), np32(v)
+    out = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    if op == "stream":
+        streaming_forward(dq, dk, dv, n_init, n_local, out=out)
+        ref = O.streaming_attention(qn, kn, vn, n_init, n_local)
+    elif op == "block":
+        n_kb = math.ceil(S_k / 64)
+        ids = select_block_sparse_topk_indices(dq, dk, topk).cpu().numpy()
+        ref_ids, _ = O.select_block_sparse_topk_indices(qn, kn, min(topk, n_kb), dtype_tag(dtype))
+        assert np.array_equal(ids, ref_ids), f"case {i}: ids differ"
+        block_sparse_attention(dq, dk, dv, topk, out=out)
+        ref = O.block_sparse_from_indices(qn, kn, vn, ref_ids)
+    elif op == "dense":
+        dense_attention(dq, dk, dv, out=out)
+        ref = O.dense_causal(qn, kn, vn)
+    else:
+        dense_attention(dq, dk, dv, causal=False, out=out)
+        ref = O.dense_causal(qn, kn, vn, causal=False)
+    assert_close_f32(out, ref, what=f"random op case {i}")
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_random_decode(gpu_device, i):
+    """decode_dense (one query row against the whole cache; split-K partials
+    and their merge) at random cache lengths, GQA groups and head dims
+    (backend_npu/attention.py:274-314)."""
+    from minference.backend.attention import decode_dense
+
+    rng = np.random.default_rng(91000 + i)
+    D = int(rng.choice([2 * int(rng.integers(4, 65)), 64, 96, 128]))  # even: RoPE'd inputs
+    B = int(rng.choice([1, 2, 3]))
+    Hkv = int(rng.choice([1, 2, 4]))
+    H = Hkv * int(rng.choice([1, 2, 4]))
+    S = int(rng.choice([int(rng.integers(1, 200)), int(rng.integers(200, 20000))]))
+    dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float16
+    print(f"[random decode] case {i}: B={B} H={H} Hkv={Hkv} S={S} D={D} {dtype_tag(dtype)}",
+          flush=True)
+    q, _, _ = make_qkv(B, H, 1, S, D, dtype, seed=6000 + i)
+    _, k, v = make_qkv(B, Hkv, S, S, D, dtype, seed=6100 + i, sink_scale=8.0)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    out = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    decode_dense(dq, dk, dv, out=out)
+    rep = H // Hkv
+    ref = O.dense_causal(np32(q), np.repeat(np32(k), rep, axis=1), np.repeat(np32(v), rep, axis=1))
+    assert_close_f32(out, ref, what=f"random decode case {i}")
