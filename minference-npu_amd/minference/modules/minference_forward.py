@@ -272,8 +272,9 @@ _SIDE_STREAMS: Dict[int, "torch.cuda.Stream"] = {}
 
 
 def _side_stream(device: torch.device) -> "torch.cuda.Stream":
-    """The per-device stream K/V staging overlaps the estimators on (default
-    priority, created once)."""
+    """The per-device side stream (default priority, created once): the block
+    selection runs on it beside the K/V staging, and in layers with
+    vertical_and_slash heads the staging runs on it beside the estimators."""
     index = device.index if device.index is not None else torch.cuda.current_device()
     st = _SIDE_STREAMS.get(index)
     if st is None:

@@ -1,0 +1,77 @@
+"""Host logic of the layer schedule (launch_block_layer) on the CPU: the
+library calls and the streams they go to, recorded by test doubles of the
+C ABI wrapper and of torch's stream API (no GPU).  The GPU tests check that
+the schedule computes what the plain calls compute."""
+
+from __future__ import annotations
+
+import contextlib
+
+import torch
+
+from minference import _abi
+from minference.modules import minference_forward as mf
+
+
+class _Stream:
+    def __init__(self, name, log):
+        self.name, self.log = name, log
+
+    def wait_stream(self, other):
+        self.log.append(("wait", self.name, other.name))
+
+
+def test_block_layer_schedule(monkeypatch):
+    log = []
+    main = _Stream("main", log)
+    current = [main]
+
+    @contextlib.contextmanager
+    def stream_ctx(st):
+        current.append(st)
+        try:
+            yield
+        finally:
+            current.pop()
+
+    monkeypatch.setattr(mf, "_SIDE_STREAMS", {})
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda device=None: main)
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
+    monkeypatch.setattr(torch.cuda, "Stream", lambda device=None: _Stream("side", log))
+    monkeypatch.setattr(torch.cuda, "stream", stream_ctx)
+
+    def block_estimate(q, k, heads, topk, topk_max, scale, idx, cnt, ws=None, flags=0):
+        log.append(("estimate", current[-1].name, flags, tuple(heads), ws is not None))
+
+    def stage_kv(k, v, ws, kv_heads=None):
+        log.append(("stage", current[-1].name))
+
+    def layer_attention(q, k, v, out, heads, **kw):
+        log.append(("attention", current[-1].name, len(heads), kw.get("staged"),
+                    kw.get("idx_slots")))
+
+    monkeypatch.setattr(mf._abi, "block_estimate", block_estimate)
+    monkeypatch.setattr(mf._abi, "stage_kv", stage_kv)
+    monkeypatch.setattr(mf._abi, "layer_attention", layer_attention)
+
+    pats = {0: ["stream_llm", 64, 256, 1], 1: ["block_sparse", 4, 0, 1], 2: ["dense", 0, 0, 1],
+            3: ["block_sparse", 2, 0, 1]}
+    plan = mf.build_layer_plan(pats, 4, 96, 1024)
+    q = torch.zeros(1, 4, 1024, 96)
+    marks = []
+    mf.launch_block_layer(q, q, q, plan, q, None, None, None, "est-ws",
+                          flags=_abi.MSA_SELECT_FORCE_DIAG,
+                          mark=lambda name, st: marks.append((name, st.name)))
+    pool = _abi.MSA_ESTIMATE_POOL_ONLY | _abi.MSA_SELECT_FORCE_DIAG
+    select = _abi.MSA_ESTIMATE_SELECT_ONLY | _abi.MSA_SELECT_FORCE_DIAG
+    assert log == [
+        ("estimate", "main", pool, (1, 3), True),       # pooling first, on the main stream
+        ("wait", "side", "main"),                       # the side stream follows the pooling
+        ("estimate", "side", select, (1, 3), True),     # selection beside the staging
+        ("stage", "main"),
+        ("wait", "main", "side"),                       # attention after the selection
+        ("attention", "main", 4, True, 2),              # one launch of all heads
+    ]
+    assert [m[0] for m in marks] == ["start", "est0", "est1", "stage0", "stage1", "attn0",
+                                     "attn0_end"]
+    assert dict(marks)["est1"] == "side"
