@@ -186,3 +186,37 @@ def test_random_decode(gpu_device, i):
     rep = H // Hkv
     ref = O.dense_causal(np32(q), np.repeat(np32(k), rep, axis=1), np.repeat(np32(v), rep, axis=1))
     assert_close_f32(out, ref, what=f"random decode case {i}")
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_random_rope(gpu_device, i):
+    """msa_rope_qk at random shapes (head dims multiples of 8, rotary widths
+    multiples of 16 up to the head dim, GQA, per-batch or broadcast tables,
+    random table halves): bit-exact with HF's eager apply_rotary_pos_emb on
+    the same GPU (looked up at minference/modules/minference_forward.py:205-212)."""
+    from minference.ops.rope import apply_rotary_pos_emb, rope_supported
+    from test_rope import hf_rope, rope_tables
+
+    rng = np.random.default_rng(88000 + i)
+    D = 8 * int(rng.integers(2, 17))
+    rot = 16 * int(rng.integers(1, D // 16 + 1))
+    B = int(rng.choice([1, 2]))
+    Hkv = int(rng.choice([1, 2, 4]))
+    H = Hkv * int(rng.choice([1, 2, 4]))
+    S = int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 3000))]))
+    dtype = torch.bfloat16 if rng.random() < 0.6 else torch.float16
+    tb = B if rng.random() < 0.5 else 1
+    rnd = bool(rng.random() < 0.5)
+    print(f"[random rope] case {i}: B={B} H={H} Hkv={Hkv} S={S} D={D} rot={rot} "
+          f"{dtype_tag(dtype)} tables={tb} random={rnd}", flush=True)
+    g = torch.Generator().manual_seed(8800 + i)
+    q = (torch.randn(B, H, S, D, generator=g) * 3).to(dtype)
+    k = (torch.randn(B, Hkv, S, D, generator=g) * 3).to(dtype)
+    cos, sin = rope_tables(tb, S, rot, dtype, offset=int(rng.integers(0, 100000)),
+                           random_halves=rnd, seed=i)
+    dq, dk, dc, ds = to_dev(gpu_device, q, k, cos, sin)
+    assert rope_supported(dq, dk, dc, ds)
+    gq, gk = apply_rotary_pos_emb(dq, dk, dc, ds)
+    rq, rk = hf_rope(dq, dk, dc, ds)
+    torch.cuda.synchronize()
+    assert torch.equal(gq, rq) and torch.equal(gk, rk), f"random rope case {i}"
