@@ -335,9 +335,15 @@ struct TileSeq {
     total = c;
     mpos = nfull == 1 ? c1 : c2;
   }
-  // tile at position q, clamped into [0, n_kb) for memory safety; positions
-  // past the end repeat the last tile (loads that are never consumed)
-  __device__ int tile(int q) const {
+  // Tile at position q, clamped into [0, n_kb) for memory safety; positions
+  // past the end repeat the last tile (loads that are never consumed).  In
+  // two halves, so that a caller can issue the scalar load a step before it
+  // needs the tile: fetch (position -> index, and the list entry's load) and
+  // finish (the tile from them).
+  struct Pending {
+    int v, i;
+  };
+  __device__ Pending fetch(int q) const {
     q = max(min(q, total - 1), 0);
     int i = lo4 + (q - c4);
     i = q < c4 ? lo3 + (q - c3) : i;
@@ -346,10 +352,13 @@ struct TileSeq {
     i = q < c1 ? lo0 + q : i;
     // the load is unconditional (element 0 of `any` when there is no list)
     // so that no branch splits the caller's instruction stream
-    const int32_t v = load_uniform((list ? list : any) + (list ? i : 0));
-    const int t = list ? v : i;
+    return {load_uniform((list ? list : any) + (list ? i : 0)), i};
+  }
+  __device__ int finish(Pending r) const {
+    const int t = list ? r.v : r.i;
     return min(max(t, 0), n_kb - 1);
   }
+  __device__ int tile(int q) const { return finish(fetch(q)); }
   __device__ bool masked(int q) const { return q >= mpos; }
 };
 
@@ -746,7 +755,8 @@ void attn_kernel(AttnParams P) {
     if constexpr (VS) return load_uniform(P.vs_masks + vs_base + max(min(q, total - 1), 0));
     return 0ull;
   };
-  int tA = 0, tB = 0, tn = 0;
+  int tA = 0, tB = 0;
+  TileSeq::Pending pn{0, 0};  // lookup of the position two ahead, issued a step early
   uint64_t mA = 0, mB = 0, mn = 0;
   // the first two positions' operands of the item (and the third's tile)
   auto start_tiles = [&]() INLINE {
@@ -759,7 +769,7 @@ void attn_kernel(AttnParams P) {
     load_v(tA, vA, !VS && total < 1);
     load_k(tB, kB, !VS && total < 2);
     load_v(tB, vB, !VS && total < 2);
-    tn = seq.tile(2);
+    pn = seq.fetch(2);
   };
   // one step: QK of both halves; half 0's softmax under half 1's QK, half
   // 1's softmax under half 0's PV; K is reloaded once the rare path can no
@@ -767,7 +777,11 @@ void attn_kernel(AttnParams P) {
   auto step = [&](auto masked, u32x4 (&kr)[NKS], u32x4 (&vr)[NDB], int& tcur, uint64_t& mcur,
                   int p) INLINE {
     constexpr bool MT = decltype(masked)::value;
-    const int tnn = seq.tile(p + 3);
+    // the tile of position p + 2 from the lookup issued in the previous step
+    // (its scalar load has had a step to arrive), then position p + 3's
+    // lookup.  (A scheduling barrier pinning that load here cost 1.5 %.)
+    const int tn = seq.finish(pn);
+    pn = seq.fetch(p + 3);
     const uint64_t mnn = mask_at(p + 3);
     // (vertical_and_slash items walk long lists: the per-step test costs
     // more there than the two loads it saves per item)
@@ -785,7 +799,6 @@ void attn_kernel(AttnParams P) {
     pv_half(sb, pb, 1, vr);
     load_v(tn, vr, drop);
     tcur = tn;
-    tn = tnn;
     mcur = mn;
     mn = mnn;
   };
