@@ -367,6 +367,19 @@ def main():
         return sum(e[a].elapsed_time(e[b]) for e in ev) / args.steps
 
     t_est = avg("est0", "est1") if n_slots else 0.0
+    # the estimator's own time: both passes with nothing beside them (in the
+    # step the selection shares the GPU with the staging)
+    t_est_alone = 0.0
+    if n_slots:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for rep_i in range(args.warmup + args.steps):
+            if rep_i == args.warmup:
+                e0.record(stream)
+            _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max,
+                                s_sparse, idx, cnt, ws_est, flags=sel_flags)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t_est_alone = e0.elapsed_time(e1) / args.steps
     t_stage = avg("stage0", "stage1")
     t_attn = avg("attn0", "attn0_end")
     t_pre = avg("start", "attn0")
@@ -414,6 +427,9 @@ def main():
                      if n_slots else "staging; one attention launch"),
         "ms_before_first_attention": round(t_pre, 4),
         "estimator_gbps": round(est_bytes / (t_est * 1e-3) / 1e9, 1) if n_slots else None,
+        "estimator_alone": ({"ms": round(t_est_alone, 4),
+                             "gbps": round(est_bytes / (t_est_alone * 1e-3) / 1e9, 1)}
+                            if n_slots else None),
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved_attn, 3),
