@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MSA_ABI_VERSION 9
+#define MSA_ABI_VERSION 10
 
 /* status codes (negative: validation, nothing launched) */
 #define MSA_OK 0
@@ -45,6 +45,7 @@ extern "C" {
 #define MSA_E_SEQ (-10)        /* S_q > S_k (causal kinds), S_q == 0, or too long */
 #define MSA_E_SLOTS (-11)      /* sparse head without an index slot, or bad index lists */
 #define MSA_E_SCRATCH (-12)    /* more than the fixed scratch of a no-allocation entry point */
+#define MSA_E_FLAGS (-13)      /* unknown flags, or flags that exclude each other */
 
 /* element types */
 #define MSA_DTYPE_BF16 1
@@ -101,7 +102,10 @@ typedef struct ihipStream_t* msa_stream_t; /* == hipStream_t */
 int msa_abi_version(void);
 const char* msa_status_str(int status);
 
-/* Bytes of workspace msa_block_estimate needs (pooled Q and K^T, fp32). */
+/* Bytes of workspace msa_block_estimate needs: pooled Q and K in the input
+ * dtype and the pooled scores of every row, fp32 (quadratic in S: 64 MiB per
+ * slot at S = 64K, 1 GiB per slot at S = 2^18; the long-sequence limit is
+ * S_k <= 2^20). */
 size_t msa_estimate_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_q,
                                     int64_t s_k, int32_t head_dim);
 
@@ -202,6 +206,23 @@ int msa_layer_attention_staged(const msa_tensor4* q, const msa_tensor4* k,
                                const int32_t* idx, const int32_t* cnt,
                                int32_t idx_slots, int32_t topk_max, void* workspace,
                                size_t workspace_bytes, msa_stream_t stream);
+
+/* msa_stage_kv and the pooling pass of the block estimator in one launch, for
+ * the layer schedule of a layer with block_sparse heads:
+ *   msa_stage_kv_pool (K/V staging + Q/K pooling) -> msa_block_estimate_ex
+ *   (MSA_ESTIMATE_SELECT_ONLY, same estimator workspace) ->
+ *   msa_layer_attention_staged, all on one stream.
+ * q, k, slot_heads and n_slots are those of the msa_block_estimate_ex call
+ * that follows; est_workspace is its workspace (msa_estimate_workspace_bytes),
+ * workspace the attention workspace (msa_attention_workspace_bytes).
+ * n_slots = 0 stages only (q, slot_heads and est_workspace unused).
+ * Replaces the same calls as msa_stage_kv and the pooling step of
+ * _select_block_sparse_topk_indices
+ * (minference/ops/block_sparse_kernel_npu.py:240-252). */
+int msa_stage_kv_pool(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
+                      const int32_t* slot_heads, int32_t n_slots, void* est_workspace,
+                      size_t est_workspace_bytes, void* workspace, size_t workspace_bytes,
+                      msa_stream_t stream);
 
 
 /* vertical_and_slash index lists of a layer: one slot per vertical_and_slash

@@ -84,25 +84,93 @@ const char* msa_status_str(int status) {
     case MSA_E_SEQ: return "sequence lengths must satisfy 0 < S_q <= S_k <= 2^20 (S_q > S_k only for full heads)";
     case MSA_E_SLOTS: return "sparse head without a valid index slot, or bad idx/cnt or vertical_and_slash lists";
     case MSA_E_SCRATCH: return "the call needs more than the fixed scratch of a no-allocation entry point (MSA_DECODE_SCRATCH_BYTES)";
+    case MSA_E_FLAGS: return "unknown flags, or MSA_ESTIMATE_POOL_ONLY and MSA_ESTIMATE_SELECT_ONLY together";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
   return "unknown status";
 }
 
+}  // extern "C"
+
+namespace {
+
+// Estimator workspace: pooled Q [B*slots][n_qb_pad][D] and pooled K
+// [B*slots][n_kb][D] (the slots' distinct kv heads) in the input dtype, then
+// the approximate scores [B*slots][n_qb_pad][n_kb_pad] fp32.
+struct EstLayout {
+  int n_qb, n_kb, n_qb_pad, n_kb_pad;
+  size_t q, k, sc, total;
+};
+
+EstLayout est_layout(int64_t batch, int64_t n_slots, int64_t s_q, int64_t s_k, int64_t D) {
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  EstLayout L;
+  L.n_qb = int(cdiv(s_q, MSA_BLOCK));
+  L.n_kb = int(cdiv(s_k, MSA_BLOCK));
+  L.n_qb_pad = int(cdiv(L.n_qb, kScoreRowPad) * kScoreRowPad);
+  L.n_kb_pad = int(cdiv(L.n_kb, 16) * 16);
+  const int64_t sb = batch * n_slots;
+  L.q = 0;
+  L.k = up(size_t(sb) * L.n_qb_pad * D * 2);
+  L.sc = L.k + up(size_t(sb) * L.n_kb * D * 2);
+  L.total = L.sc + up(size_t(sb) * L.n_qb_pad * L.n_kb_pad * 4);
+  return L;
+}
+
+// Checks shared by the estimator entry points; fills the pooling parameters
+// (slot -> distinct kv head entry in slot_kvp).
+int pool_setup(const msa_tensor4* q, const msa_tensor4* k, const int32_t* slot_heads,
+               int32_t n_slots, void* workspace, size_t workspace_bytes, PoolParams& pp,
+               int16_t* slot_kvp, EstLayout& L) {
+  int st = check_qk(q, k);
+  if (st != MSA_OK) return st;
+  if (!slot_heads) return MSA_E_NULL;
+  if (n_slots <= 0 || n_slots > kMaxHeads) return MSA_E_HEADS;
+  const int H = int(q->size[1]);
+  for (int s = 0; s < n_slots; ++s)
+    if (slot_heads[s] < 0 || slot_heads[s] >= H) return MSA_E_HEADS;
+  if (q->size[0] * n_slots > 65535) return MSA_E_HEADS;
+  const int D = int(q->size[3]);
+  L = est_layout(q->size[0], n_slots, q->size[2], k->size[2], D);
+  if (score_rows_for(L.n_kb) == 0) return MSA_E_SEQ;
+  if (!workspace || workspace_bytes < L.total) return MSA_E_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
+  memset(&pp, 0, sizeof(pp));
+  pp.q = q->data;
+  pp.k = k->data;
+  pp.q_sb = q->stride[0]; pp.q_sh = q->stride[1]; pp.q_ss = q->stride[2];
+  pp.k_sb = k->stride[0]; pp.k_sh = k->stride[1]; pp.k_ss = k->stride[2];
+  pp.s_q = q->size[2];
+  pp.s_k = k->size[2];
+  pp.n_qb = L.n_qb;
+  pp.n_kb = L.n_kb;
+  pp.n_qb_pad = L.n_qb_pad;
+  pp.batch = int(q->size[0]);
+  pp.n_slots = n_slots;
+  pp.kv_group = int(q->size[1] / k->size[1]);
+  pp.q_pool = ws_at<uint16_t>(workspace, L.q);
+  pp.k_pool = ws_at<uint16_t>(workspace, L.k);
+  pp.n_kvp = 0;
+  for (int s = 0; s < n_slots; ++s) {
+    pp.slot_heads[s] = int16_t(slot_heads[s]);
+    const int kvh = slot_heads[s] / pp.kv_group;
+    int i = 0;
+    while (i < pp.n_kvp && pp.kvp_head[i] != kvh) ++i;
+    if (i == pp.n_kvp) pp.kvp_head[pp.n_kvp++] = int16_t(kvh);
+    slot_kvp[s] = int16_t(i);
+  }
+  return MSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 size_t msa_estimate_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_q, int64_t s_k,
                                     int32_t head_dim) {
   if (batch <= 0 || n_slots <= 0 || s_q <= 0 || s_k <= 0 || head_dim <= 0) return 0;
-  const int64_t sb = batch * n_slots;
-  // pooled Q in fp64 (read through the scalar cache; rows padded to the
-  // scoring row group), pooled K^T in fp32
-  const int64_t n_qb_pad = cdiv(cdiv(s_q, MSA_BLOCK), kScoreRowPad) * kScoreRowPad;
-  const int64_t n_kb = cdiv(s_k, MSA_BLOCK);
-  int64_t bytes = sb * (n_qb_pad * 8 + n_kb * 4) * head_dim;
-  // the pooled scores of every row, fp32 (the reference's [B, H, n_bq, n_bk]
-  // score tensor)
-  bytes += sb * n_qb_pad * n_kb * 4;
-  return size_t((bytes + 255) / 256 * 256);
+  return est_layout(batch, n_slots, s_q, s_k, head_dim).total;
 }
 
 int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t* slot_heads,
@@ -120,55 +188,29 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
                           msa_stream_t stream) {
   constexpr int32_t kKnown = MSA_SELECT_FORCE_FIRST | MSA_SELECT_FORCE_DIAG |
                               MSA_ESTIMATE_POOL_ONLY | MSA_ESTIMATE_SELECT_ONLY;
-  if ((flags & ~kKnown) != 0) return MSA_E_TOPK;
+  if ((flags & ~kKnown) != 0) return MSA_E_FLAGS;
   const int32_t phase = flags & (MSA_ESTIMATE_POOL_ONLY | MSA_ESTIMATE_SELECT_ONLY);
-  if (phase == (MSA_ESTIMATE_POOL_ONLY | MSA_ESTIMATE_SELECT_ONLY)) return MSA_E_TOPK;
+  if (phase == (MSA_ESTIMATE_POOL_ONLY | MSA_ESTIMATE_SELECT_ONLY)) return MSA_E_FLAGS;
   flags &= MSA_SELECT_FORCE_FIRST | MSA_SELECT_FORCE_DIAG;
   int st = check_qk(q, k);
   if (st != MSA_OK) return st;
   if (block != MSA_BLOCK) return MSA_E_BLOCK;
   if (!slot_heads || !idx || !cnt) return MSA_E_NULL;
   if (n_slots <= 0 || n_slots > kMaxHeads) return MSA_E_HEADS;
-  const int H = int(q->size[1]);
-  for (int s = 0; s < n_slots; ++s)
-    if (slot_heads[s] < 0 || slot_heads[s] >= H) return MSA_E_HEADS;
-  const int n_qb = int(cdiv(q->size[2], MSA_BLOCK));
-  const int n_kb = int(cdiv(k->size[2], MSA_BLOCK));
-  if (topk_max < 1 || topk_max > n_kb) return MSA_E_TOPK;
+  const int64_t n_kb64 = cdiv(k->size[2], MSA_BLOCK);
+  if (topk_max < 1 || topk_max > n_kb64) return MSA_E_TOPK;
   if (slot_topk)
     for (int s = 0; s < n_slots; ++s)
       if (slot_topk[s] < 1 || slot_topk[s] > topk_max) return MSA_E_TOPK;
   if (!(score_scale > 0.0f) || !isfinite(score_scale)) return MSA_E_TOPK;
-  if (score_rows_for(n_kb) == 0) return MSA_E_SEQ;
+  PoolParams pp;
+  int16_t slot_kvp[kMaxHeads];
+  EstLayout L;
+  st = pool_setup(q, k, slot_heads, n_slots, workspace, workspace_bytes, pp, slot_kvp, L);
+  if (st != MSA_OK) return st;
   const int D = int(q->size[3]);
-  const size_t need = msa_estimate_workspace_bytes(q->size[0], n_slots, q->size[2], k->size[2], D);
-  if (!workspace || workspace_bytes < need) return MSA_E_WORKSPACE;
-  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
-  if (q->size[0] * n_slots > 65535) return MSA_E_HEADS;
 
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
-  const int64_t sb = q->size[0] * n_slots;
-  const int n_qb_pad = int(cdiv(n_qb, kScoreRowPad) * kScoreRowPad);
-  double* q_pool = static_cast<double*>(workspace);
-  float* k_poolT = reinterpret_cast<float*>(q_pool + sb * n_qb_pad * D);
-
-  PoolParams pp;
-  memset(&pp, 0, sizeof(pp));
-  pp.q = q->data;
-  pp.k = k->data;
-  pp.q_sb = q->stride[0]; pp.q_sh = q->stride[1]; pp.q_ss = q->stride[2];
-  pp.k_sb = k->stride[0]; pp.k_sh = k->stride[1]; pp.k_ss = k->stride[2];
-  pp.s_q = q->size[2];
-  pp.s_k = k->size[2];
-  pp.n_qb = n_qb;
-  pp.n_kb = n_kb;
-  pp.n_qb_pad = n_qb_pad;
-  pp.batch = int(q->size[0]);
-  pp.n_slots = n_slots;
-  pp.kv_group = int(q->size[1] / k->size[1]);
-  pp.q_pool = q_pool;
-  pp.k_poolT = k_poolT;
-  for (int s = 0; s < n_slots; ++s) pp.slot_heads[s] = int16_t(slot_heads[s]);
   hipError_t e = hipSuccess;
   if (phase != MSA_ESTIMATE_SELECT_ONLY) e = launch_pool(pp, q->dtype, D, hs);
   if (e != hipSuccess) return int(e);
@@ -176,14 +218,15 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
 
   ScoreParams sp;
   memset(&sp, 0, sizeof(sp));
-  sp.q_pool = q_pool;
-  sp.k_poolT = k_poolT;
-  sp.scores = k_poolT + sb * D * n_kb;
+  sp.q_pool = pp.q_pool;
+  sp.k_pool = pp.k_pool;
+  sp.scores = ws_at<float>(workspace, L.sc);
   sp.idx = idx;
   sp.cnt = cnt;
-  sp.n_qb = n_qb;
-  sp.n_kb = n_kb;
-  sp.n_qb_pad = n_qb_pad;
+  sp.n_qb = L.n_qb;
+  sp.n_kb = L.n_kb;
+  sp.n_qb_pad = L.n_qb_pad;
+  sp.n_kb_pad = L.n_kb_pad;
   sp.topk_max = topk_max;
   sp.batch = int(q->size[0]);
   sp.n_slots = n_slots;
@@ -191,8 +234,11 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
   sp.s_k = int(k->size[2]);
   sp.scale = score_scale;
   sp.flags = flags;
-  for (int s = 0; s < n_slots; ++s) sp.slot_topk[s] = int16_t(slot_topk ? slot_topk[s] : topk_max);
-  e = launch_score(sp, D, hs);
+  for (int s = 0; s < n_slots; ++s) {
+    sp.slot_topk[s] = int16_t(slot_topk ? slot_topk[s] : topk_max);
+    sp.slot_kvp[s] = slot_kvp[s];
+  }
+  e = launch_score(sp, q->dtype, D, hs);
   return e == hipSuccess ? MSA_OK : int(e);
 }
 
@@ -237,8 +283,8 @@ static int cus_per_xcd() {
 }
 
 
-static int stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
-                    size_t workspace_bytes, hipStream_t hs) {
+static int stage_setup(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
+                       size_t workspace_bytes, StageParams& sp) {
   if (!k || !v || !k->data || !v->data) return MSA_E_NULL;
   for (int i = 0; i < 4; ++i) {
     if (v->size[i] <= 0) return MSA_E_RANK;
@@ -255,7 +301,6 @@ static int stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
   const size_t need = msa_attention_workspace_bytes(B, Hkv, Sk, D);
   if (!workspace || workspace_bytes < need) return MSA_E_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
-  StageParams sp;
   memset(&sp, 0, sizeof(sp));  // gather-mode fields stay null: plain staging
   sp.k = k->data;
   sp.v = v->data;
@@ -270,14 +315,41 @@ static int stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
   sp.kv_heads = int(Hkv);
   sp.s_k = int(Sk);
   sp.s_pad = int(cdiv(Sk, MSA_BLOCK) * MSA_BLOCK);
-  hipError_t e = launch_stage(sp, v->dtype, D, hs);
-  if (e == hipSuccess) e = launch_vscale(sp, v->dtype, D, hs);
+  return MSA_OK;
+}
+
+static int stage_launch(const StageParams& sp, int dtype, int D, hipStream_t hs) {
+  hipError_t e = launch_stage(sp, dtype, D, hs);
+  if (e == hipSuccess) e = launch_vscale(sp, dtype, D, hs);
   return e == hipSuccess ? MSA_OK : int(e);
 }
 
 int msa_stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
                  size_t workspace_bytes, msa_stream_t stream) {
-  return stage_kv(k, v, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+  StageParams sp;
+  const int st = stage_setup(k, v, workspace, workspace_bytes, sp);
+  if (st != MSA_OK) return st;
+  return stage_launch(sp, v->dtype, int(v->size[3]), reinterpret_cast<hipStream_t>(stream));
+}
+
+int msa_stage_kv_pool(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
+                      const int32_t* slot_heads, int32_t n_slots, void* est_workspace,
+                      size_t est_workspace_bytes, void* workspace, size_t workspace_bytes,
+                      msa_stream_t stream) {
+  StageParams sp;
+  int st = stage_setup(k, v, workspace, workspace_bytes, sp);
+  if (st != MSA_OK) return st;
+  if (n_slots > 0) {
+    int16_t slot_kvp[kMaxHeads];
+    EstLayout L;
+    st = pool_setup(q, k, slot_heads, n_slots, est_workspace, est_workspace_bytes, sp.pool,
+                    slot_kvp, L);
+    if (st != MSA_OK) return st;
+    sp.n_pool_wg = pool_workgroups(sp.pool);
+  } else if (n_slots < 0) {
+    return MSA_E_HEADS;
+  }
+  return stage_launch(sp, v->dtype, int(v->size[3]), reinterpret_cast<hipStream_t>(stream));
 }
 
 // vertical_and_slash workspace: tile ids, key masks, counts per (slot,
@@ -561,7 +633,9 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
 
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   if (stage) {
-    st = stage_kv(k, v, workspace, workspace_bytes, hs);
+    StageParams sp;
+    st = stage_setup(k, v, workspace, workspace_bytes, sp);
+    if (st == MSA_OK) st = stage_launch(sp, v->dtype, D, hs);
     if (st != MSA_OK) return st;
   }
 

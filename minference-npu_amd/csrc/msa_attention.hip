@@ -39,6 +39,7 @@
 
 #include "msa_common.h"
 #include "msa_kernels.h"
+#include "msa_pool.h"
 
 namespace msa {
 
@@ -95,70 +96,93 @@ struct StageRows {
   }
 };
 
-__device__ inline float block_max256(float v, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  return v;
-}
-
 // V of 64 keys from j0 (staged row index) of head bk, times sc, into the
 // operand layout; returns the largest finite |V| read (before scaling),
-// reduced over the workgroup.
+// reduced over the workgroup.  The caller must place a barrier between two
+// calls that reuse `tile` / `red`.
 template <typename T, int D>
 __device__ float stage_v_tile(const StageParams& P, const uint16_t* src, const StageRows& src_row,
                               int64_t bk, int j0, float sc, uint16_t* tile, float* red) {
   using SS = StageShape<D>;
-  float vmax = 0.0f;
-  for (int ci = threadIdx.x; ci < kBlock * SS::KCH; ci += 256) {
+  constexpr int G = kBlock * SS::KCH / 256;  // 16-byte granules per thread
+  static_assert(G * 256 == kBlock * SS::KCH, "whole granules per thread");
+  // every load first, then the conversions
+  u32x4 in[G];
+  bool have[G];
+#pragma unroll
+  for (int u = 0; u < G; ++u) {
+    const int ci = threadIdx.x + 256 * u;
     const int r = ci / SS::KCH, c = ci - r * SS::KCH;
     const int j = src_row(j0 + r);
-    u32x4 out = zero_u32x4();
-    if (j >= 0) {
-      const u32x4 in = load16(src + int64_t(j) * P.v_ss + c * 8);
+    have[u] = j >= 0;
+    in[u] = have[u] ? load16(src + int64_t(j) * P.v_ss + c * 8) : zero_u32x4();
+  }
+  float vmax = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float flo = T::to_float(uint16_t(in[e] & 0xffffu));
-        const float fhi = T::to_float(uint16_t(in[e] >> 16));
-        vmax = fmaxf(vmax, fmaxf(finite_abs(flo), finite_abs(fhi)));
-        const _Float16 lo = to_f16_scaled(flo, sc);
-        const _Float16 hi = to_f16_scaled(fhi, sc);
-        out[e] = uint32_t(__builtin_bit_cast(uint16_t, lo)) |
-                 (uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16);
-      }
+  for (int u = 0; u < G; ++u) {
+    const int ci = threadIdx.x + 256 * u;
+    const int r = ci / SS::KCH, c = ci - r * SS::KCH;
+    u32x4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float flo = T::to_float(uint16_t(in[u][e] & 0xffffu));
+      const float fhi = T::to_float(uint16_t(in[u][e] >> 16));
+      vmax = fmaxf(vmax, fmaxf(finite_abs(flo), finite_abs(fhi)));
+      const _Float16 lo = to_f16_scaled(flo, sc);
+      const _Float16 hi = to_f16_scaled(fhi, sc);
+      out[e] = uint32_t(__builtin_bit_cast(uint16_t, lo)) |
+               (uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16);
     }
     store16(&tile[r * SS::LP + c * 8], out);
   }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = vmax;
   __syncthreads();
   const int64_t dst0 = (bk * P.s_pad + j0) * D;
-  for (int ci = threadIdx.x; ci < 4 * SS::NDB * 64; ci += 256) {
+  u32x4 outv[SS::NDB];
+#pragma unroll
+  for (int u = 0; u < SS::NDB; ++u) {
+    const int ci = threadIdx.x + 256 * u;
     const int l = ci & 63;
     const int cd = ci >> 6;  // chunk * NDB + db
     const int c = cd / SS::NDB, db = cd - c * SS::NDB;
     const int key0 = 16 * c + 8 * (l >> 5);
     const int d = 32 * db + (l & 31);
-    u32x4 out;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const uint16_t lo = tile[(key0 + 2 * e) * SS::LP + d];
       const uint16_t hi = tile[(key0 + 2 * e + 1) * SS::LP + d];
-      out[e] = uint32_t(lo) | (uint32_t(hi) << 16);
+      outv[u][e] = uint32_t(lo) | (uint32_t(hi) << 16);
     }
-    store16(P.vt + dst0 + ci * 8, out);
   }
-  return block_max256(vmax, red);  // its barriers also free `tile` for reuse
+#pragma unroll
+  for (int u = 0; u < SS::NDB; ++u) store16(P.vt + dst0 + (threadIdx.x + 256 * u) * 8, outv[u]);
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
+// Workgroup i of a launch: the first n_pool_wg run the block estimator's
+// pooling pass (fused launch of msa_stage_kv_pool); then, in the dispatch
+// order of a (tile, kv head, plane) grid, the V tiles of every kv head and
+// then the K tiles.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
   using SS = StageShape<D>;
   __shared__ __align__(16) uint16_t tile[kBlock * SS::LP];
   __shared__ float red[4];
-  const int j0 = blockIdx.x * kBlock;
-  const int bk = blockIdx.y;  // b * kv_heads + kvh (gather mode: b * n_slots + slot)
+  int wi = int(blockIdx.x);
+  if (wi < P.n_pool_wg) {
+    pool_workgroup<T, D>(P.pool, wi);
+    return;
+  }
+  wi -= P.n_pool_wg;
+  const int n_tiles = P.s_pad / kBlock;
+  const int n_bk = P.batch * (P.rows ? P.n_slots : P.kv_heads);
+  const int tile_i = wi % n_tiles;
+  const int rest = wi / n_tiles;
+  const int bk = rest % n_bk;  // b * kv_heads + kvh (gather mode: b * n_slots + slot)
+  const int plane = rest / n_bk;  // 0: V, 1: K
+  const int j0 = tile_i * kBlock;
   int b, kvh;
   StageRows src_row{nullptr, 0, P.s_k};
   if (P.rows) {
@@ -172,24 +196,28 @@ __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
   }
   // the tile's 4 chunks are 64*D consecutive halves starting at key j0
   const int64_t dst0 = (int64_t(bk) * P.s_pad + j0) * D;
-  if (blockIdx.z == 1) {
+  if (plane == 1) {
     const uint16_t* src = reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + kvh * P.k_sh;
-    for (int gi = threadIdx.x; gi < 4 * SS::NDB * 64; gi += 256) {
+    // NDB granules per thread, every load before the stores
+    u32x4 x[SS::NDB];
+#pragma unroll
+    for (int u = 0; u < SS::NDB; ++u) {
+      const int gi = threadIdx.x + 256 * u;
       const int l = gi & 63;
       const int cks = gi >> 6;  // chunk * NDB + ks
       const int c = cks / SS::NDB, ks = cks - c * SS::NDB;
       const int j = src_row(j0 + 16 * c + (l & 15));
-      const u32x4 x = j >= 0 ? load16(src + int64_t(j) * P.k_ss + 32 * ks + 8 * (l >> 4))
-                             : zero_u32x4();
-      store16(P.kt + dst0 + gi * 8, x);
+      x[u] = j >= 0 ? load16(src + int64_t(j) * P.k_ss + 32 * ks + 8 * (l >> 4)) : zero_u32x4();
     }
+#pragma unroll
+    for (int u = 0; u < SS::NDB; ++u) store16(P.kt + dst0 + (threadIdx.x + 256 * u) * 8, x[u]);
     return;
   }
   const uint16_t* src = reinterpret_cast<const uint16_t*>(P.v) + b * P.v_sb + kvh * P.v_sh;
   // gather mode uses the scale the head's plain staging chose
   const float sc = P.rows ? __builtin_amdgcn_ldexpf(1.0f, -P.vexp[b * P.kv_heads + kvh]) : 1.0f;
   const float m = stage_v_tile<T, D>(P, src, src_row, bk, j0, sc, tile, red);
-  if (!P.rows && threadIdx.x == 0) P.tmax[int64_t(bk) * (P.s_pad / kBlock) + blockIdx.x] = m;
+  if (!P.rows && threadIdx.x == 0) P.tmax[int64_t(bk) * n_tiles + tile_i] = m;
 }
 
 // One workgroup per (batch, kv head): picks the head's V exponent from the
@@ -203,7 +231,12 @@ __global__ __launch_bounds__(256) void vscale_kernel(StageParams P) {
   const int n_kb = P.s_pad / kBlock;
   float m = 0.0f;
   for (int t = threadIdx.x; t < n_kb; t += 256) m = fmaxf(m, P.tmax[int64_t(bk) * n_kb + t]);
-  m = block_max256(m, red);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
   int e = 0;
   while (m * __builtin_amdgcn_ldexpf(1.0f, -e) > kF16Max) ++e;  // m < 2^128: e <= 113
   if (threadIdx.x == 0) P.vexp[bk] = e;
@@ -213,13 +246,17 @@ __global__ __launch_bounds__(256) void vscale_kernel(StageParams P) {
   const uint16_t* src = reinterpret_cast<const uint16_t*>(P.v) + b * P.v_sb + kvh * P.v_sh;
   const StageRows src_row{nullptr, 0, P.s_k};
   const float sc = __builtin_amdgcn_ldexpf(1.0f, -e);
-  for (int t = 0; t < n_kb; ++t) stage_v_tile<T, D>(P, src, src_row, bk, t * kBlock, sc, tile, red);
+  for (int t = 0; t < n_kb; ++t) {
+    stage_v_tile<T, D>(P, src, src_row, bk, t * kBlock, sc, tile, red);
+    __syncthreads();  // tile and red are reused by the next tile
+  }
 }
 
 template <typename T, int D>
 static hipError_t launch_stage_t(const StageParams& p, hipStream_t st) {
-  dim3 grid(p.s_pad / kBlock, p.batch * (p.rows ? p.n_slots : p.kv_heads), 2);
-  hipLaunchKernelGGL((stage_kernel<T, D>), grid, dim3(256), 0, st, p);
+  const int64_t n = p.n_pool_wg + int64_t(p.s_pad / kBlock) *
+                                     (p.batch * (p.rows ? p.n_slots : p.kv_heads)) * 2;
+  hipLaunchKernelGGL((stage_kernel<T, D>), dim3(uint32_t(n)), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 

@@ -8,6 +8,11 @@
 
 namespace msa {
 
+// Pooled Q and K of the block estimator, in the input dtype (the pooled
+// values are the reference's bf16/fp16 means, so 16 bits hold them exactly):
+//   q_pool [batch*n_slots][n_qb_pad][D]  (rows n_qb .. n_qb_pad-1 unused)
+//   k_pool [batch*n_slots][n_kb][D]      (entry b * n_slots + i: the i-th
+//                                         distinct kv head of the slots)
 struct PoolParams {
   const void* q;
   const void* k;
@@ -16,29 +21,34 @@ struct PoolParams {
   int64_t s_q, s_k;
   int n_qb, n_kb, n_qb_pad;  // n_qb_pad: n_qb rounded up to kScoreRowPad
   int batch, n_slots, kv_group;
-  double* q_pool;  // [batch*n_slots][n_qb_pad][D] (pooled values, exact in fp64)
-  float* k_poolT;  // [batch*n_slots][D][n_kb]
+  int n_kvp;                 // distinct kv heads of the slots
+  uint16_t* q_pool;
+  uint16_t* k_pool;
   int16_t slot_heads[kMaxHeads];  // head of q for each slot (kernel-argument copy)
+  int16_t kvp_head[kMaxHeads];    // kv head of each distinct pooled K entry
 };
 
 struct ScoreParams {
-  const double* q_pool;  // [batch*n_slots][n_qb_pad][D]
-  const float* k_poolT;
-  float* scores;  // [batch*n_slots][n_qb_pad][n_kb]: pooled scores of every row
+  const uint16_t* q_pool;  // [batch*n_slots][n_qb_pad][D]
+  const uint16_t* k_pool;  // [batch*n_slots][n_kb][D]
+  float* scores;  // [batch*n_slots][n_qb_pad][n_kb_pad]: approximate pooled scores; the
+                  // selection keeps its per-row keys there when they do not fit registers
   int32_t* idx;  // [batch*n_slots][n_qb][topk_max]
   int32_t* cnt;  // [batch*n_slots][n_qb]
-  int n_qb, n_kb, n_qb_pad, topk_max, batch, n_slots;
+  int n_qb, n_kb, n_qb_pad, n_kb_pad, topk_max, batch, n_slots;
   int s_q, s_k;  // row i of the query is absolute position s_k - s_q + i
   float scale;
   int flags;     // kSelectForceFirst | kSelectForceDiag
   int16_t slot_topk[kMaxHeads];
+  int16_t slot_kvp[kMaxHeads];  // pooled K entry of each slot
 };
 
 // Selector options: block 0 / the query block's own (diagonal, q-frame)
 // block always selected, inside the top-k (their scores count as +inf; ties
 // among forced ids go to the lower id).
 constexpr int kSelectForceFirst = 1;
-// Pooled-Q rows are padded to a multiple of the largest scoring row group.
+// Pooled-Q rows are padded to a multiple of the scoring row group; score
+// rows to a multiple of 16 candidates (16-byte aligned quads).
 constexpr int kScoreRowPad = 16;
 constexpr int kSelectForceDiag = 2;
 
@@ -155,6 +165,10 @@ struct StageParams {
   float* tmax;
   int32_t* vexp;
   int16_t slot_kvh[kMaxHeads];
+  // Fused pooling (plain mode): the first n_pool_wg workgroups of the launch
+  // run the block estimator's pooling pass with these parameters.
+  int n_pool_wg;
+  PoolParams pool;
 };
 
 struct DecodeParams {
@@ -199,7 +213,8 @@ constexpr int kRopeMaxRot = 256;
 constexpr int kDecodeMaxSplit = 2048;
 
 hipError_t launch_pool(const PoolParams& p, int dtype, int D, hipStream_t st);
-hipError_t launch_score(const ScoreParams& p, int D, hipStream_t st);
+int pool_workgroups(const PoolParams& p);
+hipError_t launch_score(const ScoreParams& p, int dtype, int D, hipStream_t st);
 int score_rows_for(int n_kb);
 hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st);
 hipError_t launch_vscale(const StageParams& p, int dtype, int D, hipStream_t st);

@@ -31,6 +31,7 @@ MSA_E_WORKSPACE = -9
 MSA_E_SEQ = -10
 MSA_E_SLOTS = -11
 MSA_E_SCRATCH = -12
+MSA_E_FLAGS = -13
 MSA_DECODE_SCRATCH_BYTES = 4 << 20
 
 MSA_DTYPE_BF16 = 1
@@ -52,7 +53,7 @@ MSA_ESTIMATE_SELECT_ONLY = 8
 
 MSA_MAX_HEADS = 128
 MSA_BLOCK = 64
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _DTYPE_CODE = {
     torch.bfloat16: MSA_DTYPE_BF16,
@@ -71,6 +72,7 @@ EXPORTED_SYMBOLS = (
     "msa_layer_attention",
     "msa_stage_kv",
     "msa_layer_attention_staged",
+    "msa_stage_kv_pool",
     "msa_decode_workspace_bytes",
     "msa_decode_attention",
     "msa_decode_attention_noalloc",
@@ -190,6 +192,12 @@ def load_library() -> ctypes.CDLL:
         lib.msa_stage_kv.argtypes = [
             ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
+        lib.msa_stage_kv_pool.restype = ctypes.c_int
+        lib.msa_stage_kv_pool.argtypes = [
+            ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4), ctypes.POINTER(MsaTensor4),
+            ctypes.POINTER(ctypes.c_int32), ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
         lib.msa_decode_workspace_bytes.restype = ctypes.c_size_t
         lib.msa_decode_workspace_bytes.argtypes = [
@@ -400,6 +408,23 @@ def stage_kv(k: torch.Tensor, v: torch.Tensor, ws: torch.Tensor) -> None:
     kd, vd = tensor4(k), tensor4(v)
     check(load_library().msa_stage_kv(ctypes.byref(kd), ctypes.byref(vd), ws.data_ptr(),
                                       ws.numel(), current_stream_handle(v.device)))
+
+
+def stage_kv_pool(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                  slot_heads: Sequence[int], est_ws: Optional[torch.Tensor],
+                  ws: torch.Tensor) -> None:
+    """Launch msa_stage_kv_pool on the current stream: K/V staged into ``ws``
+    and, for the block slots ``slot_heads``, Q and K pooled into ``est_ws``
+    (the workspace of the MSA_ESTIMATE_SELECT_ONLY block_estimate call that
+    follows)."""
+    n = len(slot_heads)
+    heads_arr = (ctypes.c_int32 * max(n, 1))(*[int(h) for h in slot_heads])
+    qd, kd, vd = tensor4(q), tensor4(k), tensor4(v)
+    est_p = est_ws.data_ptr() if est_ws is not None else None
+    est_n = est_ws.numel() if est_ws is not None else 0
+    check(load_library().msa_stage_kv_pool(
+        ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), heads_arr, n, est_p, est_n,
+        ws.data_ptr(), ws.numel(), current_stream_handle(v.device)))
 
 
 def vs_estimate_workspace_bytes(batch: int, n_slots: int, s: int, head_dim: int) -> int:

@@ -12,6 +12,8 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC_DIR = os.path.join(os.path.dirname(PKG_DIR), "csrc")
@@ -25,7 +27,6 @@ HIPCC_FLAGS = (
     "--offload-arch=gfx950",
     "-O3",
     "-std=c++17",
-    "-shared",
     "-fPIC",
     # packed fp32 VALU ops are kept out of the generated code
     "-Xclang",
@@ -46,25 +47,42 @@ def hipcc_path() -> str:
     return found
 
 
-def build(verbose: bool = False, extra_flags: tuple[str, ...] = ()) -> str:
-    """Compile every HIP source into libmsa.so; returns the library path."""
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc_path(), *HIPCC_FLAGS, *extra_flags, "-o", tmp]
-    cmd += [os.path.join(CSRC_DIR, s) for s in SOURCES]
+def _run(cmd: list) -> subprocess.CompletedProcess:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(
             "hipcc failed (%d):\n%s\n%s" % (proc.returncode, " ".join(cmd), proc.stderr)
         )
+    return proc
+
+
+def build(verbose: bool = False, extra_flags: tuple[str, ...] = (), csrc_dir: str = CSRC_DIR,
+          out_path: str = LIB_PATH, jobs: int = 0) -> str:
+    """Compile every HIP source into libmsa.so; returns the library path.
+
+    Each source is compiled to an object of its own (in parallel, ``jobs``
+    processes, default one per source up to the CPU count), then the objects
+    are linked into the shared library."""
+    out_dir = os.path.dirname(os.path.abspath(out_path))
+    os.makedirs(out_dir, exist_ok=True)
+    hipcc = hipcc_path()
+    jobs = jobs or max(1, min(len(SOURCES), os.cpu_count() or 1))
+    with tempfile.TemporaryDirectory(prefix="msa_obj_", dir=out_dir) as obj_dir:
+        objs = [os.path.join(obj_dir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+        cmds = [[hipcc, *HIPCC_FLAGS, *extra_flags, "-c", "-o", o, os.path.join(csrc_dir, s)]
+                for s, o in zip(SOURCES, objs)]
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            procs = list(pool.map(_run, cmds))
+        tmp = out_path + ".tmp"
+        procs.append(_run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]))
     if verbose:
         err = "\n".join(
-            ln for ln in proc.stderr.splitlines() if "packed-fp32-ops" not in ln
+            ln for p in procs for ln in p.stderr.splitlines() if "packed-fp32-ops" not in ln
         )
         if err.strip():
             print(err, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out_path)
+    return out_path
 
 
 if __name__ == "__main__":

@@ -228,39 +228,32 @@ def launch_block_layer(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: 
                        ws: torch.Tensor, est_ws: torch.Tensor, flags: int = 0,
                        mark=None) -> None:
     """Launches of a layer with block_sparse heads and no vertical_and_slash
-    heads, on the current ("main") stream and the device's side stream:
+    heads, in order on the current stream:
 
-      main: block pooling -> K/V staging -> wait for side -> one attention
-            launch of all heads
-      side: (after the pooling) block scoring + top-k
+      1. K/V staging and the block estimator's pooling pass, one launch
+         (msa_stage_kv_pool; then the small V-range pass);
+      2. the block selection: scores and top-k (msa_block_estimate_ex,
+         MSA_ESTIMATE_SELECT_ONLY);
+      3. one attention launch of all heads.
 
-    The selection pass (compute-bound) runs beside the staging (HBM-bound);
-    the pooling, also HBM-bound, runs before both.  Every head of the layer
-    is in the one attention grid, whatever the pattern mix.  ``est_ws`` is
-    the estimator workspace both passes share.  ``mark(name, stream)``, when
-    given, is called at the phase boundaries ("start", "est0", "est1",
-    "stage0", "stage1", "attn0", "attn0_end"; the benchmark records events
-    there)."""
+    One stream and no events between the launches: each launch starts as the
+    previous one drains (cross-stream waits cost 10-20 us each here).  Every
+    head of the layer is in the one attention grid, whatever the pattern mix.
+    ``est_ws`` is the estimator workspace both estimator passes share.
+    ``mark(name, stream)``, when given, is called at the phase boundaries
+    ("start", "stage0", "stage1", "est0", "est1", "attn0", "attn0_end"; the
+    benchmark records events there)."""
     mark = mark or (lambda name, stream: None)
     main = torch.cuda.current_stream(q.device)
-    side = _side_stream(q.device)
-    scale = sparse_scale(q.shape[-1])
-
-    def estimate(phase):
-        _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max, scale,
-                            idx, cnt, est_ws, flags=flags | phase)
-
     mark("start", main)
-    mark("est0", main)
-    estimate(_abi.MSA_ESTIMATE_POOL_ONLY)
-    side.wait_stream(main)
-    with torch.cuda.stream(side):
-        estimate(_abi.MSA_ESTIMATE_SELECT_ONLY)
-        mark("est1", side)
     mark("stage0", main)
-    _abi.stage_kv(k, v, ws)
+    _abi.stage_kv_pool(q, k, v, plan.block_heads, est_ws, ws)
     mark("stage1", main)
-    main.wait_stream(side)
+    mark("est0", main)
+    _abi.block_estimate(q, k, plan.block_heads, plan.block_topk, plan.topk_max,
+                        sparse_scale(q.shape[-1]), idx, cnt, est_ws,
+                        flags=flags | _abi.MSA_ESTIMATE_SELECT_ONLY)
+    mark("est1", main)
     mark("attn0", main)
     _abi.layer_attention(q, k, v, out, plan.heads, idx=idx, cnt=cnt,
                          idx_slots=len(plan.block_heads), topk_max=plan.topk_max, ws=ws,
@@ -272,9 +265,9 @@ _SIDE_STREAMS: Dict[int, "torch.cuda.Stream"] = {}
 
 
 def _side_stream(device: torch.device) -> "torch.cuda.Stream":
-    """The per-device side stream (default priority, created once): the block
-    selection runs on it beside the K/V staging, and in layers with
-    vertical_and_slash heads the staging runs on it beside the estimators."""
+    """The per-device side stream (default priority, created once): in layers
+    with vertical_and_slash heads the K/V staging runs on it beside the
+    estimators."""
     index = device.index if device.index is not None else torch.cuda.current_device()
     st = _SIDE_STREAMS.get(index)
     if st is None:

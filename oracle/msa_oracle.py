@@ -198,28 +198,37 @@ def select_topk(scores: np.ndarray, topk: int, force_first: bool = False,
     attended (token causal mask, :281-284), and here they are the next
     future ids bq+1, bq+2, ... in ascending order.
 
+    NaN scores rank above +inf, all NaNs alike, ties to the lower id
+    (torch.topk, which the reference calls at :262, returns NaN entries
+    first: topk([1, nan, 2, inf, nan], 3) gives ids 1, 4, 3).
+
     force_first / force_diag (this build's selector option, not the
-    reference's): block 0 / block bq rank above every scored block (their
-    scores count as +inf), inside the top-k; between them the lower id wins.
+    reference's): block 0 / block bq rank above every scored block,
+    NaN included, inside the top-k; between them the lower id wins.
     """
     *lead, n_bq, n_bk = scores.shape
+    # rank classes: 2 = forced, 1 = NaN, 0 = scored (ordered by value)
+    cls = np.where(np.isnan(scores), 1, 0).astype(np.int8)
     if force_first or force_diag:
-        scores = np.array(scores, dtype=np.float32, copy=True)
         if force_first:
-            scores[..., :, 0] = np.inf
+            cls[..., :, 0] = 2
         if force_diag:
             d = np.arange(min(n_bq, n_bk))
-            scores[..., d, d] = np.inf
+            cls[..., d, d] = 2
     topk = min(int(topk), n_bk)
     flat = scores.reshape(-1, n_bq, n_bk)
+    fcls = cls.reshape(-1, n_bq, n_bk)
     idx = np.empty((flat.shape[0], n_bq, topk), dtype=np.int64)
     cnt = np.empty((flat.shape[0], n_bq), dtype=np.int64)
     for bq in range(n_bq):
         n = min(bq + 1, n_bk)
         c = min(topk, n)
-        row = flat[:, bq, :n]
-        # stable sort on -score keeps equal scores in ascending id order
-        order = np.argsort(-row.astype(np.float64), axis=-1, kind="stable")[:, :c]
+        row = flat[:, bq, :n].astype(np.float64)
+        rcls = fcls[:, bq, :n]
+        val = np.where(rcls == 0, row, 0.0) + 0.0  # -0 ranks with +0
+        ids = np.broadcast_to(np.arange(n), row.shape)
+        # class descending, then value descending, then id ascending
+        order = np.lexsort((ids, -val, -rcls), axis=-1)[:, :c]
         sel = np.sort(order, axis=-1)
         idx[:, bq, :c] = sel
         if c < topk:

@@ -36,7 +36,7 @@ def test_library_exports_every_header_symbol():
 def test_abi_version_and_status_strings():
     lib = _abi.load_library()
     assert lib.msa_abi_version() == _abi.ABI_VERSION
-    for code in range(-12, 1):
+    for code in range(-13, 1):
         s = _abi.status_str(code)
         assert s and s != "unknown status"
     assert _abi.status_str(-99) == "unknown status"
@@ -56,16 +56,17 @@ def test_decode_noalloc_refuses_oversize_before_any_device_call():
 
 
 def test_workspace_sizes():
-    # estimator: pooled Q in fp64 (rows padded to 16), pooled K^T in fp32 and
-    # the fp32 pooled scores of every (padded) row, rounded up to 256 bytes
+    # estimator: pooled Q (rows padded to 16) and pooled K in the input dtype,
+    # then the fp32 pooled scores of every (padded) row, rows padded to 16
+    # candidates; each part rounded up to 256 bytes
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     assert _abi.estimate_workspace_bytes(1, 32, 16384, 16384, 96) == \
-        32 * (256 * 96 * (8 + 4) + 256 * 256 * 4)
+        up(32 * 256 * 96 * 2) + up(32 * 256 * 96 * 2) + up(32 * 256 * 256 * 4)
     assert _abi.estimate_workspace_bytes(1, 1, 100, 100, 64) == \
-        (16 * 64 * 8 + 2 * 64 * 4 + 16 * 2 * 4 + 255) // 256 * 256
+        up(16 * 64 * 2) + up(2 * 64 * 2) + up(16 * 16 * 4)
     # attention: staged K and V operands (16-bit) padded to 64 keys, the V
     # maxima per 64-key tile (fp32) and the V exponent per kv head (int32),
     # each rounded up to 256 bytes, then 256 bytes of work-queue counters
-    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     staged = 2 * 32 * 96 * 65536 * 2
     assert _abi.attention_workspace_bytes(1, 32, 65536, 96) == \
         up(up(staged + 32 * 1024 * 4) + 32 * 4) + 256
@@ -164,13 +165,38 @@ def test_estimate_ex_flags_validated():
     q = t4(SHAPE)
     ha = (ctypes.c_int32 * 1)(0)
     both = _abi.MSA_ESTIMATE_POOL_ONLY | _abi.MSA_ESTIMATE_SELECT_ONLY
-    for flags, want in [(16, _abi.MSA_E_TOPK), (-1, _abi.MSA_E_TOPK), (both, _abi.MSA_E_TOPK),
+    for flags, want in [(16, _abi.MSA_E_FLAGS), (-1, _abi.MSA_E_FLAGS),
+                        (both, _abi.MSA_E_FLAGS),
                         (3, _abi.MSA_E_WORKSPACE),
                         (_abi.MSA_ESTIMATE_POOL_ONLY, _abi.MSA_E_WORKSPACE),
                         (_abi.MSA_ESTIMATE_SELECT_ONLY | 3, _abi.MSA_E_WORKSPACE)]:
         st = lib.msa_block_estimate_ex(ctypes.byref(q), ctypes.byref(q), ha, None, 1, 64, 2,
                                        0.088, flags, FAKE, FAKE, FAKE, 100, None)
         assert st == want, flags
+    # the message names the flags, not another argument
+    assert "flags" in _abi.status_str(_abi.MSA_E_FLAGS)
+
+
+def test_stage_kv_pool_validated():
+    """msa_stage_kv_pool checks the staging arguments and, with block slots,
+    the estimator's (fake pointers: nothing is launched)."""
+    lib = _abi.load_library()
+    q = t4(SHAPE)
+    ha = (ctypes.c_int32 * 2)(0, 5)
+    need_att = _abi.attention_workspace_bytes(1, 4, 256, 96)
+    need_est = _abi.estimate_workspace_bytes(1, 1, 256, 256, 96)
+
+    def call(n_slots=1, heads_arr=ha, est_ws=FAKE, est_b=need_est, ws=FAKE, wsb=need_att, k=q):
+        return lib.msa_stage_kv_pool(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k),
+                                     heads_arr, n_slots, est_ws, est_b, ws, wsb, None)
+
+    assert call(wsb=need_att - 1) == _abi.MSA_E_WORKSPACE
+    assert call(est_b=need_est - 1) == _abi.MSA_E_WORKSPACE
+    assert call(est_ws=None) == _abi.MSA_E_WORKSPACE
+    assert call(n_slots=2) == _abi.MSA_E_HEADS  # head 5 of 4
+    assert call(n_slots=-1) == _abi.MSA_E_HEADS
+    assert call(heads_arr=None) == _abi.MSA_E_NULL
+    assert call(k=t4([1, 4, 256, 80])) == _abi.MSA_E_HEAD_DIM
 
 
 def test_one_pass_estimate_needs_caller_workspace():

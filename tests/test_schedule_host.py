@@ -46,12 +46,16 @@ def test_block_layer_schedule(monkeypatch):
     def stage_kv(k, v, ws, kv_heads=None):
         log.append(("stage", current[-1].name))
 
+    def stage_kv_pool(q, k, v, slot_heads, est_ws, ws):
+        log.append(("stage+pool", current[-1].name, tuple(slot_heads), est_ws))
+
     def layer_attention(q, k, v, out, heads, **kw):
         log.append(("attention", current[-1].name, len(heads), kw.get("staged"),
                     kw.get("idx_slots")))
 
     monkeypatch.setattr(mf._abi, "block_estimate", block_estimate)
     monkeypatch.setattr(mf._abi, "stage_kv", stage_kv)
+    monkeypatch.setattr(mf._abi, "stage_kv_pool", stage_kv_pool)
     monkeypatch.setattr(mf._abi, "layer_attention", layer_attention)
 
     pats = {0: ["stream_llm", 64, 256, 1], 1: ["block_sparse", 4, 0, 1], 2: ["dense", 0, 0, 1],
@@ -62,16 +66,13 @@ def test_block_layer_schedule(monkeypatch):
     mf.launch_block_layer(q, q, q, plan, q, None, None, None, "est-ws",
                           flags=_abi.MSA_SELECT_FORCE_DIAG,
                           mark=lambda name, st: marks.append((name, st.name)))
-    pool = _abi.MSA_ESTIMATE_POOL_ONLY | _abi.MSA_SELECT_FORCE_DIAG
     select = _abi.MSA_ESTIMATE_SELECT_ONLY | _abi.MSA_SELECT_FORCE_DIAG
     assert log == [
-        ("estimate", "main", pool, (1, 3), True),       # pooling first, on the main stream
-        ("wait", "side", "main"),                       # the side stream follows the pooling
-        ("estimate", "side", select, (1, 3), True),     # selection beside the staging
-        ("stage", "main"),
-        ("wait", "main", "side"),                       # attention after the selection
+        ("stage+pool", "main", (1, 3), "est-ws"),       # staging + pooling, one launch
+        ("estimate", "main", select, (1, 3), True),     # then the selection, same stream
         ("attention", "main", 4, True, 2),              # one launch of all heads
     ]
-    assert [m[0] for m in marks] == ["start", "est0", "est1", "stage0", "stage1", "attn0",
+    # one stream, no cross-stream waits
+    assert [m[0] for m in marks] == ["start", "stage0", "stage1", "est0", "est1", "attn0",
                                      "attn0_end"]
-    assert dict(marks)["est1"] == "side"
+    assert {st for _, st in marks} == {"main"}
