@@ -558,12 +558,15 @@ void attn_kernel(AttnParams P) {
       gvrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.gvt + gb), short(0),
                                                P.nv_pad * D * 2, 0x00020000);
     }
-    // the item's rows of Q: row q0 + r at byte r * q_ss * 2; rows past S_q lie
-    // beyond the record count and load as zeros
+    // the item's rows of Q: row q0 + r at byte r * q_ss * 2.  The record
+    // count ends at the last row's last element, so every load of a row past
+    // S_q either lies beyond it (zeros) or reads memory of the view (a row
+    // stride below D: overlapping or repeated rows); rows past S_q feed only
+    // their own, never stored, outputs.
     qrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb +
                               int64_t(h) * P.q_sh + int64_t(q0) * P.q_ss),
-        short(0), int(nrows * P.q_ss * 2), 0x00020000);
+        short(0), int(((nrows - 1) * P.q_ss + D) * 2), 0x00020000);
     c_log2 = P.hd[h].scale_log2;
     arow0 = a0 + lc;  // absolute position of this lane's row in group 0
     is_full = kind == KIND_FULL;

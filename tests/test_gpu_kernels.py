@@ -73,8 +73,8 @@ def test_estimator_bit_exact(gpu_device, case):
 
 
 def test_estimator_long_key_axis(gpu_device):
-    """More than 2048 key blocks (S = 200000): the selection reads its keys
-    from LDS instead of registers; ids bit-exact with the oracle."""
+    """More than 2048 key blocks (S = 200000): the selection keeps its keys
+    in the workspace instead of registers; ids bit-exact with the oracle."""
     from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
 
     S, topk = 200000, 160
@@ -85,6 +85,36 @@ def test_estimator_long_key_axis(gpu_device):
     got = idx.cpu().numpy()
     assert np.array_equal(cnt.cpu().numpy(), rcnt)
     assert np.array_equal(got, ridx), f"{(got != ridx).sum()} ids differ"
+
+
+@pytest.mark.parametrize("first,diag", [(False, False), (True, True), (False, True)])
+def test_estimator_non_finite_scores(gpu_device, first, diag):
+    """NaN and infinite pooled scores (a NaN key, a row of infinite keys, a
+    zero query block against it: 0 * inf): NaN ranks above +inf, as
+    torch.topk orders it, and forced ids rank above NaN; ids bit-exact with
+    the oracle (such rows take the exact fp64 path)."""
+    from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
+
+    S, D, topk = 64 * 24, 96, 4
+    q, k, _ = make_qkv(1, 2, S, S, D, torch.bfloat16, seed=5)
+    k[0, 0, 64 * 3 + 5, 7] = float("nan")   # block 3 of head 0: NaN in every row's score
+    k[0, 1, 64 * 5 + 1, :] = float("inf")   # block 5 of head 1: +-inf or NaN scores
+    k[0, 1, 64 * 9 + 2, :48] = float("inf")
+    k[0, 1, 64 * 9 + 2, 48:] = float("-inf")
+    q[0, 1, 64 * 10:64 * 11] = 0.0          # query block 10 of head 1: 0 * inf
+    idx, cnt = select_block_sparse_topk_indices(*to_dev(gpu_device, q, k), topk,
+                                                return_counts=True, force_first=first,
+                                                force_diag=diag)
+    ridx, rcnt = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, "bf16",
+                                                    force_first=first, force_diag=diag)
+    got = idx.cpu().numpy()
+    assert np.array_equal(cnt.cpu().numpy(), rcnt)
+    assert np.array_equal(got, ridx), f"{(got != ridx).sum()} ids differ"
+    if not first:
+        # head 0: the NaN block is selected in every row that sees it (and
+        # no forced id outranks it unless the diagonal is forced)
+        for bq in range(3, 24):
+            assert 3 in got[0, 0, bq, :topk]
 
 
 def test_estimator_ties_to_lower_id(gpu_device):
@@ -432,3 +462,29 @@ def test_mixed_layer_strided_views(gpu_device, S, H, H_kv):
     vr = np.repeat(np32(v), rep, axis=1)
     ref, _ = O.layer_attention(np32(q), kr, vr, [pats[h] for h in range(H)], "bf16")
     assert_close_f32(out_bshd.transpose(1, 2), ref, what=f"mixed layer S={S} H={H} Hkv={H_kv}")
+
+
+@pytest.mark.parametrize("S", [200, 1000])
+def test_mixed_layer_repeated_query_rows(gpu_device, S):
+    """q views whose row stride is below D: an expanded q (stride 0, every
+    row the same) and overlapping rows (stride D/2) are read as the tensor
+    the view describes, against the oracle on the materialised q."""
+    from minference.modules.minference_forward import build_layer_plan, run_layer_attention
+
+    H, D = 4, 96
+    pats = _mixed_patterns(H)
+    q, k, v = make_qkv(1, H, S, S, D, torch.bfloat16, seed=S, sink_scale=8.0)
+    plan = build_layer_plan(pats, H, D, S)
+    dk, dv = k.to(gpu_device), v.to(gpu_device)
+    base = q[:, :, :1].to(gpu_device)
+    flat = q.reshape(1, H, -1)[:, :, :(S + 1) * D // 2].contiguous().to(gpu_device)
+    views = {
+        "expanded": base.expand(1, H, S, D),
+        "overlapping": flat.as_strided((1, H, S, D), (H * flat.shape[-1], flat.shape[-1], D // 2, 1)),
+    }
+    for name, dq in views.items():
+        out = torch.empty((1, H, S, D), dtype=torch.float32, device=gpu_device)
+        run_layer_attention(dq, dk, dv, plan, out)
+        ref, _ = O.layer_attention(np32(dq.cpu().contiguous()), np32(k), np32(v),
+                                   [pats[h] for h in range(H)], "bf16")
+        assert_close_f32(out, ref, what=f"{name} q rows S={S}")

@@ -168,6 +168,43 @@ def test_selector_forced_known_answer():
         assert list(both1[0, 0, bq, :1]) == [0]
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_selector_nan_order_vs_torch_topk(seed):
+    """NaN scores rank above every number, +inf included, with ties between
+    NaNs to the lower id: the selection equals torch.topk's (the library
+    call of the reference, block_sparse_kernel_npu.py:262) on rows of
+    distinct finite values, +-inf and NaN entries."""
+    rng = np.random.default_rng(seed)
+    n_bq = n_bk = 40
+    sc = rng.permutation(n_bq * n_bk).reshape(n_bq, n_bk).astype(np.float32) * 1e-3 - 0.8
+    sc[rng.random(sc.shape) < 0.08] = np.nan
+    sc[rng.random(sc.shape) < 0.03] = np.inf
+    sc[rng.random(sc.shape) < 0.03] = -np.inf
+    for topk in (1, 3, 7):
+        idx, cnt = O.select_topk(sc[None], topk)
+        for bq in range(n_bq):
+            n = bq + 1
+            row = torch.from_numpy(sc[bq, :n].copy())
+            # torch.topk orders equal values (+-inf here) by its own rule:
+            # compare on rows where the k-th pick is not tied
+            vals, ids = torch.topk(row, min(topk, n))
+            kth = vals[-1].item()
+            rest = row[[i for i in range(n) if i not in ids.tolist()]]
+            if (not math.isnan(kth) and (rest == kth).any()) or (
+                    math.isnan(kth) and torch.isnan(rest).any()):
+                continue
+            assert sorted(ids.tolist()) == list(idx[0, bq, :cnt[0, bq]]), (topk, bq)
+
+
+def test_selector_forced_above_nan():
+    """Forced ids rank above NaN scores (this build's selector option)."""
+    sc = np.full((1, 6, 6), np.nan, dtype=np.float32)
+    idx, cnt = O.select_topk(sc, 2, force_first=True, force_diag=True)
+    for bq in range(6):
+        want = [0] if bq == 0 else [0, bq]
+        assert list(idx[0, bq, :cnt[0, bq]]) == want
+
+
 @pytest.mark.parametrize("first,diag,topk", [(True, True, 5), (False, True, 3), (True, False, 1),
                                              (True, True, 2)])
 def test_selector_forced_bruteforce(first, diag, topk):
