@@ -26,6 +26,9 @@ something other than its own formula):
                         per-row brute force over the expanded token set
   dense_causal        : torch scaled_dot_product_attention in fp64 (is_causal
                         True and False)
+  rows_attention and the *_rows_visible rules : every row of small heads equal to
+                        streaming_attention / block_sparse_from_indices /
+                        dense_causal, rows given in any grouping
   rope_rotate_half    : HF Phi-3's apply_rotary_pos_emb on CPU torch in bf16 / fp16
                         (the call the reference makes), bit for bit, full and
                         partial rotary; in fp64 a norm-preserving rotation of
@@ -53,6 +56,9 @@ __all__ = [
     "select_block_sparse_topk_indices",
     "attend_count",
     "vs_sizes",
+    "vs_logits",
+    "vs_probs",
+    "vs_diagonal_sums",
     "vs_scores",
     "vs_estimate",
     "vs_token_visible",
@@ -64,6 +70,10 @@ __all__ = [
     "block_sparse_from_indices",
     "dense_causal",
     "masked_attention",
+    "rows_attention",
+    "stream_rows_visible",
+    "block_rows_visible",
+    "causal_rows_visible",
     "layer_attention",
     "stream_pairs",
     "block_tiles",
@@ -276,23 +286,13 @@ def vs_sizes(s: int, vertical_size: int, slash_size: int):
     return min(s, max(int(vertical_size), 30)), min(s, max(int(slash_size), 50))
 
 
-def vs_scores(q: np.ndarray, k: np.ndarray, dtype: str):
-    """Column sums and anti-diagonal sums of the last-rows attention of one
-    head (:148-164).  q, k: [S, D] with S_q == S_k.
-
-    * scores: q[-n:] . k^T formed in fp64 (exact for 16-bit operands), rounded
-      to fp32 and to the input dtype (the reference's matmul output dtype),
-      then divided by fp32(sqrt(D)) and rounded to the input dtype again
-      (``/ math.sqrt(D)`` on a bf16/fp16 tensor);
-    * the last n columns get the causal mask of :150-151 (row r sees column
-      S - n + c iff c <= r);
-    * softmax in fp64 (the reference's fp32 softmax, here without its
-      rounding), then column sums and the sums along each diagonal
-      t = 0 .. S-1 (t indexes sum_all_diagonal_matrix's output, :124-137,
-      truncated at :161-162), each rounded once to fp32;
-    * the first 30 columns and the last 100 diagonals are set to +inf.
-
-    Returns (vertical [S] fp32, slash [S] fp32)."""
+def vs_logits(q: np.ndarray, k: np.ndarray, dtype: str) -> np.ndarray:
+    """Last-rows logits of one head (:149-151), q, k [S, D] with S_q == S_k:
+    q[-n:] . k^T formed in fp64 (exact for 16-bit operands), rounded to fp32
+    and to the input dtype (the reference's matmul output dtype), divided by
+    fp32(sqrt(D)) and rounded to the input dtype again (``/ math.sqrt(D)`` on
+    a bf16/fp16 tensor); the last n columns carry the causal mask (row r
+    sees column S - n + c iff c <= r) as -inf.  Returns x [n, S] fp64."""
     S, D = k.shape
     n = min(LAST_Q, S)
     ql = np.asarray(q[S - n:], dtype=np.float64)
@@ -301,16 +301,43 @@ def vs_scores(q: np.ndarray, k: np.ndarray, dtype: str):
     x = round_to(a / np.float32(math.sqrt(D)), dtype).astype(np.float64)
     r = np.arange(n)[:, None]
     c = np.arange(S)[None, :] - (S - n)
-    x = np.where(c > r, -np.inf, x)
+    return np.where(c > r, -np.inf, x)
+
+
+def vs_probs(x: np.ndarray) -> np.ndarray:
+    """Row softmax of vs_logits in fp64 (the reference's fp32 softmax of
+    :152, here without its rounding)."""
     m = x.max(axis=1, keepdims=True)
     e = np.exp(x - m)
-    p = e / e.sum(axis=1, keepdims=True)
-    vert = p.sum(axis=0).astype(np.float32)
+    return e / e.sum(axis=1, keepdims=True)
+
+
+def vs_diagonal_sums(p: np.ndarray) -> np.ndarray:
+    """Sums of p [n, S] along each diagonal t = 0 .. S-1 in fp64: element
+    (i, i + t + 1 - n) for every row i where that column exists
+    (sum_all_diagonal_matrix's output, :124-137, truncated at :161-162)."""
+    n, S = p.shape
     slash = np.zeros(S)
     for i in range(n):
         lo = n - 1 - i                     # first diagonal that meets row i
-        slash[lo:] += p[i, : S - lo]       # column i + t + 1 - n for t = lo .. S-1
-    slash = slash.astype(np.float32)
+        slash[lo:] += p[i, : S - lo]
+    return slash
+
+
+def vs_scores(q: np.ndarray, k: np.ndarray, dtype: str):
+    """Column sums and anti-diagonal sums of the last-rows attention of one
+    head (:148-164).  q, k: [S, D] with S_q == S_k.
+
+    * the logits of vs_logits;
+    * softmax in fp64 (vs_probs), then column sums and the diagonal sums of
+      vs_diagonal_sums, each rounded once to fp32;
+    * the first 30 columns and the last 100 diagonals are set to +inf.
+
+    Returns (vertical [S] fp32, slash [S] fp32)."""
+    S = k.shape[0]
+    p = vs_probs(vs_logits(q, k, dtype))
+    vert = p.sum(axis=0).astype(np.float32)
+    slash = vs_diagonal_sums(p).astype(np.float32)
     vert[:VS_SINK_COLS] = np.inf
     slash[max(0, S - VS_LOCAL_DIAGS):] = np.inf
     return vert, slash
@@ -427,6 +454,104 @@ def masked_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, visible: np.nd
     den = p.sum(axis=-1, keepdims=True)
     out = (p @ v.astype(acc)) / np.where(den > 0, den, 1.0)
     return np.where(den > 0, out, 0.0).astype(acc)
+
+
+def rows_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, rows: np.ndarray, visible,
+                   scale: float, keys=None, group: int = 64, acc=np.float64) -> np.ndarray:
+    """Output rows ``rows`` of one head (q [S_q, D], k/v [S_k, D], S_q == S_k):
+    masked_attention restricted to those rows, ``group`` rows at a time, for
+    full-length checks that sample rows.  ``visible(rows_g, keys_g) -> bool
+    [len(rows_g), len(keys_g)]`` is the head's token visibility;
+    ``keys(rows_g)`` (ascending key ids that may be visible to any of the
+    rows; default every key up to the last row) only narrows the product.
+    Rows that see no key give 0 (masked_attention's rule).  The logits and
+    the gathered keys / values live in buffers reused across groups."""
+    rows = np.asarray(rows, dtype=np.int64)
+    D = q.shape[1]
+    out = np.zeros((rows.size, D), dtype=acc)
+    bufs = {}
+
+    def buf(name, shape, dtype):
+        n = int(np.prod(shape))
+        b = bufs.get(name)
+        if b is None or b.size < n:
+            b = bufs[name] = np.empty(max(n, 2 * (0 if b is None else b.size)), dtype=dtype)
+        return b[:n].reshape(shape)
+
+    for g0 in range(0, rows.size, group):
+        rg = rows[g0:g0 + group]
+        kg = np.arange(int(rg.max()) + 1) if keys is None else np.asarray(keys(rg), np.int64)
+        n = kg.size
+        if n == 0:
+            continue
+        kk, vv = buf("k", (n, D), acc), buf("v", (n, D), acc)
+        if kg[-1] - kg[0] + 1 == n:            # a key range
+            kk[...] = k[kg[0]:kg[-1] + 1]
+            vv[...] = v[kg[0]:kg[-1] + 1]
+        else:
+            kk[...] = np.take(k, kg, axis=0, out=buf("g", (n, D), k.dtype))
+            vv[...] = np.take(v, kg, axis=0, out=buf("g", (n, D), v.dtype))
+        lg = buf("lg", (rg.size, n), acc)
+        np.matmul(q[rg].astype(acc), kk.T, out=lg)
+        lg *= acc(scale)
+        np.copyto(lg, -np.inf, where=np.logical_not(visible(rg, kg)))
+        m = lg.max(axis=-1)
+        m = np.where(np.isfinite(m), m, 0.0)
+        lg -= m[:, None]
+        np.exp(lg, out=lg)
+        den = lg.sum(axis=-1)
+        o = lg @ vv
+        out[g0:g0 + rg.size] = np.where(den[:, None] > 0, o / np.where(den > 0, den, 1.0)[:, None],
+                                        0.0)
+    return out
+
+
+def stream_rows_visible(n_init: int, n_local: int):
+    """visible(rows, keys) and keys(rows) of a stream_llm head (S_q == S_k):
+    j <= i and (j > i - n_local or j < n_init), stream_visible's rule."""
+    def visible(rows, keys):
+        a = rows[:, None]
+        j = keys[None, :]
+        return (j <= a) & ((j > a - n_local) | (j < n_init))
+
+    def keys(rows):
+        lo = max(0, int(rows.min()) - n_local + 1)
+        return np.concatenate([np.arange(min(n_init, lo)), np.arange(lo, int(rows.max()) + 1)])
+
+    return visible, keys
+
+
+def block_rows_visible(idx_row: np.ndarray, cnt_row: np.ndarray | None, s_k: int,
+                       block: int = BLOCK):
+    """visible(rows, keys) and keys(rows) of a block_sparse head from its ids
+    idx_row [n_bq, topk] (the first cnt_row[bq] of each row when given; ids
+    outside [0, n_kv_blocks) ignored) intersected with j <= i:
+    block_token_visible's rule (S_q == S_k).  keys(rows) lists the keys of
+    the blocks any of the rows attends."""
+    n_bq = idx_row.shape[0]
+    n_bk = -(-s_k // block)
+    ids = np.asarray(idx_row, dtype=np.int64)
+    use = (ids >= 0) & (ids < n_bk)
+    if cnt_row is not None:
+        use &= np.arange(ids.shape[1])[None, :] < np.asarray(cnt_row)[:, None]
+    attend = np.zeros((n_bq, n_bk), dtype=bool)
+    r, c = np.nonzero(use)
+    attend[r, ids[r, c]] = True
+
+    def visible(rows, keys):
+        return attend[(rows // block)[:, None], (keys // block)[None, :]] & (keys[None, :] <= rows[:, None])
+
+    def keys(rows):
+        blocks = np.nonzero(attend[rows // block].any(axis=0))[0]
+        js = (blocks[:, None] * block + np.arange(block)[None, :]).ravel()
+        return js[js <= int(rows.max())]
+
+    return visible, keys
+
+
+def causal_rows_visible(rows, keys):
+    """visible(rows, keys) of a causal dense head: j <= i."""
+    return keys[None, :] <= rows[:, None]
 
 
 def _heads(x: np.ndarray):

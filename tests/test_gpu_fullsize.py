@@ -5,8 +5,11 @@ config 1: stream_llm, 32 heads, S=4096, 64 sinks + 1024 band, RoPE (theta
 here the fused RoPE and the stream kernel run on bf16 inputs).
 config 2: block_sparse, 32 heads, S=16384, top-100, K rows 0-3 x8.
 config 3: stream_llm, 32 heads, S=65536, 128 sinks + 4096 band.
-Block ids are compared with the oracle in full; outputs on sampled rows
-(every kind of tile boundary) and through size-independent properties."""
+Block ids are compared with the oracle in full; outputs against the
+oracle's fp64 rows on every row of every head (config 1 and config 2) or 8
+rows in every query block of every head (config 3, config 2 with forced
+blocks), plus every kind of tile boundary, and through size-independent
+properties."""
 
 from __future__ import annotations
 
@@ -17,6 +20,7 @@ import pytest
 import torch
 
 import oracle as O
+import row_sampling as RS
 from msa_data import rope
 
 pytestmark = pytest.mark.gpu
@@ -56,6 +60,27 @@ def oracle_rows(q, k, v, rows, visible_fn, scale):
     return np.stack(out)
 
 
+def check_block_heads(tag, qn, kn, vn, og, ridx, rcnt, heads, per_block):
+    """per_block rows of every query block of every listed head (plus the
+    boundary rows) against the oracle's fp64 rows under the head's oracle
+    block ids."""
+    S, D = qn.shape[2], qn.shape[3]
+    scale = O.sparse_scale(D)
+    extra = rows_for(S, extra=(64 * 99, 64 * 100 + 5, 64 * 200 + 17))
+
+    def check(h):
+        rows = RS.block_rows(S, h, per_block=per_block, extra=extra)
+        ref = RS.head_rows_reference(qn[0, h], kn[0, h], vn[0, h], rows, RS.BLOCK, 0, 0, scale,
+                                     ridx[0, h], rcnt[0, h])
+        return h, rows.size, float(np.abs(og[0, h, rows] - ref).max())
+
+    res = RS.map_heads(check, heads, tag=tag)
+    print(f"{tag} {sum(r[1] for r in res)} rows, worst error {max(r[2] for r in res):.3e}",
+          flush=True)
+    for h, n, err in res:
+        assert err < TOL, (h, n, err)
+
+
 def test_cfg2_block_ids_bit_exact_and_rows(gpu_device):
     from minference.ops.block_sparse_kernel import (block_sparse_attention_with_indices,
                                                     select_block_sparse_topk_indices)
@@ -75,17 +100,7 @@ def test_cfg2_block_ids_bit_exact_and_rows(gpu_device):
     out = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
     block_sparse_attention_with_indices(q, k, v, idx, out=out)
     og = out.cpu().numpy()
-    scale = O.sparse_scale(D)
-    rows = rows_for(S, extra=(64 * 99, 64 * 100 + 5, 64 * 200 + 17))
-    for h in range(0, H, 5):
-        def vis(r, h=h):
-            bq = r // 64
-            ids = ridx[0, h, bq, :rcnt[0, h, bq]]
-            js = np.concatenate([np.arange(64 * b, 64 * b + 64) for b in ids])
-            return js[js <= r]
-        ref = oracle_rows(qn[0, h], kn[0, h], vn[0, h], rows, vis, scale)
-        err = np.abs(og[0, h, rows] - ref).max()
-        assert err < TOL, (h, err)
+    check_block_heads("[cfg2]", qn, kn, vn, og, ridx, rcnt, range(H), per_block=64)  # every row
 
 
 def test_cfg2_as_worded_forced_first_and_diagonal(gpu_device):
@@ -93,7 +108,7 @@ def test_cfg2_as_worded_forced_first_and_diagonal(gpu_device):
     the diagonal and the first block always included (the selector option
     FORCE_FIRST | FORCE_DIAG, inside the top-k).  All 32 heads x 256 query
     blocks bit-exact with the oracle; then block_sparse_attention with the
-    option against the oracle on sampled rows."""
+    option against the oracle on 8 rows per query block of every head."""
     from minference import block_sparse_attention
     from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
 
@@ -119,17 +134,7 @@ def test_cfg2_as_worded_forced_first_and_diagonal(gpu_device):
     out = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
     block_sparse_attention(q, k, v, topk, out=out, force_first=True, force_diag=True)
     og = out.cpu().numpy()
-    scale = O.sparse_scale(D)
-    rows = rows_for(S, extra=(64 * 99, 64 * 100 + 5, 64 * 200 + 17))
-    for h in range(1, H, 6):
-        def vis(r, h=h):
-            bq = r // 64
-            ids = ridx[0, h, bq, :rcnt[0, h, bq]]
-            js = np.concatenate([np.arange(64 * b, 64 * b + 64) for b in ids])
-            return js[js <= r]
-        ref = oracle_rows(qn[0, h], kn[0, h], vn[0, h], rows, vis, scale)
-        err = np.abs(og[0, h, rows] - ref).max()
-        assert err < TOL, (h, err)
+    check_block_heads("[cfg2 forced]", qn, kn, vn, og, ridx, rcnt, range(H), per_block=8)
 
 
 def test_cfg1_rope_then_stream_all_rows(gpu_device):
@@ -144,16 +149,22 @@ def test_cfg1_rope_then_stream_all_rows(gpu_device):
                for _ in range(3))
     cos, sin = (t.to(gpu_device) for t in rope_tables(1, S, D, torch.bfloat16, theta=10000.0))
     qr, kr = apply_rotary_pos_emb(q, k, cos, sin)
-    heads = [0, 9, 20, 31]
     cn, sn = cos.float().cpu().numpy(), sin.float().cpu().numpy()
-    qn = O.rope_rotate_half(q[:, heads].float().cpu().numpy(), cn, sn, "bf16")
-    kn = O.rope_rotate_half(k[:, heads].float().cpu().numpy(), cn, sn, "bf16")
-    assert np.array_equal(qr[:, heads].float().cpu().numpy(), qn)
-    assert np.array_equal(kr[:, heads].float().cpu().numpy(), kn)
+    qn = O.rope_rotate_half(q.float().cpu().numpy(), cn, sn, "bf16")
+    kn = O.rope_rotate_half(k.float().cpu().numpy(), cn, sn, "bf16")
+    assert np.array_equal(qr.float().cpu().numpy(), qn)
+    assert np.array_equal(kr.float().cpu().numpy(), kn)
     out = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
     streaming_forward(qr, kr, v, n_init, n_local, out=out)
-    ref = O.streaming_attention(qn, kn, v[:, heads].float().cpu().numpy(), n_init, n_local)
-    err = np.abs(out[:, heads].cpu().numpy() - ref).max()
+    og, vn = out[0].cpu().numpy(), v[0].float().cpu().numpy()
+    rows = np.arange(S)
+
+    def check(h):   # every row of every head
+        ref = RS.head_rows_reference(qn[0, h], kn[0, h], vn[h], rows, RS.STREAM, n_init,
+                                     n_local, O.sparse_scale(D))
+        return float(np.abs(og[h] - ref).max())
+
+    err = max(RS.map_heads(check, range(H), tag="[cfg1]"))
     assert err < TOL, err
     vc = torch.full_like(v, -1.25)
     assert torch.all(streaming_forward(qr, kr, vc, n_init, n_local) == -1.25)
@@ -168,18 +179,22 @@ def test_cfg3_stream_rows_and_properties(gpu_device):
     out = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
     streaming_forward(q, k, v, n_init, n_local, out=out)
     scale = O.sparse_scale(D)
-    rows = rows_for(S, extra=(n_local - 1, n_local, n_local + 63, n_local + 64, n_local + 127))
-    for h in (0, 7, 31):
-        qn, kn, vn = (t[0, h].float().cpu().numpy() for t in (q, k, v))
-
-        def vis(r):
-            lo = max(0, r - n_local + 1)
-            return np.union1d(np.arange(min(n_init, r + 1)), np.arange(lo, r + 1))
-
-        ref = oracle_rows(qn, kn, vn, rows, vis, scale)
-        err = np.abs(out[0, h, rows].cpu().numpy() - ref).max()
-        assert err < TOL, (h, err)
+    extra = rows_for(S, extra=(n_local - 1, n_local, n_local + 63, n_local + 64, n_local + 127))
+    qn, kn, vn, og = (t[0].float().cpu().numpy() for t in (q, k, v, out))
     del out
+
+    def check(h):
+        rows = RS.block_rows(S, h, per_block=8, extra=extra)
+        ref = RS.head_rows_reference(qn[h], kn[h], vn[h], rows, RS.STREAM, n_init, n_local,
+                                     scale)
+        return h, rows.size, float(np.abs(og[h, rows] - ref).max())
+
+    res = RS.map_heads(check, range(H), tag="[cfg3]")
+    print(f"[cfg3] {sum(r[1] for r in res)} rows, worst error {max(r[2] for r in res):.3e}",
+          flush=True)
+    for h, n, err in res:
+        assert err < TOL, (h, n, err)
+    del qn, kn, vn, og
 
     # constant V: every row's output is that constant (normalisation, all rows)
     print("[cfg3] constant-V property", flush=True)

@@ -7,9 +7,11 @@ bench's own schedule (launch_block_layer: estimator pooling, selection beside
 the K/V staging, one attention launch with the plan's kind-interleaved,
 cost-balanced item order; the fp32 output by a second launch).  Checked here:
   * block ids of all 16 block heads bit-exact with the oracle;
-  * sampled rows of every head (tile boundaries, the sink edge, the band
-    start, the last rows) within 2e-3 of the oracle, in fp32 output and in
-    the bf16 output the bench writes (plus one bf16 rounding);
+  * 8 rows in every query block of every head (8192 x 32 rows, at
+    offsets that move with the block and the head) plus the tile
+    boundaries, the sink edge, the band start and the last rows, within
+    2e-3 of the oracle's fp64 rows, in fp32 output and in the bf16 output
+    the bench writes (plus one bf16 rounding);
   * every row of every head through a constant-V launch (the output of a
     softmax-weighted mean of a constant is that constant).
 Reference semantics: minference/ops/streaming_kernel_npu.py:94-146,
@@ -24,6 +26,7 @@ import pytest
 import torch
 
 import oracle as O
+import row_sampling as RS
 
 pytestmark = pytest.mark.gpu
 
@@ -72,38 +75,28 @@ def test_headline_launch_matches_oracle(gpu_device):
     assert np.array_equal(cnt.cpu().numpy()[0], rcnt)
     assert np.array_equal(got_idx, ridx), f"{(got_idx != ridx).sum()} block ids differ"
 
-    print("[headline] sampled rows of every head", flush=True)
+    print("[headline] 8 rows per query block of every head", flush=True)
     o32 = out32.cpu().numpy()[0]
     o16 = out16.float().cpu().numpy()[0]
     sc = sparse_scale(D)
-    worst = 0.0
-    for h in range(H):
+
+    def check(h):
         kind, p1, p2, slot, _ = plan.heads[h]
-        if kind == _abi.MSA_KIND_STREAM:
-            rows = _rows(p1, p2)
+        assert kind in (_abi.MSA_KIND_STREAM, _abi.MSA_KIND_BLOCK)
+        rows = RS.block_rows(S, h, per_block=8, extra=_rows(128, 4096))
+        ids = ridx[slot] if kind == _abi.MSA_KIND_BLOCK else None
+        cn = rcnt[slot] if kind == _abi.MSA_KIND_BLOCK else None
+        ref = RS.head_rows_reference(qn[h], kn[h], vn[h], rows, kind, p1, p2, sc, ids, cn)
+        err = np.abs(o32[h, rows] - ref)
+        bad16 = np.abs(o16[h, rows] - ref) > TOL + np.abs(ref) * 2.0 ** -8
+        return h, kind, rows.size, float(err.max()), int((err >= TOL).sum()), int(bad16.sum())
 
-            def vis(r, n_init=p1, n_local=p2):
-                j = np.arange(r + 1)
-                return j[(j > r - n_local) | (j < n_init)]
-        else:
-            assert kind == _abi.MSA_KIND_BLOCK
-            rows = _rows(128, 4096)
-
-            def vis(r, s=slot):
-                bq = r // 64
-                ids = ridx[s, bq, :rcnt[s, bq]]
-                j = (ids[:, None] * 64 + np.arange(64)[None, :]).ravel()
-                return j[j <= r]
-        for r in rows:
-            js = vis(r)
-            lg = kn[h, js].astype(np.float64) @ qn[h, r].astype(np.float64) * sc
-            p = np.exp(lg - lg.max())
-            ref = (p / p.sum()) @ vn[h, js].astype(np.float64)
-            err = np.abs(o32[h, r] - ref).max()
-            worst = max(worst, err)
-            assert err < TOL, (h, kind, r, err)
-            assert (np.abs(o16[h, r] - ref) <= TOL + np.abs(ref) * 2.0 ** -8).all(), (h, r)
-    print(f"[headline] worst sampled error {worst:.3e}", flush=True)
+    res = RS.map_heads(check, range(H), tag="[headline]")
+    n_rows = sum(r[2] for r in res)
+    worst = max(r[3] for r in res)
+    print(f"[headline] {n_rows} rows, worst error {worst:.3e}", flush=True)
+    for h, kind, n, err, n_bad, n_bad16 in res:
+        assert n_bad == 0 and n_bad16 == 0, (h, kind, n, err, n_bad, n_bad16)
 
     print("[headline] constant V, every row", flush=True)
     c = (torch.arange(H, device=gpu_device, dtype=torch.float32) * 0.25 + 0.5)

@@ -5,10 +5,10 @@ A random-init Phi-3-mini-128k-shaped model (hidden 3072, 32 heads x 96, MLP
 through the patched forward with the configs' seeded per-head mixes at their
 full lengths: 32768 tokens with 30 % stream_llm(128, 4096) / 60 %
 block_sparse(top-100) / 10 % dense, and 131072 tokens with 50 % stream_llm(128,
-8192) / 50 % block_sparse(top-160).  Every layer launch is captured; on
-sampled rows of sampled heads of each kind its output is compared with the
-oracle on the very q/k/v the model produced (block ids from the oracle
-selector), within the bf16-output bound."""
+8192) / 50 % block_sparse(top-160).  Every layer launch is captured; on one
+row in every query block of every head (plus boundary rows) its output is
+compared with the oracle's fp64 rows on the very q/k/v the model produced
+(block ids from the oracle selector), within the bf16-output bound."""
 
 from __future__ import annotations
 
@@ -17,6 +17,7 @@ import pytest
 import torch
 
 import oracle as O
+import row_sampling as RS
 from minference import MInference
 from minference import _abi
 from minference.configs import patterns as P
@@ -45,53 +46,38 @@ def phi3_mini_shaped(dev, layers):
     return model.eval()
 
 
-def sample_rows(S, extra=()):
-    base = {0, 1, 63, 64, 127, 128, 129, 4095, 4096, 4097, 4224, 8191, 8192, 8320,
+def sample_rows(S):
+    return {0, 1, 63, 64, 127, 128, 129, 4095, 4096, 4097, 4224, 8191, 8192, 8320,
             S // 3, S // 2 + 17, S - 65, S - 64, S - 1}
-    return sorted(r for r in base.union(extra) if 0 <= r < S)
 
 
-def row_oracle(qh, kh, vh, rows, vis, scale):
-    out = []
-    for r in rows:
-        js = vis(r)
-        lg = kh[js] @ qh[r] * scale
-        p = np.exp(lg - lg.max())
-        out.append((p / p.sum()) @ vh[js])
-    return np.stack(out)
-
-
-def check_layer(q, k, v, plan, got, per_kind=3):
+def check_layer(tag, q, k, v, plan, got):
+    """Every head of the layer: one row per query block plus the sampled
+    boundary rows, against the oracle's fp64 rows (block ids from the oracle
+    selector on that head), within the bf16-output bound."""
     S = q.shape[2]
-    rows = sample_rows(S)
-    by_kind = {}
-    for h, hd in enumerate(plan.heads):
-        by_kind.setdefault(hd[0], []).append(h)
-    for kind, heads in by_kind.items():
-        for h in heads[:: max(1, len(heads) // per_kind)][:per_kind]:
-            kind_, p1, p2, slot, scale = plan.heads[h]
-            qh, kh, vh = (t[0, h].double().cpu().numpy() for t in (q, k, v))
-            if kind == _abi.MSA_KIND_STREAM:
-                def vis(r, p1=p1, p2=p2):
-                    return np.union1d(np.arange(min(p1, r + 1)), np.arange(max(0, r - p2 + 1), r + 1))
-            elif kind == _abi.MSA_KIND_BLOCK:
-                idx, cnt = O.select_block_sparse_topk_indices(
-                    q[:, h:h + 1].float().cpu().numpy(), k[:, h:h + 1].float().cpu().numpy(),
-                    p1, "bf16", scale)
+    qn, kn, vn = (t[0].float().cpu().numpy() for t in (q, k, v))
+    gn = got[0].float().cpu().numpy()
 
-                def vis(r, idx=idx, cnt=cnt):
-                    bq = r // 64
-                    ids = idx[0, 0, bq, :cnt[0, 0, bq]]
-                    js = np.concatenate([np.arange(64 * b, 64 * b + 64) for b in ids])
-                    return js[js <= r]
-            else:
-                def vis(r):
-                    return np.arange(r + 1)
-            ref = row_oracle(qh, kh, vh, rows, vis, scale)
-            g = got[0, h, rows].double().cpu().numpy()
-            bound = 2e-3 + np.abs(ref) * 2.0 ** -8   # bf16 output of the model
-            err = np.abs(g - ref)
-            assert (err <= bound).all(), (kind, h, float(err.max()))
+    def check(h):
+        kind, p1, p2, slot, scale = plan.heads[h]
+        ids = cnt = None
+        if kind == _abi.MSA_KIND_BLOCK:
+            idx, cn = O.select_block_sparse_topk_indices(qn[None, h:h + 1], kn[None, h:h + 1], p1,
+                                                         "bf16", scale)
+            ids, cnt = idx[0, 0], cn[0, 0]
+        rows = RS.block_rows(S, h, extra=sample_rows(S))
+        ref = RS.head_rows_reference(qn[h], kn[h], vn[h], rows, kind, p1, p2, scale, ids, cnt)
+        err = np.abs(gn[h, rows] - ref)
+        bound = 2e-3 + np.abs(ref) * 2.0 ** -8   # bf16 output of the model
+        return h, kind, rows.size, float(err.max()), int((err > bound).sum())
+
+    res = RS.map_heads(check, range(q.shape[1]), tag=tag)
+    kinds = sorted({r[1] for r in res})
+    print(f"{tag} {sum(r[2] for r in res)} rows, kinds {kinds}, worst error "
+          f"{max(r[3] for r in res):.3e}", flush=True)
+    for h, kind, n, err, n_bad in res:
+        assert n_bad == 0, (h, kind, n, err, n_bad)
 
 
 @pytest.mark.parametrize("S,layers,mix", [
@@ -122,6 +108,5 @@ def test_full_prefill_layers_match_oracle(gpu_device, tmp_path, monkeypatch, S, 
     assert len(captured) == layers
     del model, patched
     for li, (q, k, v, plan, got) in enumerate(captured):
-        print(f"[model] layer {li}: checking sampled rows", flush=True)
         assert not plan.all_dense
-        check_layer(q, k, v, plan, got)
+        check_layer(f"[model] S={S} layer {li}:", q, k, v, plan, got)

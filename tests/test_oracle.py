@@ -482,6 +482,59 @@ def test_dense_vs_torch_sdpa(s_q, s_k):
 
 
 # ---------------------------------------------------------------------------
+# row-sampled attention (the full-length GPU checks' reference)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("group", [1, 7, 64])
+def test_rows_attention_equals_full_heads(group):
+    """Every row, grouped any way, equals the pinned full-head functions;
+    a rule with a wrong sign or an off-by-one at the band or block edge
+    would move rows at those edges."""
+    S, D = 777, 64
+    q, k, v = make_qkv(B=1, H=1, S_q=S, D=D, dtype=torch.bfloat16, seed=6)
+    qn, kn, vn = np32(q), np32(k), np32(v)
+    sc = O.sparse_scale(D)
+    rows = np.arange(S)
+    for n_init, n_local in [(0, 100), (64, 128), (3, 1), (100, 2000)]:
+        ref = O.streaming_attention(qn, kn, vn, n_init, n_local)[0, 0]
+        vis, keys = O.stream_rows_visible(n_init, n_local)
+        got = O.rows_attention(qn[0, 0], kn[0, 0], vn[0, 0], rows, vis, sc, keys=keys,
+                               group=group)
+        assert np.abs(got - ref).max() < 1e-12, (n_init, n_local)
+        got = O.rows_attention(qn[0, 0], kn[0, 0], vn[0, 0], rows, vis, sc, group=group)
+        assert np.abs(got - ref).max() < 1e-12, (n_init, n_local)
+    for topk in (1, 3, 13):
+        idx, cnt = O.select_block_sparse_topk_indices(qn, kn, topk, "bf16")
+        ref = O.block_sparse_from_indices(qn, kn, vn, idx)[0, 0]
+        vis, keys = O.block_rows_visible(idx[0, 0], cnt[0, 0], S)
+        for kf in (keys, None):
+            got = O.rows_attention(qn[0, 0], kn[0, 0], vn[0, 0], rows, vis, sc, keys=kf,
+                                   group=group)
+            assert np.abs(got - ref).max() < 1e-12, topk
+    ref = O.dense_causal(qn, kn, vn, scale=sc)[0, 0]
+    got = O.rows_attention(qn[0, 0], kn[0, 0], vn[0, 0], rows, O.causal_rows_visible, sc,
+                           group=group)
+    assert np.abs(got - ref).max() < 1e-12
+
+
+def test_block_rows_visible_counts_and_invalid_ids():
+    """Padding past cnt and ids outside [0, n_kv_blocks) see nothing; a
+    sampled row sees exactly its listed blocks' keys up to itself."""
+    S = 300
+    idx = np.array([[0, -1, 9], [1, 0, 2], [2, 4, 7], [3, 0, 1], [4, 1, 0]], np.int32)
+    cnt = np.array([1, 2, 3, 2, 3], np.int32)
+    vis, keys_of = O.block_rows_visible(idx, cnt, S)
+    keys = np.arange(S)
+    for r in (0, 63, 64, 130, 191, 250, 299):
+        want = set()
+        for b in idx[r // 64, :cnt[r // 64]]:
+            if 0 <= b < 5:
+                want |= {j for j in range(64 * b, min(S, 64 * b + 64)) if j <= r}
+        got = set(np.nonzero(vis(np.array([r]), keys)[0])[0].tolist())
+        assert got == want, r
+        assert want <= set(keys_of(np.array([r])).tolist()), r
+
+
+# ---------------------------------------------------------------------------
 # algorithmic work counts (closed forms for the benchmark configurations)
 # ---------------------------------------------------------------------------
 def test_work_counts_small_bruteforce():
