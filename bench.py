@@ -677,17 +677,18 @@ def vs_bench(args, dev):
         tiles += vs_tiles(v_idx[0, j, :int(v_cnt[0, j])].numpy(),
                           s_idx[0, j, :int(s_cnt[0, j])].numpy(), S)
     # the tile-list builder's own totals, read from the workspace (layout of
-    # vs_layout in msa_abi.hip: ids, masks, then (unmasked, total) per row)
+    # vs_layout in msa_abi.hip: the per-wave lists, then (unmasked, total)
+    # per row and wave; wave w walks the 16-key chunk w of its tiles)
     n_kb = -(-S // BLOCK)
     nv_pad = -(-max(nv, 1) // BLOCK) * BLOCK
     cap = n_kb + nv_pad // BLOCK
     n_rows = len(plan.vs_heads) * n_kb
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    cnt_off = up(up(n_rows * cap * 4) + n_rows * cap * 8)
-    counts = vs_ws[cnt_off:cnt_off + n_rows * 8].view(torch.int32).view(n_rows, 2).cpu()
-    tiles_gpu = int(counts[:, 1].sum())
+    cnt_off = up(n_rows * 4 * cap * 4)
+    counts = vs_ws[cnt_off:cnt_off + n_rows * 32].view(torch.int32).view(n_rows, 4, 2).cpu()
+    chunks = int(counts[:, :, 1].sum())
     n_stream = sum(1 for hd in plan.heads if hd[0] == _abi.MSA_KIND_STREAM)
-    flop_vs = tiles * 4 * BLOCK * BLOCK * D
+    flop_vs = chunks * 4 * BLOCK * (BLOCK // 4) * D
     flop_stream = n_stream * stream_pairs(S, 100, 800) * 4 * D
     flop = flop_vs + flop_stream
     dense_flop = H * (S * (S + 1) // 2) * 4 * D
@@ -713,8 +714,8 @@ def vs_bench(args, dev):
         "kernels_ms": {"vs_estimate": round(t_est, 4), "stage_kv": round(t_stage, 4),
                        "lists_gather_attention": round(t_attn, 4)},
         "vs_tiles": tiles,
-        "vs_tiles_builder": tiles_gpu,
-        "vs_tiles_unmasked": int(counts[:, 0].sum()),
+        "vs_chunks_builder": chunks,
+        "vs_chunks_unmasked": int(counts[:, :, 0].sum()),
         "vs_tile_density": round(tiles / (len(plan.vs_heads) * block_tiles(S, 1 << 30)), 4),
         "executed_flop": flop,
         "attention_tflops": round(flop / (t_attn * 1e-3) / 1e12, 3),

@@ -357,7 +357,7 @@ int msa_stage_kv_pool(const msa_tensor4* q, const msa_tensor4* k, const msa_tens
 struct VsLayout {
   int64_t n_rows;
   int cap, nv_pad;
-  size_t ids, masks, cnt, gk, gv, total;
+  size_t lists, cnt, gk, gv, total;
 };
 
 static VsLayout vs_layout(int64_t B, int64_t n_slots, int64_t s_k, int64_t v_stride, int64_t D) {
@@ -368,12 +368,10 @@ static VsLayout vs_layout(int64_t B, int64_t n_slots, int64_t s_k, int64_t v_str
   L.n_rows = B * n_slots * n_kb;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   size_t off = 0;
-  L.ids = off;
-  off = up(off + size_t(L.n_rows) * L.cap * 4);
-  L.masks = off;
-  off = up(off + size_t(L.n_rows) * L.cap * 8);
-  L.cnt = off;
-  off = up(off + size_t(L.n_rows) * 2 * 4);
+  L.lists = off;  // per row and wave: cap entries
+  off = up(off + size_t(L.n_rows) * 4 * L.cap * 4);
+  L.cnt = off;    // per row and wave: (unmasked, total)
+  off = up(off + size_t(L.n_rows) * 4 * 2 * 4);
   L.gk = off;
   off = up(off + size_t(B * n_slots) * L.nv_pad * D * 2);
   L.gv = off;
@@ -703,8 +701,7 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   bp.v_cnt = vs->v_cnt;
   bp.s_idx = vs->s_idx;
   bp.s_cnt = vs->s_cnt;
-  bp.ids = reinterpret_cast<int32_t*>(vw + vl.ids);
-  bp.masks = reinterpret_cast<uint64_t*>(vw + vl.masks);
+  bp.lists = reinterpret_cast<uint32_t*>(vw + vl.lists);
   bp.cnt = reinterpret_cast<int32_t*>(vw + vl.cnt);
   bp.v_stride = vs->v_stride;
   bp.s_stride = vs->s_stride;
@@ -751,8 +748,7 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   interleave_kinds(other, n_o, heads, int(H));
   for (int i = 0; i < n_o; ++i) other_work[i] = head_work(heads[other[i] % H], n_kb, topk_max);
   AttnParams vp = ap;
-  vp.vs_ids = bp.ids;
-  vp.vs_masks = bp.masks;
+  vp.vs_lists = bp.lists;
   vp.vs_cnt = bp.cnt;
   vp.gkt = gp.kt;
   vp.gvt = gp.vt;

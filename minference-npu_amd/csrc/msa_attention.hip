@@ -391,11 +391,13 @@ struct TileSeq {
     // so that no branch splits the caller's instruction stream
     return {load_uniform((list ? list : any) + (list ? i : 0)), i};
   }
+  // PACKED: list entries are tile id << 16 | 16 key bits (the
+  // vertical_and_slash lists)
+  template <bool PACKED = false>
   __device__ int finish(Pending r) const {
-    const int t = list ? r.v : r.i;
+    const int t = list ? (PACKED ? int(uint32_t(r.v) >> 16) : r.v) : r.i;
     return min(max(t, 0), n_kb - 1);
   }
-  __device__ int tile(int q) const { return finish(fetch(q)); }
   __device__ bool masked(int q) const { return q >= mpos; }
 };
 
@@ -474,7 +476,6 @@ void attn_kernel(AttnParams P) {
   // ---- state of the current work item (wave-uniform)
   int b = 0, h = 0, q0 = 0, a0 = 0, n_init = 0, n_local = 0, kind = KIND_DENSE;
   float c_log2 = 0.0f, vfac = 1.0f;
-  int64_t vs_base = 0;  // list row of a vertical_and_slash item
   TileSeq seq;
   __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(P.kt), short(0), 0, 0x00020000);
@@ -505,13 +506,12 @@ void attn_kernel(AttnParams P) {
     seq.list = nullptr;
     seq.any = reinterpret_cast<const int32_t*>(P.q);
     if constexpr (VS) {
-      // full tiles (no mask), then partial tiles, then gathered vertical tiles
-      // (ids n_kb + g), every entry with its key mask
-      vs_base = ((int64_t(b) * P.vs_slots + hd_slot) * P.n_qb + bq);
-      const int nf = load_uniform(P.vs_cnt + 2 * vs_base);
-      const int nt = load_uniform(P.vs_cnt + 2 * vs_base + 1);
-      vs_base *= P.vs_cap;
-      seq.list = P.vs_ids + vs_base;
+      // this wave's list: unmasked entries, then masked key tiles and
+      // gathered vertical tiles (ids n_kb + g), each with its chunk's key bits
+      const int64_t lrow = ((int64_t(b) * P.vs_slots + hd_slot) * P.n_qb + bq) * 4 + w;
+      const int nf = load_uniform(P.vs_cnt + 2 * lrow);
+      const int nt = load_uniform(P.vs_cnt + 2 * lrow + 1);
+      seq.list = reinterpret_cast<const int32_t*>(P.vs_lists + lrow * P.vs_cap);
       seq.n_kb = P.n_kb + P.nv_pad / kBlock;
       seq.set({0, nf, 0, 0, 0}, {nf, nt, 0, 0, 0}, 1);
     } else if (kind == KIND_BLOCK) {
@@ -673,14 +673,15 @@ void attn_kernel(AttnParams P) {
       for (int gg = 0; gg < 2; ++gg) s[gg] = mfma_qk<T>(kr[ks], qb[2 * hf + gg][ks], s[gg]);
   };
   // visible iff j <= key_hi and (j >= band_lo or j < sink_hi); for a
-  // vertical_and_slash tile: iff the key's bit is set in the tile's mask mk
-  // and (gathered tile, all keys in every row's past, or j <= key_hi)
-  auto mask_half = [&](f32x4 (&s)[2], int hf, int t, uint64_t mk) INLINE {
+  // vertical_and_slash tile: iff the key's bit is set in the wave's chunk
+  // mask mk (16 bits) and (gathered tile, all keys in every row's past, or
+  // j <= key_hi)
+  auto mask_half = [&](f32x4 (&s)[2], int hf, int t, uint32_t mk) INLINE {
     const int jb = t * kBlock + 16 * w + 4 * lr;
     uint32_t bits = 0xfu;
     bool past = false;
     if constexpr (VS) {
-      bits = uint32_t(mk >> (16 * w + 4 * lr)) & 0xfu;
+      bits = (mk >> (4 * lr)) & 0xfu;
       past = t >= P.n_kb;
       // every key of a gathered tile or of a tile before the first row's
       // tile lies in every row's past: visibility is the key's bit, the same
@@ -730,7 +731,7 @@ void attn_kernel(AttnParams P) {
   // Rare path: recompute the half's scores, raise the running max to the
   // row max, rescale the half's O and row sums, and redo the exponentials.
   auto rescale_half = [&](const u32x4 (&kr)[NKS], f32x4 (&s)[2], float (&ps)[2], int hf, int t,
-                          uint64_t mk, bool mt) INLINE {
+                          uint32_t mk, bool mt) INLINE {
     qk_half(kr, hf, s);
     if (mt) mask_half(s, hf, t, mk);
     float m0 = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
@@ -789,22 +790,22 @@ void attn_kernel(AttnParams P) {
   // stream); each loop runs whole (A, B) pairs, with a single step before or
   // after it when its range starts or ends on the other set.
   u32x4 kA[NKS], vA[NDB], kB[NKS], vB[NDB];
-  // key masks of vertical_and_slash tiles travel with their tile numbers
-  // (looked up three positions ahead, like the tiles)
-  auto mask_at = [&](int q) INLINE -> uint64_t {
-    if constexpr (VS) return load_uniform(P.vs_masks + vs_base + max(min(q, total - 1), 0));
-    return 0ull;
+  // key masks of vertical_and_slash tiles come in the list entries with
+  // their tile numbers
+  auto mask_of = [&](TileSeq::Pending r) INLINE -> uint32_t {
+    if constexpr (VS) return uint32_t(r.v) & 0xffffu;
+    return 0u;
   };
   int tA = 0, tB = 0;
   TileSeq::Pending pn{0, 0};  // lookup of the position two ahead, issued a step early
-  uint64_t mA = 0, mB = 0, mn = 0;
+  uint32_t mA = 0, mB = 0;
   // the first two positions' operands of the item (and the third's tile)
   auto start_tiles = [&]() INLINE {
-    tA = seq.tile(0);
-    tB = seq.tile(1);
-    mA = mask_at(0);
-    mB = mask_at(1);
-    mn = mask_at(2);
+    const TileSeq::Pending p0 = seq.fetch(0), p1 = seq.fetch(1);
+    tA = seq.template finish<VS>(p0);
+    tB = seq.template finish<VS>(p1);
+    mA = mask_of(p0);
+    mB = mask_of(p1);
     load_k(tA, kA, !VS && total < 1);
     load_v(tA, vA, !VS && total < 1);
     load_k(tB, kB, !VS && total < 2);
@@ -814,15 +815,15 @@ void attn_kernel(AttnParams P) {
   // one step: QK of both halves; half 0's softmax under half 1's QK, half
   // 1's softmax under half 0's PV; K is reloaded once the rare path can no
   // longer need it
-  auto step = [&](auto masked, u32x4 (&kr)[NKS], u32x4 (&vr)[NDB], int& tcur, uint64_t& mcur,
+  auto step = [&](auto masked, u32x4 (&kr)[NKS], u32x4 (&vr)[NDB], int& tcur, uint32_t& mcur,
                   int p) INLINE {
     constexpr bool MT = decltype(masked)::value;
     // the tile of position p + 2 from the lookup issued in the previous step
     // (its scalar load has had a step to arrive), then position p + 3's
     // lookup.  (A scheduling barrier pinning that load here cost 1.5 %.)
-    const int tn = seq.finish(pn);
+    const int tn = seq.template finish<VS>(pn);
+    const uint32_t mnext = mask_of(pn);
     pn = seq.fetch(p + 3);
-    const uint64_t mnn = mask_at(p + 3);
     // (vertical_and_slash items walk long lists: the per-step test costs
     // more there than the two loads it saves per item)
     const bool drop = !VS && p + 2 >= total;
@@ -839,8 +840,7 @@ void attn_kernel(AttnParams P) {
     pv_half(sb, pb, 1, vr);
     load_v(tn, vr, drop);
     tcur = tn;
-    mcur = mn;
-    mn = mnn;
+    mcur = mnext;
   };
   auto run = [&](auto masked, int p0, int p1) INLINE {
     int p = p0;

@@ -85,13 +85,14 @@ struct AttnParams {
   int xcd_count[8];
   int* queue;      // 8 counters of the XCD ranges (zeroed before each launch)
   int wg_per_xcd;  // CUs per XCD
-  // vertical_and_slash launch: per (b * vs_slots + slot, query block) a list
-  // of vs_cap tile ids (gathered vertical tiles as n_kb + g), one 64-bit key
-  // mask per entry, and (unmasked prefix, total) counts; gathered vertical
-  // operands per slot in stage_kernel's layout, nv_pad keys each.
-  const int32_t* vs_ids;
-  const uint64_t* vs_masks;
-  const int32_t* vs_cnt;
+  // vertical_and_slash launch: per (b * vs_slots + slot, query block) and
+  // wave w (the 16-key chunk [16w, 16w+16) of every tile) a list of vs_cap
+  // entries (tile id << 16 | the chunk's 16 key bits; gathered vertical
+  // tiles as n_kb + g) holding only the tiles whose chunk has a visible key,
+  // and its (unmasked prefix, total) counts; gathered vertical operands per
+  // slot in stage_kernel's layout, nv_pad keys each.
+  const uint32_t* vs_lists;  // [row][4][vs_cap]
+  const int32_t* vs_cnt;     // [row][4][2]
   const uint16_t* gkt;
   const uint16_t* gvt;
   int vs_slots, vs_cap, nv_pad;
@@ -107,8 +108,7 @@ struct VsBuildParams {
   const int32_t* v_cnt;  // [batch*slots]
   const int32_t* s_idx;  // [batch*slots][s_stride]: slash offsets, any order
   const int32_t* s_cnt;  // [batch*slots]
-  int32_t* ids;          // outputs in the AttnParams vs_* layout
-  uint64_t* masks;
+  uint32_t* lists;       // outputs in the AttnParams vs_* layout
   int32_t* cnt;
   int v_stride, s_stride, cap, n_qb, n_kb, s_k;
 };

@@ -10,7 +10,7 @@
 //   * every vertical column (clamped into [0, S_k)),
 // under the causal mask j <= i.
 //
-// vs_build_kernel turns that into a list per (slot, query block):
+// vs_build_kernel turns that into lists per (slot, query block):
 //   * key tiles t <= bq that a slash window meets, plus tile bq if a vertical
 //     column lies in it; the mask holds the slash keys and the vertical
 //     columns of the tile (the kernel adds the causal mask for t == bq);
@@ -18,10 +18,14 @@
 //     the slot's column list that lie before 64 bq in a tile no slash window
 //     meets; their K/V rows are staged contiguously (stage_kernel, gather
 //     mode) so that scattered columns cost a dense tile, not one tile each.
-// Entries whose 64 keys are all visible to every row (key tiles t < bq with
-// a full mask, gathered tiles with a full mask) come first and run without
-// a mask; then the key tiles, then the gathered tiles, that need one.
-// Every visible key appears in exactly one entry.
+// The attention kernel's wave w walks the 16-key chunk w of every tile, so
+// each wave gets a list of its own: the tiles whose chunk w holds a visible
+// key, entry = tile id << 16 | the chunk's 16 key bits.  (A slash window of
+// 64 keys meets two tiles but only four or five of their eight chunks.)
+// Entries whose 16 keys are all visible to every row (key tiles t < bq and
+// gathered tiles, chunk bits all set) come first and run without a mask;
+// then the key tiles, then the gathered tiles, that need one.  Every visible
+// key appears in exactly one entry of one list.
 
 #include "msa_common.h"
 #include "msa_kernels.h"
@@ -44,29 +48,47 @@ __device__ inline uint64_t lds_get64(const uint32_t* m, int t) {
   return uint64_t(m[2 * t]) | (uint64_t(m[2 * t + 1]) << 32);
 }
 
-// Block-wide exclusive prefix of a 0/1 flag over 256 threads; returns the
-// prefix and writes the block total to *total.
-__device__ inline int block_prefix(bool flag, int* scratch, int* total) {
+// Block-wide exclusive prefixes of N 0/1 flags over 256 threads: pre[i] =
+// the flags i of the threads before this one, tot[i] = the block's total.
+// scratch: 4 * N ints.
+template <int N>
+__device__ inline void block_prefix(const bool (&flag)[N], int* scratch, int (&pre)[N],
+                                    int (&tot)[N]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const uint64_t bal = __ballot(flag);
-  const int in_wave = __popcll(bal & ((1ull << lane) - 1ull));
-  if (lane == 0) scratch[w] = __popcll(bal);
-  __syncthreads();
-  int before = 0, all = 0;
+  const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    before += v < w ? scratch[v] : 0;
-    all += scratch[v];
+  for (int i = 0; i < N; ++i) {
+    const uint64_t bal = __ballot(flag[i]);
+    pre[i] = __popcll(bal & below);
+    if (lane == 0) scratch[4 * i + w] = __popcll(bal);
   }
   __syncthreads();
-  *total = all;
-  return before + in_wave;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    int before = 0, all = 0;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      before += v < w ? scratch[4 * i + v] : 0;
+      all += scratch[4 * i + v];
+    }
+    pre[i] += before;
+    tot[i] = all;
+  }
+  __syncthreads();
+}
+
+// Chunk w of a tile's mask m for wave w's list: 1 = unmasked entry (all 16
+// keys visible to every row: a key tile below the block or a gathered
+// tile), 2 = masked entry, 0 = no visible key in the chunk.
+__device__ inline int chunk_class(uint64_t m, int w, bool below_block) {
+  const uint32_t c = uint32_t(m >> (16 * w)) & 0xffffu;
+  return c == 0u ? 0 : (c == 0xffffu && below_block ? 1 : 2);
 }
 
 __global__ __launch_bounds__(256) void vs_build_kernel(VsBuildParams P) {
   __shared__ uint32_t um[2 * kVsMaxTiles];  // per key tile: slash keys, then vertical keys
   __shared__ uint32_t gm[2 * kVsMaxTiles];  // per gathered tile: gathered columns
-  __shared__ int scratch[4];
+  __shared__ int scratch[32];
   const int bq = blockIdx.x;
   const int bs = blockIdx.y;  // b * slots + slot
   const int tid = threadIdx.x;
@@ -112,74 +134,53 @@ __global__ __launch_bounds__(256) void vs_build_kernel(VsBuildParams P) {
   }
   __syncthreads();
 
-  // counts: full and partial key tiles, full and partial gathered tiles
-  int n_full = 0, n_part = 0, n_gfull = 0, n_gpart = 0;
-  for (int t0 = 0; t0 < n_t; t0 += 256) {
-    const int t = t0 + tid;
-    const uint64_t m = t < n_t ? lds_get64(um, t) : 0ull;
-    const bool full = t < bq && m == ~0ull;
-    int tot;
-    block_prefix(full, scratch, &tot);
-    n_full += tot;
-    block_prefix(m != 0ull && !full, scratch, &tot);
-    n_part += tot;
-  }
-  for (int g0 = 0; g0 < n_g; g0 += 256) {
-    const int g = g0 + tid;
-    const uint64_t m = g < n_g ? lds_get64(gm, g) : 0ull;
-    int tot;
-    block_prefix(m == ~0ull, scratch, &tot);
-    n_gfull += tot;
-    block_prefix(m != 0ull && m != ~0ull, scratch, &tot);
-    n_gpart += tot;
-  }
-
-  // write the list: full key tiles, full gathered tiles | partial key tiles,
-  // partial gathered tiles
+  // pass 1: each wave's count of unmasked entries (key tiles, then gathered)
   const int64_t row = int64_t(bs) * P.n_qb + bq;
-  int32_t* ids = P.ids + row * P.cap;
-  uint64_t* masks = P.masks + row * P.cap;
-  int off_full = 0, off_part = n_full + n_gfull;
-  for (int t0 = 0; t0 < n_t; t0 += 256) {
-    const int t = t0 + tid;
-    const uint64_t m = t < n_t ? lds_get64(um, t) : 0ull;
-    const bool full = t < bq && m == ~0ull;
-    const bool part = m != 0ull && !full;
-    int tf, tp;
-    const int pf = block_prefix(full, scratch, &tf);
-    const int pp = block_prefix(part, scratch, &tp);
-    if (full) {
-      ids[off_full + pf] = t;
-      masks[off_full + pf] = m;
-    } else if (part) {
-      ids[off_part + pp] = t;
-      masks[off_part + pp] = m;
-    }
-    off_full += tf;
-    off_part += tp;
+  int n_un[4] = {0, 0, 0, 0};
+  for (int e0 = 0; e0 < n_t + n_g; e0 += 256) {
+    const int e = e0 + tid;
+    const bool gat = e >= n_t;
+    const uint64_t m = e < n_t ? lds_get64(um, e) : (e < n_t + n_g ? lds_get64(gm, e - n_t) : 0ull);
+    const bool below = gat || e < bq;
+    bool f[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) f[w] = chunk_class(m, w, below) == 1;
+    int pre[4], tot[4];
+    block_prefix<4>(f, scratch, pre, tot);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) n_un[w] += tot[w];
   }
-  int off_gfull = n_full, off_gpart = n_full + n_gfull + n_part;
-  for (int g0 = 0; g0 < n_g; g0 += 256) {
-    const int g = g0 + tid;
-    const uint64_t m = g < n_g ? lds_get64(gm, g) : 0ull;
-    const bool full = m == ~0ull;
-    const bool part = m != 0ull && !full;
-    int tf, tp;
-    const int pf = block_prefix(full, scratch, &tf);
-    const int pp = block_prefix(part, scratch, &tp);
-    if (full) {
-      ids[off_gfull + pf] = P.n_kb + g;
-      masks[off_gfull + pf] = m;
-    } else if (part) {
-      ids[off_gpart + pp] = P.n_kb + g;
-      masks[off_gpart + pp] = m;
+  // pass 2: the entries, unmasked from 0 and masked from n_un[w] in each
+  // wave's list
+  uint32_t* lists = P.lists + row * 4 * P.cap;
+  int off_u[4] = {0, 0, 0, 0}, off_m[4] = {n_un[0], n_un[1], n_un[2], n_un[3]};
+  for (int e0 = 0; e0 < n_t + n_g; e0 += 256) {
+    const int e = e0 + tid;
+    const bool gat = e >= n_t;
+    const uint64_t m = e < n_t ? lds_get64(um, e) : (e < n_t + n_g ? lds_get64(gm, e - n_t) : 0ull);
+    const bool below = gat || e < bq;
+    const uint32_t id = uint32_t(gat ? P.n_kb + (e - n_t) : e) << 16;
+    bool f[8];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int c = chunk_class(m, w, below);
+      f[w] = c == 1;
+      f[4 + w] = c == 2;
     }
-    off_gfull += tf;
-    off_gpart += tp;
+    int pre[8], tot[8];
+    block_prefix<8>(f, scratch, pre, tot);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t ent = id | (uint32_t(m >> (16 * w)) & 0xffffu);
+      if (f[w]) lists[w * P.cap + off_u[w] + pre[w]] = ent;
+      if (f[4 + w]) lists[w * P.cap + off_m[w] + pre[4 + w]] = ent;
+      off_u[w] += tot[w];
+      off_m[w] += tot[4 + w];
+    }
   }
-  if (tid == 0) {
-    P.cnt[2 * row] = n_full + n_gfull;
-    P.cnt[2 * row + 1] = n_full + n_gfull + n_part + n_gpart;
+  if (tid < 4) {
+    P.cnt[2 * (row * 4 + tid)] = n_un[tid];
+    P.cnt[2 * (row * 4 + tid) + 1] = off_m[tid];
   }
 }
 
