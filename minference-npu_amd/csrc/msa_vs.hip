@@ -384,18 +384,53 @@ __device__ inline double block_reduce(double v, bool is_max, double* red) {
   return r;
 }
 
-// Row max and the fp64 sum of exp(x - max) of one estimator row.
+// Row max and the fp64 sum of exp(x - max) of one estimator row; 16-byte
+// loads (8 entries), four in flight per thread; entries past s (the row
+// padding) do not count.
 template <typename T>
 __global__ __launch_bounds__(256) void vs_rowstat_kernel(VsEstParams P) {
   __shared__ double red[4];
   const int r = blockIdx.x;
   const int bs = blockIdx.y;
   const uint16_t* xr = P.x + (int64_t(bs) * kBlock + r) * P.s_pad;
+  const int n8 = (P.s + 7) / 8;  // 8-entry groups holding entries < s
+  auto entry = [&](const u32x4& v, int g, int e) -> double {
+    const uint16_t b = uint16_t(e & 1 ? v[e >> 1] >> 16 : v[e >> 1] & 0xffffu);
+    return 8 * g + e < P.s ? double(T::to_float(b)) : -__builtin_inf();
+  };
   double m = -__builtin_inf();
-  for (int j = threadIdx.x; j < P.s; j += 256) m = fmax(m, double(T::to_float(xr[j])));
+  for (int g0 = threadIdx.x; g0 < n8; g0 += 4 * 256) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = g0 + 256 * u;
+      v[u] = g < n8 ? load16(xr + 8 * g) : zero_u32x4();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = g0 + 256 * u;
+      if (g < n8)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmax(m, entry(v[u], g, e));
+    }
+  }
   m = block_reduce(m, true, red);
   double l = 0.0;
-  for (int j = threadIdx.x; j < P.s; j += 256) l += exp(double(T::to_float(xr[j])) - m);
+  for (int g0 = threadIdx.x; g0 < n8; g0 += 4 * 256) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = g0 + 256 * u;
+      v[u] = g < n8 ? load16(xr + 8 * g) : zero_u32x4();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = g0 + 256 * u;
+      if (g < n8)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) l += exp(entry(v[u], g, e) - m);
+    }
+  }
   l = block_reduce(l, false, red);
   if (threadIdx.x == 0) {
     P.rmax[bs * kBlock + r] = float(m);
@@ -405,37 +440,57 @@ __global__ __launch_bounds__(256) void vs_rowstat_kernel(VsEstParams P) {
 
 // Column sums and diagonal sums of p, rounded to fp32, with the forced
 // entries set to +inf.  Thread t of a block owns column / diagonal
-// c0 + t; row by row, the block forms p for columns [c0 - 63, c0 + 256)
-// once in LDS, and each thread adds its column's p and its diagonal's p
-// (column t + 1 - n + r), rows in order r = 0 .. n-1.
+// c0 + t; four rows at a time, the block forms p for columns [c0 - 63,
+// c0 + 256) once in LDS, and each thread adds its column's p and its
+// diagonal's p (column t + 1 - n + r), rows in order r = 0 .. n-1.
 template <typename T>
 __global__ __launch_bounds__(256) void vs_sums_kernel(VsEstParams P) {
   constexpr int W = 256 + kBlock - 1;  // columns one block needs per row
-  __shared__ double sm[kBlock], sl[kBlock];
-  __shared__ double prow[W];
+  constexpr int RB = 4;                // rows per round
+  __shared__ double sm[kBlock], sl[kBlock];  // row max, 1 / row sum
+  __shared__ double prow[RB][W];
   const int bs = blockIdx.y;
   const int n = P.n_rows;
   const int tid = threadIdx.x;
   if (tid < n) {
     sm[tid] = double(P.rmax[bs * kBlock + tid]);
-    sl[tid] = P.rsum[bs * kBlock + tid];
+    sl[tid] = 1.0 / P.rsum[bs * kBlock + tid];  // p = e * (1 / l): within an ulp of e / l
   }
   const int c0 = blockIdx.x * 256;
   const int t = c0 + tid;
   const uint16_t* x = P.x + int64_t(bs) * kBlock * P.s_pad;
   double cv = 0.0, cs = 0.0;
-  for (int r = 0; r < n; ++r) {
-    __syncthreads();  // previous row consumed (and sm / sl written)
-    for (int idx = tid; idx < W; idx += 256) {
-      const int col = c0 - (kBlock - 1) + idx;
-      prow[idx] = (col >= 0 && col < P.s)
-                      ? exp(double(T::to_float(x[int64_t(r) * P.s_pad + col])) - sm[r]) / sl[r]
-                      : 0.0;
+  for (int r0 = 0; r0 < n; r0 += RB) {
+    __syncthreads();  // previous rows consumed (and sm / sl written)
+    uint16_t xv[(RB * W + 255) / 256];
+#pragma unroll
+    for (int u = 0; u < (RB * W + 255) / 256; ++u) {
+      const int idx = tid + 256 * u;
+      const int rr = idx / W, col = c0 - (kBlock - 1) + (idx - rr * W);
+      xv[u] = idx < RB * W && r0 + rr < n && col >= 0 && col < P.s
+                  ? x[int64_t(r0 + rr) * P.s_pad + col]
+                  : uint16_t(0);
+    }
+#pragma unroll
+    for (int u = 0; u < (RB * W + 255) / 256; ++u) {
+      const int idx = tid + 256 * u;
+      if (idx >= RB * W) break;
+      const int rr = idx / W, col = c0 - (kBlock - 1) + (idx - rr * W);
+      const int r = r0 + rr;
+      prow[rr][idx - rr * W] = r < n && col >= 0 && col < P.s
+                                   ? exp(double(T::to_float(xv[u])) - sm[r]) * sl[r]
+                                   : 0.0;
     }
     __syncthreads();
     if (t < P.s) {
-      cv += prow[tid + kBlock - 1];
-      if (r >= n - 1 - t) cs += prow[tid + kBlock - 1 + 1 - n + r];
+#pragma unroll
+      for (int rr = 0; rr < RB; ++rr) {
+        const int r = r0 + rr;
+        if (r < n) {
+          cv += prow[rr][tid + kBlock - 1];
+          if (r >= n - 1 - t) cs += prow[rr][tid + kBlock - 1 + 1 - n + r];
+        }
+      }
     }
   }
   if (t >= P.s) return;
