@@ -42,7 +42,9 @@ PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 BLOCK = 64
 
 # workload -> profile summary holding the calibrated HBM traffic of the attention kernel
-TRAFFIC_PROFILE = {"headline": "attn_kernel_headline64k_traffic.txt"}
+TRAFFIC_PROFILE = {"headline": "attn_kernel_headline64k_traffic.txt",
+                   "cfg2_block16k": "attn_kernel_cfg2_block16k_traffic.txt",
+                   "cfg3_stream64k": "attn_kernel_cfg3_stream64k_traffic.txt"}
 
 WORKLOADS = {
     # name: (S, n_stream, n_block, n_dense, n_init, n_local, topk)
@@ -92,6 +94,9 @@ def parse_args():
     ap.add_argument("--dim", type=int, default=96)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-dense", action="store_true", help="skip the same-GPU dense baselines")
+    ap.add_argument("--skip-kind", choices=("stream", "block"), default=None,
+                    help="profiling aid (not a benchmark line): the attention launch leaves the "
+                         "heads of this kind out (MSA_KIND_SKIP), to count one kind's traffic")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
     ap.add_argument("--no-rope", action="store_true", help="skip the RoPE measurement")
@@ -308,6 +313,13 @@ def main():
     H, D = args.heads, args.dim
     pats, (n_stream, n_block, n_dense) = layer_patterns(args.workload, H, args.seed)
     plan = build_layer_plan(pats, H, D, S)
+    if args.skip_kind:
+        import dataclasses
+
+        skip = _abi.MSA_KIND_STREAM if args.skip_kind == "stream" else _abi.MSA_KIND_BLOCK
+        plan = dataclasses.replace(plan, heads=tuple(
+            (_abi.MSA_KIND_SKIP,) + tuple(hd[1:]) if hd[0] == skip else hd for hd in plan.heads))
+        n_stream, n_block = (0, n_block) if args.skip_kind == "stream" else (n_stream, 0)
 
     q, k, v = make_inputs(S, H, D, args.seed, dev)
     out = torch.empty_like(q)
@@ -416,6 +428,7 @@ def main():
                          else "top-%d (reference selector)" % topk),
             "global_batch": 1,
             "parallelism": "single GPU",
+            **({"skip_kind": args.skip_kind} if args.skip_kind else {}),
         },
         "ms_per_layer": round(ms_step, 4),
         "pct_mfma_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),

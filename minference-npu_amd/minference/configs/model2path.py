@@ -57,15 +57,5 @@ def default_phi3_config():
     return pathb_configs(PHI3_PROBE_HEADS)[PHI3_DEFAULT_NAME]
 
 
-def ensure_configs() -> None:
-    """Writes the registered files if they are missing."""
-    from .patterns import headline_config, write
-
-    if not os.path.exists(PHI3_DEFAULT):
-        write(PHI3_DEFAULT, default_phi3_config())
-    if not os.path.exists(PHI3_HEADLINE):
-        write(PHI3_HEADLINE, headline_config(seed=0))
-
-
 def get_support_models():
     return list(MODEL2PATH.keys())
