@@ -1,9 +1,9 @@
 """The layer schedule (launch_block_layer), the estimator's one-pass flags and
 MSA_KIND_SKIP heads on the GPU.
 
-A layer with block_sparse heads runs the estimator's pooling pass, then its
-selection pass on the side stream beside the K/V staging, then one attention
-launch of all heads.  The passes compute what one estimator call computes,
+A layer with block_sparse heads runs the K/V staging with the estimator's
+pooling pass in the same launch, then the selection pass, then one attention
+launch of all heads, all on one stream.  The passes compute what one estimator call computes,
 and the attention launch is the one msa_layer_attention makes, so the ids
 and the output must equal those of the plain calls bit for bit; their
 correctness against the oracle is what the other GPU tests check.
@@ -48,8 +48,8 @@ def _single_launch(plan, q, k, v, idx, cnt, out):
 
 @pytest.mark.parametrize("case", ["gqa_mixed", "mha_mixed", "block_only"])
 def test_layer_schedule_matches_plain_calls(gpu_device, case):
-    """launch_block_layer (two-pass estimator, the selection on the side
-    stream beside the staging) == msa_block_estimate + msa_layer_attention,
+    """launch_block_layer (staging + pooling in one launch, then the
+    selection, one stream) == msa_block_estimate + msa_layer_attention,
     bit for bit, fp32 and bf16 outputs, twice in a row.  gqa_mixed: kv heads
     shared by block and stream heads, one kv head holding V beyond the fp16
     range."""
