@@ -101,6 +101,34 @@ __device__ inline float exact_score(const uint16_t* qrow, const uint16_t* krow, 
   return float((acc[0] + acc[1]) + (acc[2] + acc[3])) * scale;
 }
 
+// The exact dot product of two 16-bit rows, computed by the 16 lanes of a
+// lane row (sl = lane & 15 takes dims D/16 * sl ..) and summed over them; every
+// lane of the row returns it.  Products of 16-bit values are exact in fp64 and
+// so is the sum for operands of ordinary range, whatever the order: fp32 of it
+// is exact_score's dot product.
+template <typename T, int D>
+__device__ inline double exact_dot16(const uint16_t* qrow, const uint16_t* krow, int sl) {
+  constexpr int DPL = D / 16;
+  static_assert(DPL % 2 == 0, "whole 32-bit pairs per lane");
+  uint32_t qw[DPL / 2], kw[DPL / 2];
+#pragma unroll
+  for (int i = 0; i < DPL / 2; ++i) {
+    qw[i] = *reinterpret_cast<const uint32_t*>(qrow + DPL * sl + 2 * i);
+    kw[i] = *reinterpret_cast<const uint32_t*>(krow + DPL * sl + 2 * i);
+  }
+  double acc = 0.0;
+#pragma unroll
+  for (int i = 0; i < DPL / 2; ++i) {
+    acc = __builtin_fma(double(T::to_float(uint16_t(qw[i] & 0xffffu))),
+                        double(T::to_float(uint16_t(kw[i] & 0xffffu))), acc);
+    acc = __builtin_fma(double(T::to_float(uint16_t(qw[i] >> 16))),
+                        double(T::to_float(uint16_t(kw[i] >> 16))), acc);
+  }
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  return acc;
+}
+
 // Largest threshold search: starting from T0 (count(keys >= T0) >= topk),
 // bits hb .. 0; stops as soon as a threshold counts exactly topk keys.
 template <int N, typename Get>
@@ -225,15 +253,23 @@ __device__ inline bool finish_fast(Get get, Set set, int n, int nj, int topk, ui
   }
   if (nB > kBandMax) return false;
   if constexpr (N > 0) {
-    // the band's exact keys (one or two candidates per row in practice)
+    // the band's candidates (one or two per row in practice) into the list,
+    // then their exact keys, 16 lanes per candidate
     uint32_t bm = bandmask;
     while (bm) {
       const int j = __builtin_ctz(bm);
       bm &= bm - 1u;
-      const int c = 64 * j + lane;
       const int slot = atomicAdd(&bl.n, 1);
-      bl.m[slot] = make_uint2(order_key(exact_score<T, D>(qrow, kbase + int64_t(c) * D, scale)),
-                              uint32_t(c));
+      bl.m[slot] = make_uint2(0u, uint32_t(64 * j + lane));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int m0 = 0; m0 < nB; m0 += 4) {
+      const int m = m0 + (lane >> 4);
+      const double dot = exact_dot16<T, D>(qrow, kbase + int64_t(bl.m[min(m, nB - 1)].y) * D,
+                                           lane & 15);
+      if ((lane & 15) == 0 && m < nB) bl.m[m].x = order_key(float(dot) * scale);
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
