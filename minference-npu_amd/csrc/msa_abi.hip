@@ -283,6 +283,15 @@ static int cus_per_xcd() {
 }
 
 
+// The attention kernel reads K in place, from the caller's rows, when every
+// offset of one kv head's padded rows fits 31 bits and the rows do not
+// overlap; otherwise the staging writes K in operand order first.
+static bool k_in_place(const msa_tensor4* k) {
+  const int64_t D = k->size[3], ss = k->stride[2];
+  const int64_t s_pad = cdiv(k->size[2], MSA_BLOCK) * MSA_BLOCK;
+  return ss >= D && (s_pad * ss + D) * 2 <= (int64_t(1) << 31);
+}
+
 static int stage_setup(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
                        size_t workspace_bytes, StageParams& sp) {
   if (!k || !v || !k->data || !v->data) return MSA_E_NULL;
@@ -315,6 +324,7 @@ static int stage_setup(const msa_tensor4* k, const msa_tensor4* v, void* workspa
   sp.kv_heads = int(Hkv);
   sp.s_k = int(Sk);
   sp.s_pad = int(cdiv(Sk, MSA_BLOCK) * MSA_BLOCK);
+  sp.stage_k = k_in_place(k) ? 0 : 1;
   return MSA_OK;
 }
 
@@ -644,6 +654,7 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   const AttnLayout AL = attn_layout(B, Hkv, Sk, D);
   ap.vt = ws_at<uint16_t>(workspace, AL.vt);
   ap.kt = ws_at<uint16_t>(workspace, AL.kt);
+  ap.k_in_place = k_in_place(k) ? 1 : 0;
   int32_t* vexp = ws_at<int32_t>(workspace, AL.vexp);
   ap.vexp = vexp;
   ap.o = o->data;
@@ -747,7 +758,18 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   }
   interleave_kinds(other, n_o, heads, int(H));
   for (int i = 0; i < n_o; ++i) other_work[i] = head_work(heads[other[i] % H], n_kb, topk_max);
+  if (ap.k_in_place) {
+    // the vertical_and_slash kernel reads staged K: stage the K the plain
+    // staging left in place (V and its exponents are staged already)
+    StageParams kp;
+    st = stage_setup(k, v, workspace, workspace_bytes, kp);
+    if (st != MSA_OK) return st;
+    kp.stage_k = 2;
+    e = launch_stage(kp, q->dtype, D, hs);
+    if (e != hipSuccess) return int(e);
+  }
   AttnParams vp = ap;
+  vp.k_in_place = 0;
   vp.vs_lists = bp.lists;
   vp.vs_cnt = bp.cnt;
   vp.gkt = gp.kt;

@@ -22,8 +22,12 @@
 //   (registers for the whole item), one 16-row group per accumulator.  One
 //   v_permlane16_swap per register pair turns two 16-row accumulators
 //   (rounded to fp16) into the B operand of O^T = V^T.P^T on
-//   v_mfma_f32_32x32x16_f16.  K and V are staged once per layer in exact
-//   operand order (V as fp16), so every operand is one contiguous 1 KB load.
+//   v_mfma_f32_32x32x16_f16.  V is staged once per layer in exact operand
+//   order as fp16, so every V operand is one contiguous 1 KB load; K is read
+//   in place from the caller's rows (16 rows x 64 contiguous bytes per
+//   operand load) unless its rows overlap or a head's rows span more than a
+//   31-bit offset, or the launch is a vertical_and_slash one: then it is
+//   staged in operand order too.
 //   The exponentials are taken with each row's running max straight off
 //   QK, biased so that a row's maximum has P = 2^7 (P, O and the row sums
 //   all carry that factor, which cancels; it keeps small P out of fp16's
@@ -67,9 +71,10 @@ constexpr float kPCheck = 32768.0f;  // 2^(kPBias + 8)
 //     K[16 chunk + (l & 15)][32 ks + 8 (l >> 4) + e]      (QK A operand, 16x16x32)
 //   Vop[B*Hkv][chunk][db][lane 0..63][8], fp16: lane l holds
 //     V[16 chunk + 8 (l >> 5) + e][32 db + (l & 31)]     (PV A operand, 32x32x16)
-// so a wave reads every operand as one contiguous 1 KB.  blockIdx.z = 1
-// stages K (a permutation of 16-byte granules), 0 stages V (a transpose
-// through LDS, converted to fp16).  In gather mode the keys of a slot are
+// so a wave reads every operand as one contiguous 1 KB.  Plane 1 stages K
+// (a permutation of 16-byte granules; skipped where the attention kernel
+// reads K in place), plane 0 stages V (a transpose through LDS, converted to
+// fp16).  In gather mode the keys of a slot are
 // the listed rows (the vertical columns of a vertical_and_slash head)
 // instead of 0 .. s_k-1.
 //
@@ -164,7 +169,7 @@ __device__ float stage_v_tile(const StageParams& P, const uint16_t* src, const S
 // Workgroup i of a launch: the first n_pool_wg run the block estimator's
 // pooling pass (fused launch of msa_stage_kv_pool); then, in the dispatch
 // order of a (tile, kv head, plane) grid, the V tiles of every kv head and
-// then the K tiles.
+// then the K tiles (V only or K only as StageParams::stage_k says).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
   using SS = StageShape<D>;
@@ -181,7 +186,7 @@ __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
   const int tile_i = wi % n_tiles;
   const int rest = wi / n_tiles;
   const int bk = rest % n_bk;  // b * kv_heads + kvh (gather mode: b * n_slots + slot)
-  const int plane = rest / n_bk;  // 0: V, 1: K
+  const int plane = P.stage_k == 2 ? 1 : rest / n_bk;  // 0: V, 1: K
   const int j0 = tile_i * kBlock;
   int b, kvh;
   StageRows src_row{nullptr, 0, P.s_k};
@@ -255,7 +260,8 @@ __global__ __launch_bounds__(256) void vscale_kernel(StageParams P) {
 template <typename T, int D>
 static hipError_t launch_stage_t(const StageParams& p, hipStream_t st) {
   const int64_t n = p.n_pool_wg + int64_t(p.s_pad / kBlock) *
-                                     (p.batch * (p.rows ? p.n_slots : p.kv_heads)) * 2;
+                                     (p.batch * (p.rows ? p.n_slots : p.kv_heads)) *
+                                     (p.rows || p.stage_k == 1 ? 2 : 1);
   hipLaunchKernelGGL((stage_kernel<T, D>), dim3(uint32_t(n)), dim3(256), 0, st, p);
   return hipGetLastError();
 }
@@ -546,8 +552,17 @@ void attn_kernel(AttnParams P) {
     const int64_t bk = int64_t(b) * (P.heads / P.kv_group) + kvh;
     // staged V is V * 2^-vexp (stage_kernel); the output takes the 2^vexp back
     vfac = __builtin_amdgcn_ldexpf(1.0f, load_uniform(P.vexp + bk));
-    krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.kt + bk * P.s_pad * D),
-                                            short(0), P.s_pad * D * 2, 0x00020000);
+    if (!VS && P.k_in_place) {
+      // the head's own K rows; the record count ends at the last row's last
+      // element, so rows past S_k (and dropped loads) read zeros
+      krs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb +
+                                int64_t(kvh) * P.k_sh),
+          short(0), int(((P.s_k - 1) * P.k_ss + D) * 2), 0x00020000);
+    } else {
+      krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.kt + bk * P.s_pad * D),
+                                              short(0), P.s_pad * D * 2, 0x00020000);
+    }
     vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.vt + bk * P.s_pad * D),
                                             short(0), P.s_pad * D * 2, 0x00020000);
     // gathered vertical operands of a vertical_and_slash slot (tiles n_kb + g)
@@ -607,25 +622,40 @@ void attn_kernel(AttnParams P) {
     }
   };
 
-  // K and V chunk operands of tile t: wave w reads chunk 4t + w of the staged
-  // operands, each MFMA operand as one contiguous 1 KB (lane l: 16 bytes).
-  // drop: the position lies past the item's last tile; the lane offset is
-  // then out of the buffer's range, so the load returns zeros without a
-  // memory access (the loop's instruction stream stays the same).
+  // K and V chunk operands of tile t: wave w reads chunk c = 4t + w.  Staged
+  // operands: each MFMA operand is one contiguous 1 KB (lane l: 16 bytes).
+  // K in place (not in vertical_and_slash launches, whose K is staged): lane
+  // (lc, lr) of k-step ks reads K row 16c + lc at elements 32 ks + 8 lr ..
+  // +7; the row offset sits in the lane's VGPR, so a row past S_k is out of
+  // the buffer's range on its own.  drop: the position lies past the item's
+  // last tile; the lane offset is then out of the buffer's range, so the
+  // load returns zeros without a memory access (the loop's instruction
+  // stream stays the same).
   const uint32_t lane_off = 16u * lane;
+  const bool k_in_place = !VS && P.k_in_place;
+  const uint32_t k_row_bytes = uint32_t(P.k_ss) * 2u;
+  const uint32_t k_lane = k_in_place ? uint32_t(lc) * k_row_bytes + 16u * lr : lane_off;
+  const uint32_t k_cv = k_in_place ? 16u * k_row_bytes : 0u;  // VGPR bytes per chunk
+  const int k_cs = k_in_place ? 0 : S::CHUNK_BYTES;          // SGPR bytes per chunk
+  const int k_kss = k_in_place ? 64 : 1024;                  // bytes per k-step
   auto load_k = [&](int t, u32x4 (&kr)[NKS], bool drop) INLINE {
-    __amdgpu_buffer_rsrc_t rs = krs;
     if constexpr (VS) {
       const bool gat = t >= P.n_kb;
-      rs = gat ? gkrs : krs;
+      const __amdgpu_buffer_rsrc_t rs = gat ? gkrs : krs;
       t = gat ? t - P.n_kb : t;
-    }
-    const int soff = (4 * t + w) * S::CHUNK_BYTES;
-    const uint32_t vo = lane_off | (drop ? 0x80000000u : 0u);
+      const int soff = (4 * t + w) * S::CHUNK_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-      kr[ks] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, soff + 1024 * ks, 0));
+      for (int ks = 0; ks < NKS; ++ks)
+        kr[ks] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, soff + 1024 * ks, 0));
+    } else {
+      const int c = 4 * t + w;
+      const uint32_t vo = (k_lane + uint32_t(c) * k_cv) | (drop ? 0x80000000u : 0u);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        kr[ks] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo, c * k_cs + k_kss * ks, 0));
+    }
   };
   auto load_v = [&](int t, u32x4 (&vr)[NDB], bool drop) INLINE {
     __amdgpu_buffer_rsrc_t rs = vrs;

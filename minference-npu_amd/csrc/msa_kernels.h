@@ -65,13 +65,16 @@ struct HeadArg {
 struct AttnParams {
   const void* q;
   const void* k;
-  const uint16_t* kt;  // staged K operands (stage_kernel)
+  const uint16_t* kt;  // staged K operands (stage_kernel; unused when k_in_place)
   const uint16_t* vt;  // staged V operands (stage_kernel)
   void* o;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t o_sb, o_sh, o_ss;
   int batch, heads, kv_group, s_q, s_k, n_qb, n_kb, s_pad;
+  // 1: the QK operands are read from k's own rows (every operand load is 16
+  // rows x 64 contiguous bytes) instead of the staged kt (see k_in_place)
+  int k_in_place;
   const int32_t* idx;
   const int32_t* cnt;
   int idx_slots, topk_max;
@@ -149,6 +152,9 @@ struct StageParams {
   uint16_t* kt;  // [batch*kv_heads][s_pad/16][D/32][64][8] QK A operands (input dtype)
   uint16_t* vt;  // [batch*kv_heads][s_pad/16][D/32][64][8] PV A operands (fp16)
   int batch, kv_heads, s_k, s_pad;
+  // plain mode: 1 stages V and K; 0 V only (the attention kernel reads K in
+  // place); 2 K only (no V maxima: the V staging has run)
+  int stage_k;
   // Gather mode (rows != nullptr): blockIdx.y = b * n_slots + slot; staged key
   // j of that slot is row rows[(b * n_slots + slot) * rows_stride + j] of kv
   // head slot_kvh[slot] for j < rows_cnt[b * n_slots + slot], zero after;

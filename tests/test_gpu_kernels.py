@@ -465,26 +465,35 @@ def test_mixed_layer_strided_views(gpu_device, S, H, H_kv):
 
 
 @pytest.mark.parametrize("S", [200, 1000])
-def test_mixed_layer_repeated_query_rows(gpu_device, S):
-    """q views whose row stride is below D: an expanded q (stride 0, every
-    row the same) and overlapping rows (stride D/2) are read as the tensor
-    the view describes, against the oracle on the materialised q."""
+@pytest.mark.parametrize("which", ["q", "k"])
+def test_mixed_layer_strided_rows(gpu_device, S, which):
+    """q or k views with unusual row strides are read as the tensor the view
+    describes, against the oracle on the materialised view: an expanded view
+    (stride 0, every row the same) and overlapping rows (stride D/2; for k
+    both take the staged-K path), and padded rows (stride D + 40; k read in
+    place with a row stride above D)."""
     from minference.modules.minference_forward import build_layer_plan, run_layer_attention
 
     H, D = 4, 96
     pats = _mixed_patterns(H)
     q, k, v = make_qkv(1, H, S, S, D, torch.bfloat16, seed=S, sink_scale=8.0)
     plan = build_layer_plan(pats, H, D, S)
-    dk, dv = k.to(gpu_device), v.to(gpu_device)
-    base = q[:, :, :1].to(gpu_device)
-    flat = q.reshape(1, H, -1)[:, :, :(S + 1) * D // 2].contiguous().to(gpu_device)
+    src = q if which == "q" else k
+    base = src[:, :, :1].to(gpu_device)
+    flat = src.reshape(1, H, -1)[:, :, :(S + 1) * D // 2].contiguous().to(gpu_device)
+    wide = torch.zeros((1, H, S, D + 40), dtype=src.dtype)
+    wide[..., :D] = src
     views = {
         "expanded": base.expand(1, H, S, D),
         "overlapping": flat.as_strided((1, H, S, D), (H * flat.shape[-1], flat.shape[-1], D // 2, 1)),
+        "padded": wide.to(gpu_device)[..., :D],
     }
-    for name, dq in views.items():
+    for name, dx in views.items():
+        print(f"[strided rows] {which} {name} S={S}", flush=True)
+        dq = dx if which == "q" else q.to(gpu_device)
+        dk = dx if which == "k" else k.to(gpu_device)
         out = torch.empty((1, H, S, D), dtype=torch.float32, device=gpu_device)
-        run_layer_attention(dq, dk, dv, plan, out)
-        ref, _ = O.layer_attention(np32(dq.cpu().contiguous()), np32(k), np32(v),
-                                   [pats[h] for h in range(H)], "bf16")
-        assert_close_f32(out, ref, what=f"{name} q rows S={S}")
+        run_layer_attention(dq, dk, v.to(gpu_device), plan, out)
+        ref, _ = O.layer_attention(np32(dq.cpu().contiguous()), np32(dk.cpu().contiguous()),
+                                   np32(v), [pats[h] for h in range(H)], "bf16")
+        assert_close_f32(out, ref, what=f"{name} {which} rows S={S}")
