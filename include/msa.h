@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MSA_ABI_VERSION 10
+#define MSA_ABI_VERSION 11
 
 /* status codes (negative: validation, nothing launched) */
 #define MSA_OK 0
@@ -190,13 +190,17 @@ int msa_layer_attention(const msa_tensor4* q, const msa_tensor4* k,
 
 /* The two launches msa_layer_attention makes, callable separately (so a
  * caller can time the attention kernel alone, or reuse one staging):
- *   msa_stage_kv: K and V [B][H_kv][S_k][D] -> MFMA operand order in the
- *                workspace (msa_attention_workspace_bytes bytes); k and v
- *                have the same shape and dtype;
+ *   msa_stage_kv: V [B][H_kv][S_k][D] -> MFMA operand order in the
+ *                workspace (msa_attention_workspace_bytes bytes), and K too
+ *                when the attention kernel cannot read it in place (rows
+ *                that overlap, row stride < D, or one kv head's padded rows
+ *                spanning more than 2^31 bytes); k and v have the same shape
+ *                and dtype;
  *   msa_layer_attention_staged: same arguments and checks as
- *                msa_layer_attention, reads K and V staged by msa_stage_kv
- *                from the same workspace on the same stream (k and v give
- *                shapes only).
+ *                msa_layer_attention, reads V (and K where it was staged)
+ *                from the workspace msa_stage_kv wrote on the same stream,
+ *                and K in place from k otherwise: k and v must be the views
+ *                msa_stage_kv received.
  * Same reference counterpart as msa_layer_attention. */
 int msa_stage_kv(const msa_tensor4* k, const msa_tensor4* v, void* workspace,
                  size_t workspace_bytes, msa_stream_t stream);
