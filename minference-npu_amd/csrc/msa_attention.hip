@@ -429,7 +429,10 @@ struct AttnShape {
   static constexpr int NDB = D / 32;              // PV output blocks of 32 dims (= V loads)
   static constexpr int CHUNK_BYTES = 16 * D * 2;  // one staged 16-key V chunk
   static constexpr int NO = NDB * 2 * 16;         // O accumulator floats per lane
-  static constexpr int SLOT = (NO + 4) * 64;      // merge slot of one wave (floats)
+  // merge area (floats): every wave's (m, l) of its rows, then per owner
+  // wave v the three other waves' floats 4v .. 4v+3 of each O block
+  static constexpr int ML = 4 * 64 * 4;
+  static constexpr int MERGE = ML + 4 * 3 * (2 * NDB) * 64 * 4;
 };
 
 // Next item of the persistent attention grid: the home XCD's range first,
@@ -455,7 +458,7 @@ void attn_kernel(AttnParams P) {
   using S = AttnShape<D>;
   constexpr int NKS = S::NKS;
   constexpr int NDB = S::NDB;
-  __shared__ __align__(16) float lds[3 * S::SLOT];
+  __shared__ __align__(16) float lds[S::MERGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -886,11 +889,14 @@ void attn_kernel(AttnParams P) {
     run(std::integral_constant<bool, true>(), mpos, total);
   };
 
-  // ---- merge the four chunk partials of each row; wave 0 writes the rows
-  // of the item (batch ib, head ih, first row iq0; iv = 2^vexp of its head).
-  // Block layout: lane rows 1, 3 hold group 2rb+1.  Chosen by an exact blend
-  // (the maxima are finite) rather than a select, which the compiler turns
-  // into a lane-indexed load from a private copy of m_g.
+  // ---- merge the four chunk partials of each row and write the item's rows
+  // (batch ib, head ih, first row iq0; iv = 2^vexp of its head).  Wave v
+  // owns floats 4v .. 4v+3 of every O block (output columns 32 db + 8 v ..
+  // +7): every wave puts its (m, l) and the other owners' floats in LDS,
+  // then combines and stores its own columns.  Block layout: lane rows 1, 3
+  // hold group 2rb+1, chosen by an exact blend (the maxima are finite)
+  // rather than a select, which the compiler turns into a lane-indexed load
+  // from a private copy of m_g.
   auto merge_store = [&](const int ib, const int ih, const int iq0, const float iv) INLINE {
     float m_b[2], l_b[2];
     const float odd = float(lr & 1);
@@ -898,74 +904,90 @@ void attn_kernel(AttnParams P) {
     for (int rb = 0; rb < 2; ++rb)
       m_b[rb] = __builtin_fmaf(odd, m_g[2 * rb + 1], (1.0f - odd) * m_g[2 * rb]);
     lanes_to_blocks(reduce_rows(l_g[0], l_g[1], l_g[2], l_g[3], RowSum()), l_b);
-    if (w > 0) {
-      float* slot = lds + (w - 1) * S::SLOT;
+    float4* ml = reinterpret_cast<float4*>(lds);
+    // part[((v * 3 + k) * 2 NDB + db * 2 + rb) * 64 + lane]: floats 4v .. 4v+3
+    // of o[db][rb] of wave c (k = c < v ? c : c - 1) for owner v
+    float4* part = reinterpret_cast<float4*>(lds + S::ML);
+    ml[w * 64 + lane] = make_float4(m_b[0], m_b[1], l_b[0], l_b[1]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (v == w) continue;
+      const int k = w < v ? w : w - 1;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) slot[((db * 2 + rb) * 16 + i) * 64 + lane] = o[db][rb][i];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        slot[(S::NO + rb) * 64 + lane] = m_b[rb];
-        slot[(S::NO + 2 + rb) * 64 + lane] = l_b[rb];
-      }
+          part[((v * 3 + k) * 2 * NDB + db * 2 + rb) * 64 + lane] =
+              make_float4(o[db][rb][4 * v], o[db][rb][4 * v + 1], o[db][rb][4 * v + 2],
+                          o[db][rb][4 * v + 3]);
     }
     __syncthreads();
-    if (w == 0) {
+    float4 mlc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) mlc[c] = ml[c * 64 + lane];
+    auto combine = [&](auto wc) INLINE {
+      constexpr int W = decltype(wc)::value;
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
         float mw[4], lw[4];
-        mw[0] = m_b[rb];
-        lw[0] = l_b[rb];
 #pragma unroll
-        for (int v = 1; v < 4; ++v) {
-          mw[v] = lds[(v - 1) * S::SLOT + (S::NO + rb) * 64 + lane];
-          lw[v] = lds[(v - 1) * S::SLOT + (S::NO + 2 + rb) * 64 + lane];
+        for (int c = 0; c < 4; ++c) {
+          mw[c] = rb ? mlc[c].y : mlc[c].x;
+          lw[c] = rb ? mlc[c].w : mlc[c].z;
         }
         const float mt = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
         float f[4];
         float lt = 0.0f;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          f[v] = __builtin_amdgcn_exp2f(mw[v] - mt);
-          lt += lw[v] * f[v];
+        for (int c = 0; c < 4; ++c) {
+          f[c] = __builtin_amdgcn_exp2f(mw[c] - mt);
+          lt += lw[c] * f[c];
         }
         const float inv = lt > 0.0f ? iv / lt : 0.0f;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) f[v] *= inv;
+        for (int c = 0; c < 4; ++c) f[c] *= inv;
 
         const int row = iq0 + 32 * rb + (lane & 31);
         if (row < P.s_q) {
           const int64_t obase = ib * P.o_sb + int64_t(ih) * P.o_sh + int64_t(row) * P.o_ss;
 #pragma unroll
           for (int db = 0; db < NDB; ++db) {
+            float4 pc[4];
 #pragma unroll
-            for (int qd = 0; qd < 4; ++qd) {
-              float v4[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int i = 4 * qd + e;
-                const int r = (db * 2 + rb) * 16 + i;
-                float acc = o[db][rb][i] * f[0];
-#pragma unroll
-                for (int v = 1; v < 4; ++v) acc += lds[(v - 1) * S::SLOT + r * 64 + lane] * f[v];
-                v4[e] = acc;
-              }
-              const int d = 32 * db + 8 * qd + 4 * (lane >> 5);
-              if constexpr (OUT_F32) {
-                store_out4<float>(reinterpret_cast<float*>(P.o) + obase + d, v4[0], v4[1], v4[2],
-                                  v4[3]);
+            for (int c = 0; c < 4; ++c) {
+              if (c == W) {
+                pc[c] = make_float4(o[db][rb][4 * W], o[db][rb][4 * W + 1], o[db][rb][4 * W + 2],
+                                    o[db][rb][4 * W + 3]);
               } else {
-                store_out4_16<T>(reinterpret_cast<uint16_t*>(P.o) + obase + d, v4[0], v4[1],
-                                 v4[2], v4[3]);
+                const int k = c < W ? c : c - 1;
+                pc[c] = part[((W * 3 + k) * 2 * NDB + db * 2 + rb) * 64 + lane];
               }
+            }
+            // the four waves' terms added in wave order, one rounding each
+            float v4[4] = {pc[0].x * f[0], pc[0].y * f[0], pc[0].z * f[0], pc[0].w * f[0]};
+#pragma unroll
+            for (int c = 1; c < 4; ++c) {
+              v4[0] = __builtin_fmaf(pc[c].x, f[c], v4[0]);
+              v4[1] = __builtin_fmaf(pc[c].y, f[c], v4[1]);
+              v4[2] = __builtin_fmaf(pc[c].z, f[c], v4[2]);
+              v4[3] = __builtin_fmaf(pc[c].w, f[c], v4[3]);
+            }
+            const int d = 32 * db + 8 * W + 4 * (lane >> 5);
+            if constexpr (OUT_F32) {
+              store_out4<float>(reinterpret_cast<float*>(P.o) + obase + d, v4[0], v4[1], v4[2],
+                                v4[3]);
+            } else {
+              store_out4_16<T>(reinterpret_cast<uint16_t*>(P.o) + obase + d, v4[0], v4[1],
+                               v4[2], v4[3]);
             }
           }
         }
       }
-    }  // w == 0
+    };
+    if (w == 0) combine(std::integral_constant<int, 0>());
+    else if (w == 1) combine(std::integral_constant<int, 1>());
+    else if (w == 2) combine(std::integral_constant<int, 2>());
+    else combine(std::integral_constant<int, 3>());
   };
 
   if constexpr (VS) {
