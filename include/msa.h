@@ -294,8 +294,8 @@ size_t msa_vs_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_k, int32
  * for the vertical_and_slash heads (the other heads keep their own launch).
  * vertical_and_slash heads need S_q == S_k <= MSA_VS_MAX_SEQ and
  * B * H <= MSA_MAX_HEADS.  vs and vs_workspace may be NULL when no head is
- * vertical_and_slash.  stage = 0 reads K/V staged by msa_stage_kv (as
- * msa_layer_attention_staged), 1 stages them first. */
+ * vertical_and_slash.  stage = 0 reads what msa_stage_kv staged for the
+ * same k and v (as msa_layer_attention_staged), 1 stages first. */
 int msa_layer_attention_ex(const msa_tensor4* q, const msa_tensor4* k, const msa_tensor4* v,
                            const msa_tensor4* o, const msa_head_desc* heads, int32_t n_heads,
                            const int32_t* idx, const int32_t* cnt, int32_t idx_slots,

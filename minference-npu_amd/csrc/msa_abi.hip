@@ -243,8 +243,9 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
 }
 
 // Attention workspace: staged V operands (fp16), staged K operands (input
-// dtype), per-tile V maxima (fp32), per-head V exponents (int32), then the
-// work-queue counters of the attention launch.
+// dtype; written only where the attention kernel cannot read K in place,
+// see k_in_place), per-tile V maxima (fp32), per-head V exponents (int32),
+// then the work-queue counters of the attention launch.
 struct AttnLayout {
   size_t vt, kt, tmax, vexp, total;
 };

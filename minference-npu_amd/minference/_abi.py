@@ -413,8 +413,8 @@ def stage_kv(k: torch.Tensor, v: torch.Tensor, ws: torch.Tensor) -> None:
 def stage_kv_pool(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                   slot_heads: Sequence[int], est_ws: Optional[torch.Tensor],
                   ws: torch.Tensor) -> None:
-    """Launch msa_stage_kv_pool on the current stream: K/V staged into ``ws``
-    and, for the block slots ``slot_heads``, Q and K pooled into ``est_ws``
+    """Launch msa_stage_kv_pool on the current stream: V (and K where the
+    attention kernel cannot read it in place) staged into ``ws`` and, for the block slots ``slot_heads``, Q and K pooled into ``est_ws``
     (the workspace of the MSA_ESTIMATE_SELECT_ONLY block_estimate call that
     follows)."""
     n = len(slot_heads)
@@ -476,7 +476,8 @@ def layer_attention(
     vs_ws: Optional[torch.Tensor] = None,
 ) -> None:
     """Launch msa_layer_attention (or, with ``staged=True``,
-    msa_layer_attention_staged reading the K and V already staged in ``ws``).
+    msa_layer_attention_staged reading what msa_stage_kv staged in ``ws``
+    for the same k and v).
     ``heads`` = [(kind, p1, p2, slot, scale)] * H.  With vertical_and_slash
     heads, ``vs`` = (v_idx [B,slots,nv], v_cnt [B,slots], s_idx [B,slots,ns],
     s_cnt [B,slots]) int32 contiguous device tensors and the call goes to

@@ -27,6 +27,6 @@ def test_traffic_comes_from_the_committed_profile():
     assert isinstance(t, int) and t > 0
     text = open(os.path.join(ROOT, "profiles", "attn_kernel_headline64k_traffic.txt")).read()
     assert f"attn_kernel traffic_bytes_per_step: {t}" in text
-    # the calibrated traffic is at least the launch's algorithmic bytes (Q, staged K/V, O)
+    # the calibrated traffic is at least the launch's algorithmic bytes (Q, K, staged V, O)
     assert t >= 32 * 65536 * 96 * 2 * 4
     assert bench.profiled_traffic("no_such_workload") is None
