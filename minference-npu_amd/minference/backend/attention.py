@@ -13,11 +13,13 @@ from typing import Optional
 import torch
 
 from .. import _abi
-from ..ops.common import check_bnsd, check_supported, dense_scale, head_chunks, padded_call
+from ..ops.common import (accepts_float32, check_bnsd, check_supported, dense_scale, head_chunks,
+                          padded_call)
 
 __all__ = ["dense_attention", "prefill_dense", "decode_dense"]
 
 
+@accepts_float32(("q", "k", "v"))
 def dense_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -52,6 +54,7 @@ def prefill_dense(q, k, v, *, scale: Optional[float] = None, causal: bool = True
     return dense_attention(q, k, v, scale=scale, causal=causal)
 
 
+@accepts_float32(("q", "k_cache", "v_cache"))
 def decode_dense(
     q: torch.Tensor,
     k_cache: torch.Tensor,

@@ -18,8 +18,8 @@ from typing import Optional, Tuple
 import torch
 
 from .. import _abi
-from .common import (check_bnsd, check_supported, head_chunks, kernel_head_dim, kernel_view,
-                     pad_head_dim, padded_call, sparse_scale)
+from .common import (accepts_float32, check_bnsd, check_supported, head_chunks, kernel_head_dim,
+                     kernel_view, pad_head_dim, padded_call, sparse_scale)
 
 __all__ = [
     "block_sparse_attention",
@@ -67,6 +67,7 @@ def _estimate(q: torch.Tensor, k: torch.Tensor, topk: int, scale: float, flags: 
     return chunks
 
 
+@accepts_float32(("q", "k"), has_out=False)
 def select_block_sparse_topk_indices(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -110,6 +111,7 @@ def select_block_sparse_topk_indices(
 _select_block_sparse_topk_indices = select_block_sparse_topk_indices
 
 
+@accepts_float32(("q", "k", "v"))
 def block_sparse_attention_with_indices(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -174,6 +176,7 @@ def _run(q, k, v, chunks, topk, scale, result):
     return result
 
 
+@accepts_float32(("q", "k", "v"))
 def block_sparse_attention(
     q: torch.Tensor,
     k: torch.Tensor,

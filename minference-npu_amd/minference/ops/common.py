@@ -2,8 +2,10 @@
 
 from __future__ import annotations
 
+import functools
+import inspect
 import math
-from typing import Optional
+from typing import Optional, Sequence
 
 import torch
 
@@ -17,6 +19,53 @@ ALLOWED_HEAD_DIMS = (16, 32, 64, 128, 256, 512)
 # largest of them by zero-padding q, k and v to the next one.
 SUPPORTED_HEAD_DIMS = (64, 96, 128)
 SUPPORTED_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def sixteen_bit_dtype(tensors: Sequence[torch.Tensor]) -> torch.dtype:
+    """The 16-bit type float32 op inputs are rounded to on the device: fp16
+    (11 significant bits) when every finite value lies within its range,
+    else bf16; non-finite values stay non-finite in either."""
+    lim = torch.finfo(torch.float16).max
+    for t in tensors:
+        if t.numel() and float(torch.where(torch.isfinite(t), t.abs(), 0.0).amax()) > lim:
+            return torch.bfloat16
+    return torch.float16
+
+
+def accepts_float32(names: Sequence[str], has_out: bool = True):
+    """Decorator for the public ops: called with float32 tensors ``names``,
+    the op runs on their on-device roundings to sixteen_bit_dtype and, when
+    it has an output, writes it in float32 (``out`` must then be float32 or
+    None).  The reference's CPU paths take any float dtype and compute in
+    fp32 (minference/ops/streaming_kernel_npu.py:138-144,
+    minference/ops/block_sparse_kernel_npu.py:340-348); here float32 inputs
+    get the 16-bit kernels' arithmetic on their roundings.  Inputs of other
+    dtypes go to the op unchanged (bf16 / fp16, or its dtype error)."""
+
+    def wrap(fn):
+        sig = inspect.signature(fn)
+
+        @functools.wraps(fn)
+        def inner(*args, **kwargs):
+            ba = sig.bind(*args, **kwargs)
+            ts = [ba.arguments.get(n) for n in names]
+            if not all(isinstance(t, torch.Tensor) and t.dtype == torch.float32 for t in ts):
+                return fn(*args, **kwargs)
+            dt = sixteen_bit_dtype(ts)
+            for n, t in zip(names, ts):
+                ba.arguments[n] = t.to(dt)
+            if has_out:
+                out = ba.arguments.get("out")
+                if out is None:
+                    ba.arguments["out"] = torch.empty(ts[0].shape, dtype=torch.float32,
+                                                      device=ts[0].device)
+                elif out.dtype != torch.float32:
+                    raise ValueError(f"out must be float32 for float32 inputs, got {out.dtype}")
+            return fn(*ba.args, **ba.kwargs)
+
+        return inner
+
+    return wrap
 
 
 def next_allowed_head_dim(d: int) -> int:

@@ -14,11 +14,13 @@ from typing import Optional
 import torch
 
 from .. import _abi
-from .common import check_bnsd, check_supported, head_chunks, padded_call, sparse_scale
+from .common import (accepts_float32, check_bnsd, check_supported, head_chunks, padded_call,
+                     sparse_scale)
 
 __all__ = ["streaming_forward"]
 
 
+@accepts_float32(("q", "k", "v"))
 def streaming_forward(
     q: torch.Tensor,
     k: torch.Tensor,

@@ -22,7 +22,7 @@ from typing import Optional
 import torch
 
 from .. import _abi
-from .common import (check_bnsd, check_supported, kernel_view, make_out,
+from .common import (accepts_float32, check_bnsd, check_supported, kernel_view, make_out,
                      require_kernel_head_dim, sparse_scale)
 
 __all__ = [
@@ -70,6 +70,7 @@ def _check_vs_shape(q: torch.Tensor, k: torch.Tensor) -> None:
         )
 
 
+@accepts_float32(("q", "k"), has_out=False)
 def vertical_and_slash_estimate(q: torch.Tensor, k: torch.Tensor, vertical_size: int,
                                 slash_size: int):
     """Vertical and slash indices of every head (minference_forward.py:140-165):
@@ -100,6 +101,7 @@ def vertical_and_slash_estimate(q: torch.Tensor, k: torch.Tensor, vertical_size:
     return v_idx.long(), s_idx.long()
 
 
+@accepts_float32(("q", "k", "v"))
 def vertical_and_slash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                  vertical_size: int, slash_size: int, *,
                                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -143,6 +145,7 @@ def run_vs_heads(q, k, v, result, v_ids, v_cnt, s_idx, scale):
     return result
 
 
+@accepts_float32(("query", "key", "value"))
 def vertical_slash_sparse_attention(
     query: torch.Tensor,
     key: torch.Tensor,

@@ -394,3 +394,44 @@ def test_head_dim_padding_helpers():
 
     out = C.padded_call(t, t, t, None, fn)
     assert seen["d"] == 64 and out.shape == t.shape and torch.equal(out, t + 1)
+
+
+def test_float32_inputs_round_to_16_bit():
+    """float32 op inputs: fp16 when every finite value fits its range, else
+    bf16 (non-finite values ignored by the rule); the decorator hands the op
+    the roundings and a float32 output, passes other dtypes through, and
+    refuses a non-float32 ``out`` for float32 inputs."""
+    import torch
+
+    from minference.ops import common as C
+
+    small = torch.tensor([[1.0, -65504.0, float("inf"), float("nan")]])
+    big = torch.tensor([[1.0, 70000.0]])
+    assert C.sixteen_bit_dtype([small, small]) == torch.float16
+    assert C.sixteen_bit_dtype([small, big]) == torch.bfloat16
+    assert C.sixteen_bit_dtype([torch.empty(0)]) == torch.float16
+
+    seen = {}
+
+    @C.accepts_float32(("q", "k"))
+    def op(q, k, scale=1.0, *, out=None):
+        seen.update(q=q.dtype, k=k.dtype, out=None if out is None else out.dtype, scale=scale)
+        return out
+
+    q = torch.ones(1, 2, 3, 4)
+    res = op(q, q * 2, 0.5)
+    assert seen == {"q": torch.float16, "k": torch.float16, "out": torch.float32, "scale": 0.5}
+    assert res.dtype == torch.float32 and res.shape == q.shape
+    op(q, q * 1e5)
+    assert seen["q"] == torch.bfloat16 and seen["k"] == torch.bfloat16
+    seen.clear()
+    op(q.bfloat16(), q.bfloat16())
+    assert seen["q"] == torch.bfloat16 and seen["out"] is None
+    with pytest.raises(ValueError):
+        op(q, q, out=torch.empty(q.shape, dtype=torch.bfloat16))
+
+    @C.accepts_float32(("q",), has_out=False)
+    def sel(q):
+        return q.dtype
+
+    assert sel(q) == torch.float16

@@ -497,3 +497,54 @@ def test_mixed_layer_strided_rows(gpu_device, S, which):
         ref, _ = O.layer_attention(np32(dq.cpu().contiguous()), np32(dk.cpu().contiguous()),
                                    np32(v), [pats[h] for h in range(H)], "bf16")
         assert_close_f32(out, ref, what=f"{name} {which} rows S={S}")
+
+
+# ---------------------------------------------------------------------------
+# float32 inputs
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rng", ["fp16", "bf16"])
+def test_float32_inputs(gpu_device, rng):
+    """float32 q/k/v (the reference's CPU paths compute them in fp32,
+    streaming_kernel_npu.py:138-144, block_sparse_kernel_npu.py:340-348) run
+    as their on-device roundings to fp16, or to bf16 when a finite value
+    exceeds fp16's range, with a float32 output: every op equals the same
+    call on the explicitly rounded inputs, bit for bit, and the stream op
+    stays within the fp32-output tolerance of the oracle on those roundings.
+    (Against the oracle on the float32 inputs themselves the fp16 rounding of
+    q and k moves this case's outputs by up to about 8e-3: the sink keys are
+    scaled by 8, so their logits carry the larger rounding.)"""
+    from minference import block_sparse_attention, dense_attention, streaming_forward
+    from minference.backend.attention import decode_dense
+    from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
+    from minference.ops.vertical_slash_kernel import vertical_slash_sparse_attention
+
+    print(f"[float32 inputs] {rng}", flush=True)
+    B, H, S, D = 1, 4, 700, 96
+    q, k, v = make_qkv(B, H, S, S, D, torch.float32, seed=21, sink_scale=8.0)
+    if rng == "bf16":
+        v = v.clone()
+        v[0, 1, 5, 3] = 1.0e5
+    dt = torch.float16 if rng == "fp16" else torch.bfloat16
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    rq, rk, rv = (t.to(dt) for t in (dq, dk, dv))
+    vi = torch.arange(0, S, 9).expand(B, H, -1)
+    si = torch.arange(198, -1, -3).expand(B, H, -1)
+    calls = {
+        "stream": lambda a, b, c, **o: streaming_forward(a, b, c, 64, 256, **o),
+        "block": lambda a, b, c, **o: block_sparse_attention(a, b, c, 5, **o),
+        "dense": lambda a, b, c, **o: dense_attention(a, b, c, **o),
+        "decode": lambda a, b, c, **o: decode_dense(a[:, :, -1:], b, c, **o),
+        "vs": lambda a, b, c, **o: vertical_slash_sparse_attention(a, b, c, vi, si, **o),
+    }
+    for name, call in calls.items():
+        got = call(dq, dk, dv)
+        assert got.dtype == torch.float32, name
+        ref = torch.empty(got.shape, dtype=torch.float32, device=gpu_device)
+        call(rq, rk, rv, out=ref)
+        assert torch.equal(got, ref), name
+    # the selector sees q and k only, which fit fp16 in both cases
+    assert torch.equal(select_block_sparse_topk_indices(dq, dk, 5),
+                       select_block_sparse_topk_indices(dq.half(), dk.half(), 5))
+    if rng == "fp16":
+        ref = O.streaming_attention(np32(rq), np32(rk), np32(rv), 64, 256)
+        assert_close_f32(streaming_forward(dq, dk, dv, 64, 256), ref, what="float32 stream")
