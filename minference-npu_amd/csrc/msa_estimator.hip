@@ -38,6 +38,8 @@
 
 namespace msa {
 
+#define INLINE __attribute__((always_inline))
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void pool_kernel(PoolParams P) {
   pool_workgroup<T, D>(P, int(blockIdx.x));
@@ -66,14 +68,27 @@ __device__ inline float key_float(uint32_t k) {
 
 __device__ inline int popc_ballot(bool p) { return __popcll(__ballot(p)); }
 
-// f(j) for the key chunks j < nj; N > 0: at most N chunks, unrolled so that
-// register-held keys are indexed statically.
+// f(j) for the key chunks j < nj (nj wave-uniform).  N > 0: register-held
+// keys, indexed statically: f runs unconditionally on the first N, N/2 or
+// N/4 chunks, the fewest that cover nj (one branch, none per chunk), so f
+// must leave chunks past nj as it found them and count nothing there (every
+// caller's keys past its row are 0, below every threshold and every
+// selection).
 template <int N, typename F>
 __device__ inline void for_chunks(int nj, F f) {
   if constexpr (N > 0) {
+    constexpr int N2 = N / 2 > 0 ? N / 2 : 1;
+    constexpr int N4 = N / 4 > 0 ? N / 4 : 1;
+    if (nj > N2) {
 #pragma unroll
-    for (int j = 0; j < N; ++j)
-      if (j < nj) f(j);
+      for (int j = 0; j < N; ++j) f(j);
+    } else if (nj > N4) {
+#pragma unroll
+      for (int j = 0; j < N2; ++j) f(j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < N4; ++j) f(j);
+    }
   } else {
     for (int j = 0; j < nj; ++j) f(j);
   }
@@ -363,7 +378,9 @@ void score_topk_kernel(ScoreParams P) {
   const int ncand = min(rmax + 1, P.n_kb);  // causal candidates of the heaviest row
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int w = t >> 6;
+  // wave-uniform, so that the rows and their chunk counts are scalar values
+  // and the chunk loops branch once, not per lane
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int l16 = lane & 15;
   const int lq = lane >> 4;
   const int b = sb / P.n_slots;
@@ -527,28 +544,39 @@ void score_topk_kernel(ScoreParams P) {
         fin[i] = __ballot(nonfin) == 0ull;
       });
       // the pass's searches interleaved (independent reduction chains);
-      // rows that need no search (n <= topk or past the group) stay done
-      for (int bit = 31; bit >= 0; --bit) {
-        bool all_done = true;
+      // rows that need no search (n <= topk or past the group) stay done.
+      // Each round counts a fixed number of chunks, NB (KPL, KPL/2 or KPL/4,
+      // the smallest that covers the pass's rows), without a branch per
+      // chunk: keys past a row are 0 and every candidate is at least 1.
+      auto search = [&](auto nbc) INLINE {
+        constexpr int NB = decltype(nbc)::value;
+        for (int bit = 31; bit >= 0; --bit) {
+          bool all_done = true;
 #pragma unroll
-        for (int i = 0; i < RP; ++i) all_done = all_done && done[i];
-        if (all_done) break;
-        int ge[RP];
-        each_row([&](auto ic) {
-          constexpr int i = decltype(ic)::value;
-          const uint32_t cand = Ta[i] | (1u << bit);
-          int c = 0;
-          for_chunks<KPL>(njmax, [&](int j) { c += popc_ballot(keys[i][j] >= cand); });
-          ge[i] = c;
-        });
+          for (int i = 0; i < RP; ++i) all_done = all_done && done[i];
+          if (all_done) break;
+          int ge[RP];
+          each_row([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            const uint32_t cand = Ta[i] | (1u << bit);
+            int c = 0;
 #pragma unroll
-        for (int i = 0; i < RP; ++i) {
-          if (!done[i]) {
-            if (ge[i] >= topk) Ta[i] = Ta[i] | (1u << bit);
-            if (ge[i] == topk) done[i] = true;
+            for (int j = 0; j < NB; ++j) c += popc_ballot(keys[i][j] >= cand);
+            ge[i] = c;
+          });
+#pragma unroll
+          for (int i = 0; i < RP; ++i) {
+            if (!done[i]) {
+              if (ge[i] >= topk) Ta[i] = Ta[i] | (1u << bit);
+              if (ge[i] == topk) done[i] = true;
+            }
           }
         }
-      }
+      };
+      constexpr int NB4 = KPL / 4 > 0 ? KPL / 4 : 1;
+      if (njmax > KPL / 2) search(std::integral_constant<int, KPL>());
+      else if (njmax > NB4) search(std::integral_constant<int, (KPL / 2 > 0 ? KPL / 2 : 1)>());
+      else search(std::integral_constant<int, NB4>());
       each_row([&](auto ic) {
         constexpr int i = decltype(ic)::value;
         const int r = row_of(wave_slot(p0 + i));
