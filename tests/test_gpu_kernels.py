@@ -515,8 +515,11 @@ def test_float32_inputs(gpu_device, rng):
     scaled by 8, so their logits carry the larger rounding.)"""
     from minference import block_sparse_attention, dense_attention, streaming_forward
     from minference.backend.attention import decode_dense
-    from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
-    from minference.ops.vertical_slash_kernel import vertical_slash_sparse_attention
+    from minference.ops.block_sparse_kernel import (block_sparse_attention_with_indices,
+                                                    select_block_sparse_topk_indices)
+    from minference.ops.vertical_slash_kernel import (vertical_and_slash_attention,
+                                                      vertical_and_slash_estimate,
+                                                      vertical_slash_sparse_attention)
 
     print(f"[float32 inputs] {rng}", flush=True)
     B, H, S, D = 1, 4, 700, 96
@@ -535,16 +538,22 @@ def test_float32_inputs(gpu_device, rng):
         "dense": lambda a, b, c, **o: dense_attention(a, b, c, **o),
         "decode": lambda a, b, c, **o: decode_dense(a[:, :, -1:], b, c, **o),
         "vs": lambda a, b, c, **o: vertical_slash_sparse_attention(a, b, c, vi, si, **o),
+        "block ids": lambda a, b, c, **o: block_sparse_attention_with_indices(a, b, c, bi, **o),
+        "vs layer": lambda a, b, c, **o: vertical_and_slash_attention(a, b, c, 100, 200, **o),
     }
+    bi = torch.randint(0, S // 64 + 1, (B, H, S // 64 + 1, 4), generator=torch.Generator().manual_seed(3))
     for name, call in calls.items():
         got = call(dq, dk, dv)
         assert got.dtype == torch.float32, name
         ref = torch.empty(got.shape, dtype=torch.float32, device=gpu_device)
         call(rq, rk, rv, out=ref)
         assert torch.equal(got, ref), name
-    # the selector sees q and k only, which fit fp16 in both cases
+    # the estimators see q and k only, which fit fp16 in both cases
     assert torch.equal(select_block_sparse_topk_indices(dq, dk, 5),
                        select_block_sparse_topk_indices(dq.half(), dk.half(), 5))
+    for a, b in zip(vertical_and_slash_estimate(dq, dk, 100, 200),
+                    vertical_and_slash_estimate(dq.half(), dk.half(), 100, 200)):
+        assert torch.equal(a, b)
     if rng == "fp16":
         ref = O.streaming_attention(np32(rq), np32(rk), np32(rv), 64, 256)
         assert_close_f32(streaming_forward(dq, dk, dv, 64, 256), ref, what="float32 stream")
