@@ -38,7 +38,7 @@ extern "C" {
 #define MSA_E_DTYPE (-3)       /* unsupported or mismatched dtype */
 #define MSA_E_HEAD_DIM (-4)    /* D not in {64, 96, 128} */
 #define MSA_E_ALIGN (-5)       /* D stride != 1, rows not 16-byte aligned or row stride >= 2^24 */
-#define MSA_E_BLOCK (-6)       /* block size other than 64 */
+#define MSA_E_BLOCK (-6)       /* unsupported block size */
 #define MSA_E_TOPK (-7)        /* topk < 1 or topk > n_kv_blocks */
 #define MSA_E_HEADS (-8)       /* bad head count / head index / kind */
 #define MSA_E_WORKSPACE (-9)   /* workspace missing or too small */
@@ -69,7 +69,7 @@ extern "C" {
 #define MSA_VS_MAX_SEQ 131072 /* longest S of a vertical_and_slash head */
 
 #define MSA_MAX_HEADS 128 /* head descriptors per msa_layer_attention call */
-#define MSA_BLOCK 64      /* the only supported block size */
+#define MSA_BLOCK 64      /* tile of the attention kernels; estimator blocks are 64, 128, 256 or 512 */
 
 typedef struct msa_tensor4 {
   void* data;
@@ -111,8 +111,10 @@ size_t msa_estimate_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_q,
 
 /* Block top-k estimator for the block_sparse heads of a layer (one call for
  * all of them).  Replaces _select_block_sparse_topk_indices
- * (minference/ops/block_sparse_kernel_npu.py:230-263): 64-token mean pooling
- * of Q and K in the input dtype (rounded to it), fp32 pooled scores
+ * (minference/ops/block_sparse_kernel_npu.py:230-263): block-token mean
+ * pooling of Q and K in the input dtype (rounded to it; block = 64, 128, 256
+ * or 512 tokens, the reference's block_size; ids, n_qb and n_kv_blocks are
+ * in those blocks), fp32 pooled scores
  * q_pool.k_pool * score_scale, block-causal mask in the q-block frame, top-k
  * per query block, ids sorted ascending.  Ties break to the lower block id.
  *   slot_heads[s] (host array) = head index in q for slot s, s < n_slots
@@ -147,8 +149,8 @@ int msa_block_estimate(const msa_tensor4* q, const msa_tensor4* k,
  * SELECT_ONLY (one of them at a time) launch one pass, so a caller can run
  * the pooling first and the selection beside other work.  A SELECT_ONLY call
  * reads the pooled Q and K that a POOL_ONLY call with the same arguments left
- * in the same workspace, and must be ordered after it (same stream, or an
- * event); a POOL_ONLY call leaves idx and cnt untouched.  Same counterpart
+ * in the same workspace (and block), and must be ordered after it (same
+ * stream, or an event); a POOL_ONLY call leaves idx and cnt untouched.  Same counterpart
  * as msa_block_estimate
  * (minference/ops/block_sparse_kernel_npu.py:230-263). */
 int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k,

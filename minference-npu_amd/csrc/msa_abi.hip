@@ -77,7 +77,7 @@ const char* msa_status_str(int status) {
     case MSA_E_DTYPE: return "unsupported or mismatched dtype (q/k/v must be bf16 or fp16; o same or fp32)";
     case MSA_E_HEAD_DIM: return "head_dim must be 64, 96 or 128";
     case MSA_E_ALIGN: return "head_dim stride must be 1, rows 16-byte aligned and the row stride below 2^24";
-    case MSA_E_BLOCK: return "block size must be 64";
+    case MSA_E_BLOCK: return "block size must be 64, 128, 256 or 512";
     case MSA_E_TOPK: return "topk must be in [1, n_kv_blocks]";
     case MSA_E_HEADS: return "bad head count, head index or head kind";
     case MSA_E_WORKSPACE: return "workspace missing or too small";
@@ -103,11 +103,12 @@ struct EstLayout {
   size_t q, k, sc, total;
 };
 
-EstLayout est_layout(int64_t batch, int64_t n_slots, int64_t s_q, int64_t s_k, int64_t D) {
+EstLayout est_layout(int64_t batch, int64_t n_slots, int64_t s_q, int64_t s_k, int64_t D,
+                     int64_t block = MSA_BLOCK) {
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   EstLayout L;
-  L.n_qb = int(cdiv(s_q, MSA_BLOCK));
-  L.n_kb = int(cdiv(s_k, MSA_BLOCK));
+  L.n_qb = int(cdiv(s_q, block));
+  L.n_kb = int(cdiv(s_k, block));
   L.n_qb_pad = int(cdiv(L.n_qb, kScoreRowPad) * kScoreRowPad);
   L.n_kb_pad = int(cdiv(L.n_kb, 16) * 16);
   const int64_t sb = batch * n_slots;
@@ -122,7 +123,7 @@ EstLayout est_layout(int64_t batch, int64_t n_slots, int64_t s_q, int64_t s_k, i
 // (slot -> distinct kv head entry in slot_kvp).
 int pool_setup(const msa_tensor4* q, const msa_tensor4* k, const int32_t* slot_heads,
                int32_t n_slots, void* workspace, size_t workspace_bytes, PoolParams& pp,
-               int16_t* slot_kvp, EstLayout& L) {
+               int16_t* slot_kvp, EstLayout& L, int block = MSA_BLOCK) {
   int st = check_qk(q, k);
   if (st != MSA_OK) return st;
   if (!slot_heads) return MSA_E_NULL;
@@ -132,7 +133,7 @@ int pool_setup(const msa_tensor4* q, const msa_tensor4* k, const int32_t* slot_h
     if (slot_heads[s] < 0 || slot_heads[s] >= H) return MSA_E_HEADS;
   if (q->size[0] * n_slots > 65535) return MSA_E_HEADS;
   const int D = int(q->size[3]);
-  L = est_layout(q->size[0], n_slots, q->size[2], k->size[2], D);
+  L = est_layout(q->size[0], n_slots, q->size[2], k->size[2], D, block);
   if (score_rows_for(L.n_kb) == 0) return MSA_E_SEQ;
   if (!workspace || workspace_bytes < L.total) return MSA_E_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MSA_E_ALIGN;
@@ -146,6 +147,7 @@ int pool_setup(const msa_tensor4* q, const msa_tensor4* k, const int32_t* slot_h
   pp.n_qb = L.n_qb;
   pp.n_kb = L.n_kb;
   pp.n_qb_pad = L.n_qb_pad;
+  pp.pool_rows = block;
   pp.batch = int(q->size[0]);
   pp.n_slots = n_slots;
   pp.kv_group = int(q->size[1] / k->size[1]);
@@ -194,11 +196,13 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
   flags &= MSA_SELECT_FORCE_FIRST | MSA_SELECT_FORCE_DIAG;
   int st = check_qk(q, k);
   if (st != MSA_OK) return st;
-  if (block != MSA_BLOCK) return MSA_E_BLOCK;
+  if (block != MSA_BLOCK && block != 2 * MSA_BLOCK && block != 4 * MSA_BLOCK &&
+      block != 8 * MSA_BLOCK)
+    return MSA_E_BLOCK;
   if (!slot_heads || !idx || !cnt) return MSA_E_NULL;
   if (n_slots <= 0 || n_slots > kMaxHeads) return MSA_E_HEADS;
-  const int64_t n_kb64 = cdiv(k->size[2], MSA_BLOCK);
-  if (topk_max < 1 || topk_max > n_kb64) return MSA_E_TOPK;
+  const int64_t n_kb_blk = cdiv(k->size[2], block);
+  if (topk_max < 1 || topk_max > n_kb_blk) return MSA_E_TOPK;
   if (slot_topk)
     for (int s = 0; s < n_slots; ++s)
       if (slot_topk[s] < 1 || slot_topk[s] > topk_max) return MSA_E_TOPK;
@@ -206,7 +210,8 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
   PoolParams pp;
   int16_t slot_kvp[kMaxHeads];
   EstLayout L;
-  st = pool_setup(q, k, slot_heads, n_slots, workspace, workspace_bytes, pp, slot_kvp, L);
+  st = pool_setup(q, k, slot_heads, n_slots, workspace, workspace_bytes, pp, slot_kvp, L,
+                  block);
   if (st != MSA_OK) return st;
   const int D = int(q->size[3]);
 
@@ -232,6 +237,7 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
   sp.n_slots = n_slots;
   sp.s_q = int(q->size[2]);
   sp.s_k = int(k->size[2]);
+  sp.block = block;
   sp.scale = score_scale;
   sp.flags = flags;
   for (int s = 0; s < n_slots; ++s) {

@@ -478,8 +478,8 @@ void score_topk_kernel(ScoreParams P) {
     // count covers the selected ids plus those surplus ids whose first key
     // is at or before the block's last absolute row.
     for (int p = cnt + lane; p < topk; p += 64) out[p] = bq + 1 + (p - cnt);
-    const int a1 = P.s_k - P.s_q + min(64 * bq + 63, P.s_q - 1);
-    const int n_sur = max(0, min(topk - cnt, (a1 >> 6) - bq));
+    const int a1 = P.s_k - P.s_q + min(P.block * bq + P.block - 1, P.s_q - 1);
+    const int n_sur = max(0, min(topk - cnt, a1 / P.block - bq));
     if (lane == 0) P.cnt[int64_t(sb) * P.n_qb + bq] = cnt + n_sur;
   };
   // approximate key of candidate c of row r (forced ids above everything)

@@ -20,6 +20,7 @@ struct PoolParams {
   int64_t k_sb, k_sh, k_ss;
   int64_t s_q, s_k;
   int n_qb, n_kb, n_qb_pad;  // n_qb_pad: n_qb rounded up to kScoreRowPad
+  int pool_rows;             // rows per pooled block: 64, 128, 256 or 512
   int batch, n_slots, kv_group;
   int n_kvp;                 // distinct kv heads of the slots
   uint16_t* q_pool;
@@ -37,6 +38,7 @@ struct ScoreParams {
   int32_t* cnt;  // [batch*n_slots][n_qb]
   int n_qb, n_kb, n_qb_pad, n_kb_pad, topk_max, batch, n_slots;
   int s_q, s_k;  // row i of the query is absolute position s_k - s_q + i
+  int block;     // tokens per block (the pooling's rows)
   float scale;
   int flags;     // kSelectForceFirst | kSelectForceDiag
   int16_t slot_topk[kMaxHeads];

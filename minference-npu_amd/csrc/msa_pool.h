@@ -3,10 +3,11 @@
 //
 // Reference semantics: _select_block_sparse_topk_indices,
 // MInference-NPU/minference/ops/block_sparse_kernel_npu.py:240-252: the mean
-// of each 64-row block in the input dtype (a partial last block is zero
-// padded and still divided by 64), i.e. the fp32 mean rounded to bf16/fp16.
-// The 64-row sums are accumulated in fp64, exact for 16-bit inputs, so the
-// result is the correctly rounded mean whatever the summation order.
+// of each block of block_size rows (64, 128, 256 or 512) in the input dtype
+// (a partial last block is zero padded and still divided by block_size), i.e.
+// the fp32 mean rounded to bf16/fp16.  The block sums are accumulated in
+// fp64, exact for 16-bit inputs, so the result is the correctly rounded mean
+// whatever the summation order; dividing by a power of two is exact.
 #pragma once
 
 #include "msa_common.h"
@@ -27,11 +28,12 @@ __host__ __device__ inline int pool_wg_count(const PoolParams& p) {
 
 // One workgroup of 256 threads pools blocks blk0 .. blk0 + 15 (those below
 // nb) of a [S][D] matrix with row stride ss into dst [nb][D]; thread (bg, c)
-// sums 16-byte chunk c of block blk0 + bg over its 64 rows, eight rows'
-// loads in flight, and stores the 8 pooled values as one 16-byte chunk.
+// sums 16-byte chunk c of block blk0 + bg over its brows rows (a multiple of
+// 8), eight rows' loads in flight, and stores the 8 pooled values as one
+// 16-byte chunk.
 template <typename T, int D>
 __device__ inline void pool_block_group(const uint16_t* base, int64_t ss, int64_t S, int nb,
-                                        int blk0, uint16_t* dst) {
+                                        int blk0, int brows, uint16_t* dst) {
   constexpr int KCH = D / 8;  // 16-byte chunks per row
   static_assert(kPoolBlocks * KCH <= 256, "one thread per (block, chunk)");
   const int t = threadIdx.x;
@@ -42,10 +44,10 @@ __device__ inline void pool_block_group(const uint16_t* base, int64_t ss, int64_
   double acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0;
-  const int64_t row0 = int64_t(blk) * kBlock;
-  const int rows = int(min(int64_t(kBlock), S - row0));  // rows past S pool as zeros
+  const int64_t row0 = int64_t(blk) * brows;
+  const int rows = int(min(int64_t(brows), S - row0));  // rows past S pool as zeros
   const uint16_t* p = base + row0 * ss + c * 8;
-  for (int r0 = 0; r0 < kBlock; r0 += 8) {
+  for (int r0 = 0; r0 < rows; r0 += 8) {
     u32x4 v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) v[u] = r0 + u < rows ? load16(p + (r0 + u) * ss) : zero_u32x4();
@@ -57,12 +59,14 @@ __device__ inline void pool_block_group(const uint16_t* base, int64_t ss, int64_
         acc[2 * e + 1] += double(T::to_float(uint16_t(v[u][e] >> 16)));
       }
   }
-  // mean in fp32 (sum / 64 is exact), then rounded to the input dtype
+  // mean in fp32 (sum / brows is exact: a power of two), then rounded to the
+  // input dtype
+  const float inv = 1.0f / float(brows);
   u32x4 out;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const uint32_t lo = T::from_float(float(acc[2 * e]) * (1.0f / 64.0f));
-    const uint32_t hi = T::from_float(float(acc[2 * e + 1]) * (1.0f / 64.0f));
+    const uint32_t lo = T::from_float(float(acc[2 * e]) * inv);
+    const uint32_t hi = T::from_float(float(acc[2 * e + 1]) * inv);
     out[e] = lo | (hi << 16);
   }
   store16(dst + int64_t(blk) * D + c * 8, out);
@@ -80,7 +84,7 @@ __device__ inline void pool_workgroup(const PoolParams& P, int g) {
     const int head = P.slot_heads[sb - b * P.n_slots];
     const uint16_t* base =
         reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + int64_t(head) * P.q_sh;
-    pool_block_group<T, D>(base, P.q_ss, P.s_q, P.n_qb, grp * kPoolBlocks,
+    pool_block_group<T, D>(base, P.q_ss, P.s_q, P.n_qb, grp * kPoolBlocks, P.pool_rows,
                            P.q_pool + int64_t(sb) * P.n_qb_pad * D);
     return;
   }
@@ -92,7 +96,7 @@ __device__ inline void pool_workgroup(const PoolParams& P, int g) {
   const int i = bi - b * P.n_kvp;
   const uint16_t* base =
       reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + int64_t(P.kvp_head[i]) * P.k_sh;
-  pool_block_group<T, D>(base, P.k_ss, P.s_k, P.n_kb, grp * kPoolBlocks,
+  pool_block_group<T, D>(base, P.k_ss, P.s_k, P.n_kb, grp * kPoolBlocks, P.pool_rows,
                          P.k_pool + (int64_t(b) * P.n_slots + i) * P.n_kb * D);
 }
 

@@ -357,11 +357,13 @@ def block_estimate(
     cnt: torch.Tensor,
     ws: Optional[torch.Tensor] = None,
     flags: int = 0,
+    block: int = MSA_BLOCK,
 ) -> None:
     """Launch msa_block_estimate on the current stream (no sync); with
     ``flags`` (MSA_SELECT_* / MSA_ESTIMATE_*) msa_block_estimate_ex.  The
     one-pass flags need the caller's workspace (the select pass reads what
-    the pooling pass left in it)."""
+    the pooling pass left in it).  ``block``: tokens per block (64, 128, 256
+    or 512); idx / cnt are in those blocks."""
     lib = load_library()
     n_slots = len(slot_heads)
     if len(slot_topk) != n_slots:
@@ -378,12 +380,12 @@ def block_estimate(
     stream = current_stream_handle(q.device)
     if flags:
         st = lib.msa_block_estimate_ex(
-            ctypes.byref(qd), ctypes.byref(kd), heads_arr, topk_arr, n_slots, MSA_BLOCK,
+            ctypes.byref(qd), ctypes.byref(kd), heads_arr, topk_arr, n_slots, int(block),
             int(topk_max), float(score_scale), int(flags), idx.data_ptr(), cnt.data_ptr(),
             ws.data_ptr(), ws.numel(), stream)
     else:
         st = lib.msa_block_estimate(
-            ctypes.byref(qd), ctypes.byref(kd), heads_arr, topk_arr, n_slots, MSA_BLOCK,
+            ctypes.byref(qd), ctypes.byref(kd), heads_arr, topk_arr, n_slots, int(block),
             int(topk_max), float(score_scale), idx.data_ptr(), cnt.data_ptr(), ws.data_ptr(),
             ws.numel(), stream)
     check(st)

@@ -30,10 +30,16 @@ __all__ = [
 _DEFAULT_BLOCK_SIZE = 64
 
 
+# Block sizes of the selector and the token mask: the attention kernels walk
+# 64-token tiles, so a block of 64 m tokens is m consecutive tiles; the
+# pooling divides by the block size exactly, as a power of two.
+BLOCK_SIZES = (64, 128, 256, 512)
+
+
 def _check_block_size(block_size: int) -> None:
-    if int(block_size) != _abi.MSA_BLOCK:
+    if int(block_size) not in BLOCK_SIZES:
         raise NotImplementedError(
-            f"block_size={block_size}: the MI355X kernels use 64-token blocks only"
+            f"block_size={block_size}: the MI355X kernels take block sizes {BLOCK_SIZES}"
         )
 
 
@@ -45,15 +51,17 @@ def select_flags(force_first: bool = False, force_diag: bool = False) -> int:
             | (_abi.MSA_SELECT_FORCE_DIAG if force_diag else 0))
 
 
-def _estimate(q: torch.Tensor, k: torch.Tensor, topk: int, scale: float, flags: int = 0):
+def _estimate(q: torch.Tensor, k: torch.Tensor, topk: int, scale: float, flags: int = 0,
+              block: int = _DEFAULT_BLOCK_SIZE):
     """Run the estimator for every head of q (kernel views at the kernel
-    head dim; ``scale`` from the original head_dim).
+    head dim; ``scale`` from the original head_dim) with blocks of ``block``
+    tokens.
 
     Returns a list of (h0, h1, idx, cnt) per head chunk of at most
     MSA_MAX_HEADS heads, idx/cnt int32 contiguous [B, h1-h0, n_qb(, topk)].
     """
     B, H, S_q, _ = q.shape
-    n_qb = math.ceil(S_q / _abi.MSA_BLOCK)
+    n_qb = math.ceil(S_q / block)
     chunks = []
     for h0, h1 in head_chunks(H):
         n = h1 - h0
@@ -61,7 +69,7 @@ def _estimate(q: torch.Tensor, k: torch.Tensor, topk: int, scale: float, flags: 
         cnt = torch.empty((B, n, n_qb), dtype=torch.int32, device=q.device)
         _abi.block_estimate(
             q[:, h0:h1], k[:, h0:h1], list(range(n)), [topk] * n, topk, scale, idx, cnt,
-            flags=flags,
+            flags=flags, block=block,
         )
         chunks.append((h0, h1, idx, cnt))
     return chunks
@@ -98,9 +106,10 @@ def select_block_sparse_topk_indices(
     scale = sparse_scale(q.shape[-1])
     dk = kernel_head_dim(q.shape[-1])
     q, k = kernel_view(pad_head_dim(q, dk)), kernel_view(pad_head_dim(k, dk))
-    n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
+    bs = int(block_size)
+    n_kb = math.ceil(k.shape[2] / bs)
     topk = min(max(1, int(topk_blocks)), n_kb)
-    chunks = _estimate(q, k, topk, scale, select_flags(force_first, force_diag))
+    chunks = _estimate(q, k, topk, scale, select_flags(force_first, force_diag), bs)
     idx = torch.cat([c[2] for c in chunks], dim=1).long()
     if return_counts:
         return idx, torch.cat([c[3] for c in chunks], dim=1).long()
@@ -129,20 +138,37 @@ def block_sparse_attention_with_indices(
     check_supported(q, k, v)
     _check_block_size(block_size)
     B, H, S_q, _ = q.shape
-    n_qb = math.ceil(S_q / _abi.MSA_BLOCK)
-    if tuple(block_indices.shape[:3]) != (B, H, n_qb):
+    bs = int(block_size)
+    if tuple(block_indices.shape[:3]) != (B, H, math.ceil(S_q / bs)):
         raise ValueError(
             "block_indices shape must be [B,H,n_q_blocks,topk_blocks]; "
             f"got {tuple(block_indices.shape)} for q={tuple(q.shape)} block_size={block_size}"
         )
+    ids = block_indices.to(q.device)
+    if bs != _abi.MSA_BLOCK:
+        ids = tile_ids(ids, bs, math.ceil(S_q / _abi.MSA_BLOCK))
     n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
-    idx, cnt = canonical_block_lists(block_indices.to(q.device), n_kb)
+    idx, cnt = canonical_block_lists(ids, n_kb)
     topk = idx.shape[-1]
     chunks = []
     for h0, h1 in head_chunks(H):
         chunks.append((h0, h1, idx[:, h0:h1].contiguous(), cnt[:, h0:h1].contiguous()))
     scale = sparse_scale(q.shape[-1])
     return padded_call(q, k, v, out, lambda q, k, v, r: _run(q, k, v, chunks, topk, scale, r))
+
+
+def tile_ids(block_indices: torch.Tensor, block_size: int, n_qb: int) -> torch.Tensor:
+    """Ids of ``block_size``-token blocks [B, H, n_q_blocks, topk] as ids of
+    the kernels' 64-token tiles [B, H, n_qb, topk * m] (m = block_size / 64):
+    block J is tiles m J .. m J + m - 1, and 64-row query block bq takes the
+    list of its block bq // m.  The token visibility is unchanged: a key is
+    in a selected block iff its tile is among that block's tiles.  Ids
+    outside the key range stay outside it (negative ones stay negative)."""
+    m = int(block_size) // _abi.MSA_BLOCK
+    ids = block_indices.long()
+    tiles = (ids.unsqueeze(-1) * m + torch.arange(m, device=ids.device)).flatten(-2)
+    rows = torch.arange(n_qb, device=ids.device) // m
+    return tiles[:, :, rows]
 
 
 def canonical_block_lists(block_indices: torch.Tensor, n_kb: int):
@@ -194,7 +220,8 @@ def block_sparse_attention(
         q, k, v:     ``[B, H, S, D]`` (BNSD), RoPE applied, ``repeat_kv``-ed.
         topk_blocks: K blocks kept per query block (clamped to >= 1 and to the
                      number of K blocks, as in the reference).
-        block_size:  must be 64.
+        block_size:  64, 128, 256 or 512 tokens (the attention kernels walk
+                     64-token tiles; a larger block is its consecutive tiles).
         out:         optional output (q's dtype or float32).
         force_first, force_diag: keep block 0 / the diagonal block in every
                      selection (options of this build, off by default: the
@@ -205,6 +232,10 @@ def block_sparse_attention(
     check_bnsd(q, k, v)
     check_supported(q, k, v)
     _check_block_size(block_size)
+    if int(block_size) != _abi.MSA_BLOCK:
+        ids = select_block_sparse_topk_indices(q, k, topk_blocks, block_size,
+                                               force_first=force_first, force_diag=force_diag)
+        return block_sparse_attention_with_indices(q, k, v, ids, block_size, out=out)
     n_kb = math.ceil(k.shape[2] / _abi.MSA_BLOCK)
     topk = min(max(1, int(topk_blocks)), n_kb)
     scale = sparse_scale(q.shape[-1])

@@ -587,10 +587,11 @@ def streaming_attention(q, k, v, n_init: int, n_local: int, scale: float | None 
 
 
 def block_sparse_from_indices(q, k, v, idx, scale: float | None = None,
-                              acc=np.float64) -> np.ndarray:
-    """Block-sparse attention for fixed block ids idx [B, H, n_bq, topk]
-    (reference tests/test_block_sparse_kernel.py:96-119 semantics; the ids
-    are expanded to tokens and intersected with the token causal mask)."""
+                              acc=np.float64, block: int = BLOCK) -> np.ndarray:
+    """Block-sparse attention for fixed ids idx [B, H, n_bq, topk] of
+    ``block``-token blocks (reference tests/test_block_sparse_kernel.py:96-119
+    semantics; the ids are expanded to tokens and intersected with the token
+    causal mask)."""
     if scale is None:
         scale = sparse_scale(q.shape[-1])
     B, H, s_q, D = q.shape
@@ -598,7 +599,7 @@ def block_sparse_from_indices(q, k, v, idx, scale: float | None = None,
     kvg = H // k.shape[1]
     out = np.zeros((B, H, s_q, D), dtype=acc)
     for b, h in _heads(q):
-        vis = block_token_visible(np.asarray(idx[b, h]), s_q, s_k)
+        vis = block_token_visible(np.asarray(idx[b, h]), s_q, s_k, block)
         out[b, h] = masked_attention(q[b, h], k[b, h // kvg], v[b, h // kvg], vis, scale, acc)
     return out
 

@@ -21,17 +21,20 @@ def test_streaming_reference_matches_oracle(S, n_init, n_local, D):
     assert np.abs(got - ref).max() < 1e-5
 
 
-@pytest.mark.parametrize("S,topk,D", [(1000, 4, 96), (640, 100, 64)])
-def test_block_reference_matches_oracle(S, topk, D):
+@pytest.mark.parametrize("S,topk,D,block", [(1000, 4, 96, 64), (640, 100, 64, 64),
+                                             (1000, 3, 96, 128), (1100, 2, 96, 256),
+                                             (1500, 2, 64, 512)])
+def test_block_reference_matches_oracle(S, topk, D, block):
     q, k, v = make_qkv(1, 2, S, S, D, torch.bfloat16, seed=7, sink_scale=8.0)
-    ids = R.select_blocks(R._padded(q), R._padded(k), topk).numpy()
-    ridx, rcnt = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, "bf16")
+    ids = R.select_blocks(R._padded(q), R._padded(k), topk, block).numpy()
+    ridx, rcnt = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, "bf16", block=block)
+    assert np.array_equal(rcnt[0], O.attend_count(ridx, S, S, block)[0])
     for h in range(2):
         for bq in range(ridx.shape[2]):
             c = rcnt[0, h, bq]
             assert set(ridx[0, h, bq, :c]) == set(x for x in ids[0, h, bq] if x <= bq)
-    got = R.block_sparse_reference(q.float(), k.float(), v.float(), topk).numpy()
+    got = R.block_sparse_reference(q.float(), k.float(), v.float(), topk, block).numpy()
     # the fp32 inputs pool in fp32: select on the same values for the oracle
-    ridx32, _ = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, "fp32")
-    ref = O.block_sparse_from_indices(np32(q), np32(k), np32(v), ridx32)
+    ridx32, _ = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, "fp32", block=block)
+    ref = O.block_sparse_from_indices(np32(q), np32(k), np32(v), ridx32, block=block)
     assert np.abs(got - ref).max() < 1e-5

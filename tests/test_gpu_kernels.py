@@ -231,6 +231,66 @@ def test_block_fixed_indices_with_future_and_duplicates(gpu_device):
     assert_close_f32(out32, ref, what="fixed indices")
 
 
+LARGE_BLOCK_CASES = [
+    # (block, B, H, S_q, S_k, D, topk, dtype, sink, force_first, force_diag)
+    (128, 1, 3, 1000, 1000, 96, 3, torch.bfloat16, 8.0, False, False),
+    (256, 2, 2, 2048 + 17, 2048 + 17, 96, 4, torch.float16, None, False, False),
+    (512, 1, 2, 4096, 4096, 128, 2, torch.bfloat16, 8.0, False, False),
+    (128, 1, 2, 300, 1100, 96, 3, torch.bfloat16, None, False, False),    # chunk
+    (256, 1, 2, 500, 2000, 64, 100, torch.bfloat16, None, False, False),  # top-k clamped
+    (128, 1, 2, 1000, 1000, 96, 2, torch.bfloat16, 8.0, True, True),
+]
+
+
+@pytest.mark.parametrize("case", LARGE_BLOCK_CASES,
+                         ids=[str(c[:7]) + dtype_tag(c[7]) + ("-forced" if c[9] else "")
+                              for c in LARGE_BLOCK_CASES])
+def test_block_sizes_above_64(gpu_device, case):
+    """Selector ids and counts bit-exact at 128/256/512-token blocks, and the
+    attention over those blocks within the bars of the 64-token path."""
+    from minference import block_sparse_attention
+    from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
+
+    block, B, H, S_q, S_k, D, topk, dtype, sink, first, diag = case
+    q, k, v = make_qkv(B, H, S_q, S_k, D, dtype, seed=block + S_q, sink_scale=sink)
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    idx, cnt = select_block_sparse_topk_indices(dq, dk, topk, block, return_counts=True,
+                                                force_first=first, force_diag=diag)
+    ridx, rcnt = O.select_block_sparse_topk_indices(np32(q), np32(k), topk, dtype_tag(dtype),
+                                                    block=block, force_first=first,
+                                                    force_diag=diag)
+    got_i, got_c = idx.cpu().numpy(), cnt.cpu().numpy()
+    assert got_i.shape == ridx.shape
+    assert np.array_equal(got_i, ridx), f"{(got_i != ridx).sum()} ids differ"
+    assert np.array_equal(got_c, O.attend_count(ridx, S_q, S_k, block))
+    ref = O.block_sparse_from_indices(np32(q), np32(k), np32(v), ridx, block=block)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    block_sparse_attention(dq, dk, dv, topk, block, out=out32, force_first=first,
+                           force_diag=diag)
+    assert_close_f32(out32, ref, what=f"block {block} {case[1:7]}")
+    out = block_sparse_attention(dq, dk, dv, topk, block, force_first=first, force_diag=diag)
+    assert out.dtype == dtype
+    assert_close_lowp(out, ref, what=f"block {block} lowp {case[1:7]}")
+
+
+@pytest.mark.parametrize("block,s_q,s_k", [(128, 1000, 1000), (256, 300, 1300), (512, 1100, 1100)])
+def test_block_fixed_indices_large_blocks(gpu_device, block, s_q, s_k):
+    """Fixed ids of 128/256/512-token blocks: out of range, negative, future
+    and repeated ids; chunked rows (S_q < S_k)."""
+    from minference.ops.block_sparse_kernel import block_sparse_attention_with_indices
+
+    B, H, D, topk = 1, 3, 96, 4
+    q, k, v = make_qkv(B, H, s_q, s_k, D, torch.bfloat16, seed=block + s_k)
+    n_bq, n_bk = -(-s_q // block), -(-s_k // block)
+    g = np.random.default_rng(block)
+    idx = g.integers(-2, n_bk + 2, size=(B, H, n_bq, topk))
+    dq, dk, dv = to_dev(gpu_device, q, k, v)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=gpu_device)
+    block_sparse_attention_with_indices(dq, dk, dv, torch.from_numpy(idx), block, out=out32)
+    ref = O.block_sparse_from_indices(np32(q), np32(k), np32(v), idx, block=block)
+    assert_close_f32(out32, ref, what=f"fixed indices block {block}")
+
+
 # ---------------------------------------------------------------------------
 # dense
 # ---------------------------------------------------------------------------

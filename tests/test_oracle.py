@@ -57,6 +57,18 @@ def test_pool_matches_torch_mean(dtype, S):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("block,S", [(128, 300), (256, 1000), (512, 1100)])
+def test_pool_matches_torch_mean_large_blocks(dtype, block, S):
+    q, _, _ = make_qkv(B=1, H=2, S_q=S, D=96, dtype=dtype, seed=S + block)
+    pad = (-S) % block
+    qp = F.pad(q, (0, 0, 0, pad)) if pad else q
+    ref = qp.reshape(1, 2, -1, block, 96).mean(dim=3).to(torch.float32).numpy()
+    got = O.pool_blocks(np32(q), dtype_tag(dtype), block)
+    assert got.shape == ref.shape
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 # ---------------------------------------------------------------------------
 # selector: brute force, known answers, invariants, torch.topk
 # ---------------------------------------------------------------------------

@@ -76,3 +76,32 @@ def test_block_layer_schedule(monkeypatch):
     assert [m[0] for m in marks] == ["start", "stage0", "stage1", "est0", "est1", "attn0",
                                      "attn0_end"]
     assert {st for _, st in marks} == {"main"}
+
+
+def test_tile_ids_keep_token_visibility():
+    """Ids of 128/256/512-token blocks expanded to 64-token tiles select the
+    same (query, key) pairs: chunked and ragged shapes, ids out of range,
+    negative and repeated."""
+    import numpy as np
+
+    import oracle as O
+    from minference.ops.block_sparse_kernel import canonical_block_lists, tile_ids
+
+    g = np.random.default_rng(3)
+    for block, s_q, s_k in [(128, 300, 300), (256, 1000, 1000), (512, 700, 1500),
+                            (128, 100, 900), (256, 64, 64)]:
+        n_bq, n_bk = -(-s_q // block), -(-s_k // block)
+        ids = g.integers(-2, n_bk + 2, size=(1, 2, n_bq, 4))
+        n_qt, n_kt = -(-s_q // 64), -(-s_k // 64)
+        tiles = tile_ids(torch.from_numpy(ids), block, n_qt)
+        assert tiles.shape == (1, 2, n_qt, 4 * block // 64)
+        lists, cnt = canonical_block_lists(tiles, n_kt)
+        for h in range(2):
+            want = O.block_token_visible(ids[0, h], s_q, s_k, block)
+            got = O.block_token_visible(tiles[0, h].numpy(), s_q, s_k, 64)
+            assert np.array_equal(got, want)
+            # the canonical lists: the distinct in-range tiles, ascending
+            for t in range(n_qt):
+                c = int(cnt[0, h, t])
+                row = tiles[0, h, t].numpy()
+                assert lists[0, h, t, :c].tolist() == sorted(set(row[(row >= 0) & (row < n_kt)]))
