@@ -26,7 +26,9 @@ int elem_size(int dtype) {
   }
 }
 
-bool head_dim_ok(int64_t d) { return d == 64 || d == 96 || d == 128; }
+bool head_dim_ok(int64_t d) { return d == 64 || d == 96 || d == 128 || d == 256; }
+// vertical_and_slash estimator and attention: up to 128
+bool vs_head_dim_ok(int64_t d) { return d == 64 || d == 96 || d == 128; }
 
 // D contiguous, every row and the base 16-byte aligned, row stride below
 // 2^24 elements (the attention kernel addresses a query block's 64 rows
@@ -75,7 +77,7 @@ const char* msa_status_str(int status) {
     case MSA_E_NULL: return "a required pointer is NULL";
     case MSA_E_RANK: return "shape mismatch between q, k, v and o";
     case MSA_E_DTYPE: return "unsupported or mismatched dtype (q/k/v must be bf16 or fp16; o same or fp32)";
-    case MSA_E_HEAD_DIM: return "head_dim must be 64, 96 or 128";
+    case MSA_E_HEAD_DIM: return "head_dim must be 64, 96, 128 or 256 (vertical_and_slash: 64, 96 or 128)";
     case MSA_E_ALIGN: return "head_dim stride must be 1, rows 16-byte aligned and the row stride below 2^24";
     case MSA_E_BLOCK: return "block size must be 64, 128, 256 or 512";
     case MSA_E_TOPK: return "topk must be in [1, n_kv_blocks]";
@@ -148,6 +150,7 @@ int pool_setup(const msa_tensor4* q, const msa_tensor4* k, const int32_t* slot_h
   pp.n_kb = L.n_kb;
   pp.n_qb_pad = L.n_qb_pad;
   pp.pool_rows = block;
+  pp.pool_blocks = pool_blocks_for(D);
   pp.batch = int(q->size[0]);
   pp.n_slots = n_slots;
   pp.kv_group = int(q->size[1] / k->size[1]);
@@ -436,6 +439,7 @@ int msa_vs_estimate(const msa_tensor4* q, const msa_tensor4* k, const int32_t* s
                     msa_stream_t stream) {
   int st = check_qk(q, k);
   if (st != MSA_OK) return st;
+  if (!vs_head_dim_ok(q->size[3])) return MSA_E_HEAD_DIM;
   if (!slot_heads || !slot_vsize || !slot_ssize || !v_idx || !v_cnt || !s_idx || !s_cnt)
     return MSA_E_NULL;
   const int64_t B = q->size[0], H = q->size[1], S = q->size[2];
@@ -619,6 +623,7 @@ static int layer_attention_impl(const msa_tensor4* q, const msa_tensor4* k, cons
   VsLayout vl;
   int16_t slot_kvh[kMaxHeads];
   if (n_vs) {
+    if (!vs_head_dim_ok(D)) return MSA_E_HEAD_DIM;
     if (!vs || !vs->v_idx || !vs->v_cnt || !vs->s_idx || !vs->s_cnt) return MSA_E_SLOTS;
     if (vs->n_slots < 1 || vs->n_slots > kMaxHeads || vs->v_stride < 1 ||
         vs->v_stride > kVsMaxSeq || vs->s_stride < 1)

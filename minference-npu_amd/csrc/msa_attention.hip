@@ -276,10 +276,12 @@ hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st) 
   if (dtype == Bf16::id) {
     if (D == 64) return launch_stage_t<Bf16, 64>(p, st);
     if (D == 96) return launch_stage_t<Bf16, 96>(p, st);
+    if (D == 256) return launch_stage_t<Bf16, 256>(p, st);
     return launch_stage_t<Bf16, 128>(p, st);
   }
   if (D == 64) return launch_stage_t<F16, 64>(p, st);
   if (D == 96) return launch_stage_t<F16, 96>(p, st);
+  if (D == 256) return launch_stage_t<F16, 256>(p, st);
   return launch_stage_t<F16, 128>(p, st);
 }
 
@@ -287,10 +289,12 @@ hipError_t launch_vscale(const StageParams& p, int dtype, int D, hipStream_t st)
   if (dtype == Bf16::id) {
     if (D == 64) return launch_vscale_t<Bf16, 64>(p, st);
     if (D == 96) return launch_vscale_t<Bf16, 96>(p, st);
+    if (D == 256) return launch_vscale_t<Bf16, 256>(p, st);
     return launch_vscale_t<Bf16, 128>(p, st);
   }
   if (D == 64) return launch_vscale_t<F16, 64>(p, st);
   if (D == 96) return launch_vscale_t<F16, 96>(p, st);
+  if (D == 256) return launch_vscale_t<F16, 256>(p, st);
   return launch_vscale_t<F16, 128>(p, st);
 }
 
@@ -1031,6 +1035,248 @@ void attn_kernel(AttnParams P) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Head dim 256 (the ops zero-pad head dims 129..255 to it).  The same work
+// items and tile walk as attn_kernel; the O of 64 rows x 256 dims does not
+// fit one wave, so wave w owns the 16 query rows 16w .. 16w+15 and walks
+// every key of the item's tiles itself (no merge).  Each 32-key span of a
+// tile gives two 16x16x32 QK accumulators whose rows are the keys
+//   A: 8 (r / 4) + (r % 4),   B: 8 (r / 4) + 4 + (r % 4)   (r = accumulator row)
+// (the K operand rows are read in that order), so lane l holds keys
+// 8 (l / 16) .. +7 of its query row l % 16: rounded to fp16 they are the B
+// operand of the 16x16x32 PV product as they stand.  V comes from the staged
+// 32x32x16 operand layout, one 16-byte granule per lane.  The row max is
+// exact per tile (O rescaled when it grows), P biased to 2^kPBias like
+// attn_kernel; fully masked rows give 0.
+template <typename T, bool OUT_F32>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void attn_wide_kernel(AttnParams P) {
+  constexpr int D = 256;
+  constexpr int NKS = D / 32;  // QK k-steps
+  constexpr int NDO = D / 16;  // PV output blocks of 16 dims
+  constexpr int NDB = D / 32;  // staged V blocks of 32 dims per 16-key chunk
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int lr = lane >> 4;
+  const int lc = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int xcd = blockIdx.x & 7;
+  int hh, bq;
+  if (P.n_hl) {
+    const int r = int(blockIdx.x) >> 3;
+    if (r >= P.xcd_count[xcd]) return;
+    const int g = P.xcd_start[xcd] + r;
+    const int hl = g / P.n_qb;
+    hh = int(P.head_order[hl]);
+    bq = P.n_qb - 1 - (g - hl * P.n_qb);
+  } else {
+    const int BH = P.batch * P.heads;
+    hh = int(blockIdx.x) % BH;
+    if (P.hd[hh % P.heads].kind == KIND_SKIP) return;
+    bq = P.n_qb - 1 - int(blockIdx.x) / BH;
+  }
+  const int b = hh / P.heads;
+  const int h = hh - b * P.heads;
+  const int kvh = h / P.kv_group;
+  const int kind = P.hd[h].kind;
+  const int q0 = bq * kBlock;
+  const int nrows = min(kBlock, P.s_q - q0);
+  const int a0 = q0 + P.s_k - P.s_q;
+  const int a1 = a0 + nrows - 1;
+  const int last_tile = min(a1 >> 6, P.n_kb - 1);
+  const int n_init = P.hd[h].p1;
+  const int n_local = P.hd[h].p2;
+  const int Fe = min(min((a0 + 1) >> 6, P.s_k >> 6), last_tile + 1);
+  TileSeq seq;
+  seq.n_kb = P.n_kb;
+  seq.list = nullptr;
+  seq.any = reinterpret_cast<const int32_t*>(P.q);
+  if (kind == KIND_BLOCK) {
+    const int64_t base = (int64_t(b) * P.idx_slots + P.hd[h].slot) * P.n_qb + bq;
+    const int cnt = max(0, min(load_uniform(P.cnt + base), P.topk_max));
+    seq.list = P.idx + base * P.topk_max;
+    seq.set({0, 0, 0, 0, 0}, {cnt, 0, 0, 0, 0}, 1);
+  } else if (kind == KIND_STREAM) {
+    const int lo = min(max(a0 - n_local + 1, 0) >> 6, last_tile + 1);
+    const int nsink = min((min(max(n_init, 0), P.s_k) + 63) >> 6, lo);
+    seq.set({0, lo, 0, 0, 0}, {nsink, last_tile + 1, 0, 0, 0}, 1);
+  } else if (kind == KIND_FULL) {
+    seq.set({0, 0, 0, 0, 0}, {P.n_kb, 0, 0, 0, 0}, 1);
+  } else {
+    seq.set({0, 0, 0, 0, 0}, {last_tile + 1, 0, 0, 0, 0}, 1);
+  }
+  const int total = seq.total;
+  (void)Fe;
+
+  const int64_t bk = int64_t(b) * (P.heads / P.kv_group) + kvh;
+  const float vfac = __builtin_amdgcn_ldexpf(1.0f, load_uniform(P.vexp + bk));
+  const bool kin = P.k_in_place != 0;
+  const __amdgpu_buffer_rsrc_t krs =
+      kin ? __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb +
+                                      int64_t(kvh) * P.k_sh),
+                short(0), int(((P.s_k - 1) * P.k_ss + D) * 2), 0x00020000)
+          : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.kt + bk * P.s_pad * D),
+                                              short(0), P.s_pad * D * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.vt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb +
+                            int64_t(h) * P.q_sh + int64_t(q0) * P.q_ss),
+      short(0), int(((nrows - 1) * P.q_ss + D) * 2), 0x00020000);
+
+  // Q rows 16w + lc as the QK B operand (rows past S_q read zeros or rows of
+  // the view; their outputs are not stored)
+  u32x4 qb[NKS];
+  {
+    const uint32_t roff = uint32_t((16 * w + lc) * P.q_ss * 2 + 16 * lr);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+      qb[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qrs, roff, 64 * ks, 0));
+  }
+  const float c_log2 = P.hd[h].scale_log2;
+  const int ar = a0 + 16 * w + lc;  // absolute position of this lane's row
+  const bool is_full = kind == KIND_FULL, is_stream = kind == KIND_STREAM;
+  const int key_hi = is_full ? P.s_k - 1 : min(ar, P.s_k - 1);
+  const int band_lo = is_stream ? ar - n_local + 1 : 0;
+  const int sink_hi = is_stream ? n_init : 0;
+
+  f32x4 o[NDO];
+#pragma unroll
+  for (int db = 0; db < NDO; ++db) o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -1e30f;  // running (biased) max of the row in scaled log2 units
+  float l = 0.0f;    // this lane's share of the row sum
+
+  // K operand rows of virtual chunk (span kh, half ab) of tile t: lane row lc
+  // reads key 64t + 32kh + 8 (lc / 4) + 4 ab + lc % 4, elements 32 ks + 8 lr
+  auto load_k = [&](int t, int kh, int ab, u32x4 (&kr)[NKS]) INLINE {
+    const int key = 64 * t + 32 * kh + 8 * (lc >> 2) + 4 * ab + (lc & 3);
+    if (kin) {
+      const uint32_t vo = uint32_t(key) * uint32_t(P.k_ss) * 2u + 16u * lr;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        kr[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo, 64 * ks, 0));
+    } else {
+      // staged: chunk key / 16, k-step ks, lane (key % 16) + 16 lr
+      const uint32_t vo = uint32_t(((key >> 4) * NKS) * 1024 + ((key & 15) + 16 * lr) * 16);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        kr[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo, 1024 * ks, 0));
+    }
+  };
+  // V^T operand (dims 16 db + lc, keys 32 kh + 8 lr .. +7 of tile t) from the
+  // staged layout: chunk 4t + 2kh + lr / 2, block db / 2, lane 32 (lr % 2) +
+  // 16 (db % 2) + lc
+  auto load_v = [&](int t, int kh, u32x4 (&vr)[NDO]) INLINE {
+    const int c = 4 * t + 2 * kh + (lr >> 1);
+#pragma unroll
+    for (int db = 0; db < NDO; ++db) {
+      const uint32_t vo =
+          uint32_t(((c * NDB + (db >> 1)) * 64 + 32 * (lr & 1) + 16 * (db & 1) + lc) * 16);
+      vr[db] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vo, 0, 0));
+    }
+  };
+
+  for (int p = 0; p < total; ++p) {
+    const int t = seq.template finish<false>(seq.fetch(p));
+    // scores of the tile: s[kh][ab] (lane: keys 8 lr + 4 ab + i of span kh)
+    f32x4 s[2][2];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int ab = 0; ab < 2; ++ab) {
+        u32x4 kr[NKS];
+        load_k(t, kh, ab, kr);
+        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) acc = mfma_qk<T>(kr[ks], qb[ks], acc);
+        s[kh][ab] = acc;
+      }
+    // visibility (every tile: the walk has no separate unmasked part here)
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int ab = 0; ab < 2; ++ab)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = 64 * t + 32 * kh + 8 * lr + 4 * ab + i;
+          const bool vis = (j <= key_hi) & ((j >= band_lo) | (j < sink_hi));
+          const float x = vis ? s[kh][ab][i] : -__builtin_inff();
+          s[kh][ab][i] = x;
+          mx = fmaxf(mx, x);
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx * c_log2 - kPBias);
+    if (__ballot(mn != m) != 0) {
+      const float al = __builtin_amdgcn_exp2f(m - mn);
+      l *= al;
+#pragma unroll
+      for (int db = 0; db < NDO; ++db) o[db] *= al;
+      m = mn;
+    }
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      u32x4 vr[NDO];
+      load_v(t, kh, vr);
+      float pv[2][4];
+#pragma unroll
+      for (int ab = 0; ab < 2; ++ab)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pv[ab][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][ab][i], c_log2, -m));
+          l += pv[ab][i];
+        }
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      typedef float f2 __attribute__((ext_vector_type(2)));
+      const u32x4 pb = u32x4{
+          __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{pv[0][0], pv[0][1]}, h2)),
+          __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{pv[0][2], pv[0][3]}, h2)),
+          __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{pv[1][0], pv[1][1]}, h2)),
+          __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{pv[1][2], pv[1][3]}, h2))};
+#pragma unroll
+      for (int db = 0; db < NDO; ++db)
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, vr[db]),
+                                                       __builtin_bit_cast(f16x8, pb), o[db], 0,
+                                                       0, 0);
+    }
+  }
+  // row sum over the row's four lanes; O^T block db: lane l holds dims
+  // 16 db + 4 lr .. +3 of row lc
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  const float inv = l > 0.0f ? vfac / l : 0.0f;
+  const int row = q0 + 16 * w + lc;
+  if (row < P.s_q) {
+    const int64_t obase = b * P.o_sb + int64_t(h) * P.o_sh + int64_t(row) * P.o_ss;
+#pragma unroll
+    for (int db = 0; db < NDO; ++db) {
+      const int d = 16 * db + 4 * lr;
+      if constexpr (OUT_F32) {
+        store_out4<float>(reinterpret_cast<float*>(P.o) + obase + d, o[db][0] * inv,
+                          o[db][1] * inv, o[db][2] * inv, o[db][3] * inv);
+      } else {
+        store_out4_16<T>(reinterpret_cast<uint16_t*>(P.o) + obase + d, o[db][0] * inv,
+                         o[db][1] * inv, o[db][2] * inv, o[db][3] * inv);
+      }
+    }
+  }
+}
+
+template <typename T, bool OUT_F32>
+static hipError_t launch_wide_t(const AttnParams& p, hipStream_t st) {
+  int64_t items = int64_t(p.n_qb) * p.batch * p.heads;
+  if (p.n_hl) {
+    int longest = 0;
+    for (int x = 0; x < 8; ++x) longest = p.xcd_count[x] > longest ? p.xcd_count[x] : longest;
+    items = 8 * int64_t(longest);
+  }
+  if (items == 0) return hipSuccess;
+  hipLaunchKernelGGL((attn_wide_kernel<T, OUT_F32>), dim3(uint32_t(items)), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
 template <typename T, bool OUT_F32, int D, bool VS>
 static hipError_t launch_attn_t(const AttnParams& p, hipStream_t st) {
   int64_t items = int64_t(p.n_qb) * p.batch * p.heads;
@@ -1056,6 +1302,7 @@ static hipError_t launch_attn_t(const AttnParams& p, hipStream_t st) {
 
 template <typename T, bool OUT_F32, bool VS>
 static hipError_t launch_attn_d(const AttnParams& p, int D, hipStream_t st) {
+  if (D == 256) return VS ? hipErrorInvalidValue : launch_wide_t<T, OUT_F32>(p, st);
   if (D == 64) return launch_attn_t<T, OUT_F32, 64, VS>(p, st);
   if (D == 96) return launch_attn_t<T, OUT_F32, 96, VS>(p, st);
   return launch_attn_t<T, OUT_F32, 128, VS>(p, st);

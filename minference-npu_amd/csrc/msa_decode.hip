@@ -305,6 +305,7 @@ template <typename T, bool OUT_F32>
 static hipError_t launch_decode_d(const DecodeParams& p, int D, hipStream_t st) {
   if (D == 64) return launch_decode_t<T, OUT_F32, 64>(p, st);
   if (D == 96) return launch_decode_t<T, OUT_F32, 96>(p, st);
+  if (D == 256) return launch_decode_t<T, OUT_F32, 256>(p, st);
   return launch_decode_t<T, OUT_F32, 128>(p, st);
 }
 

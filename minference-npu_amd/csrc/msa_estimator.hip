@@ -349,7 +349,7 @@ __device__ inline void finish_exact(uint32_t* rk, int n, int topk, float scale,
 // finish_fast (or finish_exact) and an ordered compaction.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int KPL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KPL > 16 ? 1 : 4)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KPL > 16 || D > 128 ? 1 : 4)))
 void score_topk_kernel(ScoreParams P) {
   constexpr int NKS = D / 32;  // k-steps of the 16x16x32 MFMA
   constexpr uint32_t kAbs = 0x7fff7fffu;
@@ -679,10 +679,12 @@ hipError_t launch_pool(const PoolParams& p, int dtype, int D, hipStream_t st) {
   if (dtype == Bf16::id) {
     if (D == 64) return launch_pool_t<Bf16, 64>(p, st);
     if (D == 96) return launch_pool_t<Bf16, 96>(p, st);
+    if (D == 256) return launch_pool_t<Bf16, 256>(p, st);
     return launch_pool_t<Bf16, 128>(p, st);
   }
   if (D == 64) return launch_pool_t<F16, 64>(p, st);
   if (D == 96) return launch_pool_t<F16, 96>(p, st);
+  if (D == 256) return launch_pool_t<F16, 256>(p, st);
   return launch_pool_t<F16, 128>(p, st);
 }
 
@@ -711,10 +713,12 @@ hipError_t launch_score(const ScoreParams& p, int dtype, int D, hipStream_t st) 
   if (dtype == Bf16::id) {
     if (D == 64) return launch_score_d<Bf16, 64>(p, st);
     if (D == 96) return launch_score_d<Bf16, 96>(p, st);
+    if (D == 256) return launch_score_d<Bf16, 256>(p, st);
     return launch_score_d<Bf16, 128>(p, st);
   }
   if (D == 64) return launch_score_d<F16, 64>(p, st);
   if (D == 96) return launch_score_d<F16, 96>(p, st);
+  if (D == 256) return launch_score_d<F16, 256>(p, st);
   return launch_score_d<F16, 128>(p, st);
 }
 

@@ -13,6 +13,10 @@ namespace msa {
 //   q_pool [batch*n_slots][n_qb_pad][D]  (rows n_qb .. n_qb_pad-1 unused)
 //   k_pool [batch*n_slots][n_kb][D]      (entry b * n_slots + i: the i-th
 //                                         distinct kv head of the slots)
+// Blocks per pooling workgroup: one thread per (block, 16-byte chunk of a
+// row), 16 blocks up to D = 128, 8 at D = 256.
+__host__ __device__ constexpr int pool_blocks_for(int D) { return D > 128 ? 8 : 16; }
+
 struct PoolParams {
   const void* q;
   const void* k;
@@ -21,6 +25,7 @@ struct PoolParams {
   int64_t s_q, s_k;
   int n_qb, n_kb, n_qb_pad;  // n_qb_pad: n_qb rounded up to kScoreRowPad
   int pool_rows;             // rows per pooled block: 64, 128, 256 or 512
+  int pool_blocks;           // blocks per pooling workgroup: pool_blocks_for(D)
   int batch, n_slots, kv_group;
   int n_kvp;                 // distinct kv heads of the slots
   uint16_t* q_pool;

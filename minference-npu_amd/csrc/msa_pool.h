@@ -15,32 +15,31 @@
 
 namespace msa {
 
-// Blocks per pooling workgroup.
-constexpr int kPoolBlocks = 16;
-
-__host__ __device__ inline int pool_groups(int nb) { return (nb + kPoolBlocks - 1) / kPoolBlocks; }
+__host__ __device__ inline int pool_groups(int nb, int per_wg) { return (nb + per_wg - 1) / per_wg; }
 
 // Workgroup g of the pass: the Q groups of every (batch, slot), then the K
 // groups of every (batch, distinct kv head).
 __host__ __device__ inline int pool_wg_count(const PoolParams& p) {
-  return p.batch * (p.n_slots * pool_groups(p.n_qb) + p.n_kvp * pool_groups(p.n_kb));
+  return p.batch * (p.n_slots * pool_groups(p.n_qb, p.pool_blocks) +
+                    p.n_kvp * pool_groups(p.n_kb, p.pool_blocks));
 }
 
-// One workgroup of 256 threads pools blocks blk0 .. blk0 + 15 (those below
-// nb) of a [S][D] matrix with row stride ss into dst [nb][D]; thread (bg, c)
-// sums 16-byte chunk c of block blk0 + bg over its brows rows (a multiple of
-// 8), eight rows' loads in flight, and stores the 8 pooled values as one
-// 16-byte chunk.
+// One workgroup of 256 threads pools blocks blk0 .. blk0 + PB - 1 (those
+// below nb) of a [S][D] matrix with row stride ss into dst [nb][D]; thread
+// (bg, c) sums 16-byte chunk c of block blk0 + bg over its brows rows (a
+// multiple of 8), eight rows' loads in flight, and stores the 8 pooled
+// values as one 16-byte chunk.
 template <typename T, int D>
 __device__ inline void pool_block_group(const uint16_t* base, int64_t ss, int64_t S, int nb,
                                         int blk0, int brows, uint16_t* dst) {
   constexpr int KCH = D / 8;  // 16-byte chunks per row
-  static_assert(kPoolBlocks * KCH <= 256, "one thread per (block, chunk)");
+  constexpr int PB = pool_blocks_for(D);
+  static_assert(PB * KCH <= 256, "one thread per (block, chunk)");
   const int t = threadIdx.x;
   const int bg = t / KCH;
   const int c = t - bg * KCH;
   const int blk = blk0 + bg;
-  if (bg >= kPoolBlocks || blk >= nb) return;
+  if (bg >= PB || blk >= nb) return;
   double acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0;
@@ -75,7 +74,8 @@ __device__ inline void pool_block_group(const uint16_t* base, int64_t ss, int64_
 // Workgroup g (0 <= g < pool_wg_count(P)) of the pooling pass.
 template <typename T, int D>
 __device__ inline void pool_workgroup(const PoolParams& P, int g) {
-  const int n_qg = pool_groups(P.n_qb);
+  constexpr int PB = pool_blocks_for(D);
+  const int n_qg = pool_groups(P.n_qb, PB);
   const int n_q_wg = P.batch * P.n_slots * n_qg;
   if (g < n_q_wg) {
     const int sb = g / n_qg;  // b * n_slots + slot
@@ -84,19 +84,19 @@ __device__ inline void pool_workgroup(const PoolParams& P, int g) {
     const int head = P.slot_heads[sb - b * P.n_slots];
     const uint16_t* base =
         reinterpret_cast<const uint16_t*>(P.q) + b * P.q_sb + int64_t(head) * P.q_sh;
-    pool_block_group<T, D>(base, P.q_ss, P.s_q, P.n_qb, grp * kPoolBlocks, P.pool_rows,
+    pool_block_group<T, D>(base, P.q_ss, P.s_q, P.n_qb, grp * PB, P.pool_rows,
                            P.q_pool + int64_t(sb) * P.n_qb_pad * D);
     return;
   }
   g -= n_q_wg;
-  const int n_kg = pool_groups(P.n_kb);
+  const int n_kg = pool_groups(P.n_kb, PB);
   const int bi = g / n_kg;  // b * n_kvp + i
   const int grp = g - bi * n_kg;
   const int b = bi / P.n_kvp;
   const int i = bi - b * P.n_kvp;
   const uint16_t* base =
       reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb + int64_t(P.kvp_head[i]) * P.k_sh;
-  pool_block_group<T, D>(base, P.k_ss, P.s_k, P.n_kb, grp * kPoolBlocks, P.pool_rows,
+  pool_block_group<T, D>(base, P.k_ss, P.s_k, P.n_kb, grp * PB, P.pool_rows,
                          P.k_pool + (int64_t(b) * P.n_slots + i) * P.n_kb * D);
 }
 

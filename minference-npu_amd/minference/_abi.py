@@ -53,7 +53,7 @@ MSA_ESTIMATE_SELECT_ONLY = 8
 
 MSA_MAX_HEADS = 128
 MSA_BLOCK = 64
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _DTYPE_CODE = {
     torch.bfloat16: MSA_DTYPE_BF16,

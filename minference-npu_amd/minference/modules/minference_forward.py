@@ -26,7 +26,7 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import torch
 
 from .. import _abi
-from ..ops.common import dense_scale, require_kernel_head_dim, sparse_scale
+from ..ops.common import VS_HEAD_DIMS, dense_scale, require_kernel_head_dim, sparse_scale
 from ..ops.rope import apply_rotary_pos_emb as apply_rotary_pos_emb_gpu, rope_supported
 from ..ops.vertical_slash_kernel import vs_sizes
 
@@ -179,6 +179,8 @@ def run_layer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan:
     """
     _abi.require_device(q, k, v)
     require_kernel_head_dim(q.shape[-1], "the patched attention forward")
+    if plan.vs_heads:
+        require_kernel_head_dim(q.shape[-1], "vertical_and_slash heads", VS_HEAD_DIMS)
     B, H, S_q, _ = q.shape
     if H > _abi.MSA_MAX_HEADS:
         raise NotImplementedError(

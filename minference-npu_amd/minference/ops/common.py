@@ -17,7 +17,9 @@ ALLOWED_HEAD_DIMS = (16, 32, 64, 128, 256, 512)
 
 # Head dims the HIP kernels are built for; the ops take any head_dim up to the
 # largest of them by zero-padding q, k and v to the next one.
-SUPPORTED_HEAD_DIMS = (64, 96, 128)
+SUPPORTED_HEAD_DIMS = (64, 96, 128, 256)
+# vertical_and_slash (estimator and attention) is built up to 128
+VS_HEAD_DIMS = (64, 96, 128)
 SUPPORTED_DTYPES = (torch.bfloat16, torch.float16)
 
 
@@ -118,14 +120,12 @@ def kernel_head_dim(d: int) -> int:
     )
 
 
-def require_kernel_head_dim(d: int, what: str) -> None:
+def require_kernel_head_dim(d: int, what: str, dims: Sequence[int] = SUPPORTED_HEAD_DIMS) -> None:
     """Paths that do not pad (vertical_and_slash, whose estimator divides by
-    the kernel's sqrt(D); the patched model forward) take the built head
-    dims only."""
-    if d not in SUPPORTED_HEAD_DIMS:
-        raise NotImplementedError(
-            f"{what} runs at head_dim {SUPPORTED_HEAD_DIMS} only, got {d}"
-        )
+    the kernel's sqrt(D) and is built up to 128; the patched model forward)
+    take the built head dims only."""
+    if d not in dims:
+        raise NotImplementedError(f"{what} runs at head_dim {tuple(dims)} only, got {d}")
 
 
 def pad_head_dim(t: torch.Tensor, dk: int) -> torch.Tensor:

@@ -22,8 +22,8 @@ from typing import Optional
 import torch
 
 from .. import _abi
-from .common import (accepts_float32, check_bnsd, check_supported, kernel_view, make_out,
-                     require_kernel_head_dim, sparse_scale)
+from .common import (VS_HEAD_DIMS, accepts_float32, check_bnsd, check_supported, kernel_view,
+                     make_out, require_kernel_head_dim, sparse_scale)
 
 __all__ = [
     "vertical_slash_sparse_attention",
@@ -78,7 +78,7 @@ def vertical_and_slash_estimate(q: torch.Tensor, k: torch.Tensor, vertical_size:
     nv, ns from :func:`vs_sizes`.  k may have fewer heads (GQA)."""
     assert q.dim() == 4 and k.dim() == 4
     check_supported(q, k)
-    require_kernel_head_dim(q.shape[-1], "vertical_and_slash")
+    require_kernel_head_dim(q.shape[-1], "vertical_and_slash", VS_HEAD_DIMS)
     _check_vs_shape(q, k)
     q, k = kernel_view(q), kernel_view(k)
     B, H, S, _ = q.shape
@@ -110,7 +110,7 @@ def vertical_and_slash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
     ``[B, H, S, D]`` tensors (k, v with H heads)."""
     check_bnsd(q, k, v)
     check_supported(q, k, v)
-    require_kernel_head_dim(q.shape[-1], "vertical_and_slash")
+    require_kernel_head_dim(q.shape[-1], "vertical_and_slash", VS_HEAD_DIMS)
     _check_vs_shape(q, k)
     q, k, v = kernel_view(q), kernel_view(k), kernel_view(v)
     v_idx, s_idx = vertical_and_slash_estimate(q, k, vertical_size, slash_size)
@@ -178,7 +178,7 @@ def vertical_slash_sparse_attention(
     )
     check_bnsd(query, key, value)
     check_supported(query, key, value)
-    require_kernel_head_dim(query.shape[-1], "vertical_and_slash")
+    require_kernel_head_dim(query.shape[-1], "vertical_and_slash", VS_HEAD_DIMS)
     B, H, S, _ = query.shape
     if tuple(v_idx.shape[:2]) != (B, H) or tuple(s_idx.shape[:2]) != (B, H):
         raise ValueError("v_idx / s_idx must be [B, H, n] for q of shape " f"{tuple(query.shape)}")

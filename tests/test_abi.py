@@ -148,6 +148,25 @@ def test_attention_validation(mutate, expected):
     assert attn(a["q"], a["k"], a["v"], a["o"], a["hd"], a["n"], ws=a["ws"], wsb=a["wsb"]) == expected
 
 
+def test_head_dim_256_accepted_and_vs_refused():
+    """D = 256 passes the attention and estimator checks (failing later, on
+    the deliberately small workspace); 160 is refused; vertical_and_slash
+    (estimator and attention) stays at D <= 128."""
+    lib = _abi.load_library()
+    d256 = [1, 4, 256, 256]
+    assert attn(t4(d256), t4(d256), t4(d256), t4(d256), heads(4), 4, wsb=100) == _abi.MSA_E_WORKSPACE
+    d160 = [1, 4, 256, 160]
+    assert attn(t4(d160), t4(d160), t4(d160), t4(d160), heads(4), 4) == _abi.MSA_E_HEAD_DIM
+    assert est(t4(d256), t4(d256), [0], [2], 2, wsb=100) == _abi.MSA_E_WORKSPACE
+    one = (ctypes.c_int32 * 1)(0)
+    sz = (ctypes.c_int32 * 1)(30)
+    st = lib.msa_vs_estimate(ctypes.byref(t4(d256)), ctypes.byref(t4(d256)), one, sz, sz, 1,
+                             FAKE, FAKE, 64, FAKE, FAKE, 64, FAKE, 1 << 40, None)
+    assert st == _abi.MSA_E_HEAD_DIM
+    vs_heads = heads(4, kind=_abi.MSA_KIND_VS, slot=0)
+    assert attn(t4(d256), t4(d256), t4(d256), t4(d256), vs_heads, 4) == _abi.MSA_E_HEAD_DIM
+
+
 def test_attention_full_kind_allows_longer_queries():
     """S_q > S_k is refused for causal kinds and accepted for MSA_KIND_FULL
     heads (the call then fails later, on the deliberately small workspace)."""
@@ -373,16 +392,22 @@ def test_skip_kind_is_exempt_from_head_checks():
 
 
 def test_head_dim_padding_helpers():
-    """Head dims up to 128 run at the next built size (zero padding); the
-    scale keeps the reference's rule for the original head_dim."""
+    """Head dims up to 256 run at the next built size (zero padding); the
+    scale keeps the reference's rule for the original head_dim;
+    vertical_and_slash takes the built sizes up to 128 only."""
     import torch
 
     from minference.ops import common as C
 
-    assert [C.kernel_head_dim(d) for d in (1, 40, 64, 65, 80, 96, 97, 112, 128)] == \
-        [64, 64, 64, 96, 96, 96, 128, 128, 128]
+    assert [C.kernel_head_dim(d) for d in (1, 40, 64, 65, 80, 96, 97, 112, 128, 129, 160, 256)] == \
+        [64, 64, 64, 96, 96, 96, 128, 128, 128, 256, 256, 256]
     with pytest.raises(NotImplementedError):
-        C.kernel_head_dim(129)
+        C.kernel_head_dim(257)
+    C.require_kernel_head_dim(256, "x")
+    with pytest.raises(NotImplementedError):
+        C.require_kernel_head_dim(256, "vertical_and_slash", C.VS_HEAD_DIMS)
+    with pytest.raises(NotImplementedError):
+        C.require_kernel_head_dim(160, "x")
     # (next allowed of 16/32/64/128/256/512)^-0.5, not of the padded size
     assert C.sparse_scale(24) == 32 ** -0.5 and C.sparse_scale(80) == 128 ** -0.5
     t = torch.arange(2 * 3 * 5 * 40, dtype=torch.float32).reshape(2, 3, 5, 40)

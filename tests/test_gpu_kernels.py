@@ -472,6 +472,8 @@ MIXED_SHAPES = [
     (1, 4, 2, 640, 640, 128, torch.bfloat16),    # D 128, GQA
     (2, 8, 4, 300, 1324, 96, torch.bfloat16),    # chunked prefill, batch 2
     (1, 8, 8, 130, 4000, 96, torch.float16),     # short chunk after a long cache
+    (1, 4, 2, 700, 700, 256, torch.bfloat16),    # D 256 (the row-split kernel), GQA
+    (1, 6, 3, 300, 1100, 256, torch.float16),    # D 256, chunked prefill, fp16
 ]
 
 

@@ -109,9 +109,16 @@ def test_random_layer(gpu_device, i):
             assert np.array_equal(got_c[:, s], want_c), f"case {i} head {h}: counts differ"
 
 
+N_OP_CASES = 24      # head dims up to 128
+N_OP_WIDE_CASES = 8  # head dims 130 .. 256 (zero-padded to 256)
+
+
 def _draw_op(i: int):
     rng = np.random.default_rng(77000 + i)
-    D = int(rng.choice([2 * int(rng.integers(4, 65)), 64, 96, 128]))  # even: RoPE'd inputs
+    if i < N_OP_CASES:
+        D = int(rng.choice([2 * int(rng.integers(4, 65)), 64, 96, 128]))  # even: RoPE'd inputs
+    else:
+        D = int(rng.choice([2 * int(rng.integers(65, 129)), 256]))
     B = int(rng.choice([1, 2]))
     H = int(rng.integers(1, 5))
     S_k = int(rng.choice([int(rng.integers(1, 300)), int(rng.integers(300, 2500))]))
@@ -125,10 +132,10 @@ def _draw_op(i: int):
     return B, H, S_q, S_k, D, dtype, op, n_init, n_local, topk
 
 
-@pytest.mark.parametrize("i", range(24))
+@pytest.mark.parametrize("i", range(N_OP_CASES + N_OP_WIDE_CASES))
 def test_random_op(gpu_device, i):
     """The op-level entry points (streaming_forward, block_sparse_attention,
-    dense_attention causal and not) at random shapes and head dims up to 128
+    dense_attention causal and not) at random shapes and head dims up to 256
     (zero-padded to the built sizes), fp32 outputs against the oracle on the
     unpadded inputs (ops/streaming_kernel_npu.py:349-397,
     ops/block_sparse_kernel_npu.py:609-709, backend_npu/attention.py:192-255)."""
@@ -162,15 +169,18 @@ def test_random_op(gpu_device, i):
     assert_close_f32(out, ref, what=f"random op case {i}")
 
 
-@pytest.mark.parametrize("i", range(12))
+@pytest.mark.parametrize("i", range(16))
 def test_random_decode(gpu_device, i):
     """decode_dense (one query row against the whole cache; split-K partials
-    and their merge) at random cache lengths, GQA groups and head dims
-    (backend_npu/attention.py:274-314)."""
+    and their merge) at random cache lengths, GQA groups and head dims up to
+    256 (backend_npu/attention.py:274-314)."""
     from minference.backend.attention import decode_dense
 
     rng = np.random.default_rng(91000 + i)
-    D = int(rng.choice([2 * int(rng.integers(4, 65)), 64, 96, 128]))  # even: RoPE'd inputs
+    if i < 12:
+        D = int(rng.choice([2 * int(rng.integers(4, 65)), 64, 96, 128]))  # even: RoPE'd inputs
+    else:
+        D = int(rng.choice([2 * int(rng.integers(65, 129)), 256]))
     B = int(rng.choice([1, 2, 3]))
     Hkv = int(rng.choice([1, 2, 4]))
     H = Hkv * int(rng.choice([1, 2, 4]))
