@@ -295,11 +295,14 @@ static int cus_per_xcd() {
 
 // The attention kernel reads K in place, from the caller's rows, when every
 // offset of one kv head's padded rows fits 31 bits and the rows do not
-// overlap; otherwise the staging writes K in operand order first.
+// overlap; otherwise the staging writes K in operand order first.  D = 256
+// always takes staged K: its kernel reads every tile's K once per wave, and
+// a staged operand is 8 whole cache lines where an in-place one touches 16
+// half lines.
 static bool k_in_place(const msa_tensor4* k) {
   const int64_t D = k->size[3], ss = k->stride[2];
   const int64_t s_pad = cdiv(k->size[2], MSA_BLOCK) * MSA_BLOCK;
-  return ss >= D && (s_pad * ss + D) * 2 <= (int64_t(1) << 31);
+  return D <= 128 && ss >= D && (s_pad * ss + D) * 2 <= (int64_t(1) << 31);
 }
 
 static int stage_setup(const msa_tensor4* k, const msa_tensor4* v, void* workspace,

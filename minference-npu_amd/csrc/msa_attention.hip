@@ -211,7 +211,12 @@ __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
       const int l = gi & 63;
       const int cks = gi >> 6;  // chunk * NDB + ks
       const int c = cks / SS::NDB, ks = cks - c * SS::NDB;
-      const int j = src_row(j0 + 16 * c + (l & 15));
+      // D = 256: the keys of each 32-key span in attn_wide_kernel's order
+      // (8 (r / 4) + r % 4, then 8 (r / 4) + 4 + r % 4), so that each of its
+      // K operands is one whole 16-key chunk
+      const int q = 16 * c + (l & 15);
+      const int kq = D > 128 ? 32 * (q >> 5) + 8 * ((q & 15) >> 2) + 4 * ((q >> 4) & 1) + (q & 3) : q;
+      const int j = src_row(j0 + kq);
       x[u] = j >= 0 ? load16(src + int64_t(j) * P.k_ss + 32 * ks + 8 * (l >> 4)) : zero_u32x4();
     }
 #pragma unroll
@@ -1042,7 +1047,8 @@ void attn_kernel(AttnParams P) {
 // every key of the item's tiles itself (no merge).  Each 32-key span of a
 // tile gives two 16x16x32 QK accumulators whose rows are the keys
 //   A: 8 (r / 4) + (r % 4),   B: 8 (r / 4) + 4 + (r % 4)   (r = accumulator row)
-// (the K operand rows are read in that order), so lane l holds keys
+// (the staging writes K of this head dim in that key order, so each QK
+// operand is one contiguous staged 16-key chunk), so lane l holds keys
 // 8 (l / 16) .. +7 of its query row l % 16: rounded to fp16 they are the B
 // operand of the 16x16x32 PV product as they stand.  V comes from the staged
 // 32x32x16 operand layout, one 16-byte granule per lane.  The row max is
@@ -1110,14 +1116,10 @@ void attn_wide_kernel(AttnParams P) {
 
   const int64_t bk = int64_t(b) * (P.heads / P.kv_group) + kvh;
   const float vfac = __builtin_amdgcn_ldexpf(1.0f, load_uniform(P.vexp + bk));
-  const bool kin = P.k_in_place != 0;
-  const __amdgpu_buffer_rsrc_t krs =
-      kin ? __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(P.k) + b * P.k_sb +
-                                      int64_t(kvh) * P.k_sh),
-                short(0), int(((P.s_k - 1) * P.k_ss + D) * 2), 0x00020000)
-          : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.kt + bk * P.s_pad * D),
-                                              short(0), P.s_pad * D * 2, 0x00020000);
+  // K is always staged at this head dim (the staging orders each 32-key
+  // span's keys for this kernel)
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.kt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(P.vt + bk * P.s_pad * D), short(0), P.s_pad * D * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -1147,22 +1149,21 @@ void attn_wide_kernel(AttnParams P) {
   float m = -1e30f;  // running (biased) max of the row in scaled log2 units
   float l = 0.0f;    // this lane's share of the row sum
 
-  // K operand rows of virtual chunk (span kh, half ab) of tile t: lane row lc
-  // reads key 64t + 32kh + 8 (lc / 4) + 4 ab + lc % 4, elements 32 ks + 8 lr
-  auto load_k = [&](int t, int kh, int ab, u32x4 (&kr)[NKS]) INLINE {
-    const int key = 64 * t + 32 * kh + 8 * (lc >> 2) + 4 * ab + (lc & 3);
-    if (kin) {
-      const uint32_t vo = uint32_t(key) * uint32_t(P.k_ss) * 2u + 16u * lr;
+  // K operand of virtual chunk vc (span vc / 2, half vc % 2) of tile t: the
+  // staged chunk 4t + vc, whose row r is key 32 (vc / 2) + 8 (r / 4) +
+  // 4 (vc % 2) + r % 4 of the tile; lane (lc, lr) of k-step ks holds
+  // elements 32 ks + 8 lr .. +7 of row lc
+  auto load_k = [&](int t, int vc, u32x4 (&kr)[NKS]) INLINE {
+    const uint32_t vo = uint32_t((4 * t + vc) * NKS * 1024 + lane * 16);
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
-        kr[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo, 64 * ks, 0));
-    } else {
-      // staged: chunk key / 16, k-step ks, lane (key % 16) + 16 lr
-      const uint32_t vo = uint32_t(((key >> 4) * NKS) * 1024 + ((key & 15) + 16 * lr) * 16);
+    for (int ks = 0; ks < NKS; ++ks)
+      kr[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo, 1024 * ks, 0));
+  };
+  auto qk = [&](const u32x4 (&kr)[NKS]) INLINE -> f32x4 {
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
-        kr[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo, 1024 * ks, 0));
-    }
+    for (int ks = 0; ks < NKS; ++ks) acc = mfma_qk<T>(kr[ks], qb[ks], acc);
+    return acc;
   };
   // V^T operand (dims 16 db + lc, keys 32 kh + 8 lr .. +7 of tile t) from the
   // staged layout: chunk 4t + 2kh + lr / 2, block db / 2, lane 32 (lr % 2) +
@@ -1177,21 +1178,26 @@ void attn_wide_kernel(AttnParams P) {
     }
   };
 
+  // K of the next virtual chunk is requested before the current one's QK
+  // (two register sets); the next tile's first chunk before the softmax
+  u32x4 k0[NKS], k1[NKS];
+  int t = total > 0 ? seq.template finish<false>(seq.fetch(0)) : 0;
+  load_k(t, 0, k0);
   for (int p = 0; p < total; ++p) {
-    const int t = seq.template finish<false>(seq.fetch(p));
+    // positions past the end repeat the last tile (loads never consumed)
+    const int tn = seq.template finish<false>(seq.fetch(p + 1));
     // scores of the tile: s[kh][ab] (lane: keys 8 lr + 4 ab + i of span kh)
     f32x4 s[2][2];
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-      for (int ab = 0; ab < 2; ++ab) {
-        u32x4 kr[NKS];
-        load_k(t, kh, ab, kr);
-        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) acc = mfma_qk<T>(kr[ks], qb[ks], acc);
-        s[kh][ab] = acc;
-      }
+    load_k(t, 1, k1);
+    s[0][0] = qk(k0);
+    load_k(t, 2, k0);
+    s[0][1] = qk(k1);
+    load_k(t, 3, k1);
+    s[1][0] = qk(k0);
+    u32x4 vr[NDO];  // V of span 0, in flight under the last QK and the softmax
+    load_v(t, 0, vr);
+    load_k(tn, 0, k0);
+    s[1][1] = qk(k1);
     // visibility (every tile: the walk has no separate unmasked part here)
     float mx = -__builtin_inff();
 #pragma unroll
@@ -1218,8 +1224,7 @@ void attn_wide_kernel(AttnParams P) {
     }
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
-      u32x4 vr[NDO];
-      load_v(t, kh, vr);
+      if (kh == 1) load_v(t, 1, vr);  // span 1 into the registers span 0's PV has read
       float pv[2][4];
 #pragma unroll
       for (int ab = 0; ab < 2; ++ab)
@@ -1241,6 +1246,7 @@ void attn_wide_kernel(AttnParams P) {
                                                        __builtin_bit_cast(f16x8, pb), o[db], 0,
                                                        0, 0);
     }
+    t = tn;
   }
   // row sum over the row's four lanes; O^T block db: lane l holds dims
   // 16 db + 4 lr .. +3 of row lc
