@@ -1092,7 +1092,6 @@ void attn_wide_kernel(AttnParams P) {
   const int last_tile = min(a1 >> 6, P.n_kb - 1);
   const int n_init = P.hd[h].p1;
   const int n_local = P.hd[h].p2;
-  const int Fe = min(min((a0 + 1) >> 6, P.s_k >> 6), last_tile + 1);
   TileSeq seq;
   seq.n_kb = P.n_kb;
   seq.list = nullptr;
@@ -1112,7 +1111,6 @@ void attn_wide_kernel(AttnParams P) {
     seq.set({0, 0, 0, 0, 0}, {last_tile + 1, 0, 0, 0, 0}, 1);
   }
   const int total = seq.total;
-  (void)Fe;
 
   const int64_t bk = int64_t(b) * (P.heads / P.kv_group) + kvh;
   const float vfac = __builtin_amdgcn_ldexpf(1.0f, load_uniform(P.vexp + bk));
