@@ -27,11 +27,14 @@ from test_gpu_kernels import assert_close_f32, to_dev
 pytestmark = pytest.mark.gpu
 
 N_CASES = 40
+N_WIDE_CASES = 8  # head dim 256 (no vertical_and_slash heads: built up to 128)
 
 
 def _draw(i: int):
     rng = np.random.default_rng(20261202 + i)
     D = int(rng.choice([64, 96, 96, 128]))
+    if i >= N_CASES:
+        D = 256
     B = int(rng.choice([1, 1, 2]))
     Hkv = int(rng.choice([1, 2, 4]))
     H = Hkv * int(rng.choice([1, 2, 3]))
@@ -42,7 +45,7 @@ def _draw(i: int):
     sink = 8.0 if rng.random() < 0.5 else None
     n_kb = math.ceil(S_k / 64)
     pats = {}
-    vs_ok = S_q == S_k
+    vs_ok = S_q == S_k and D <= 128
     for h in range(H):
         kind = rng.choice(["stream_llm", "block_sparse", "dense", "vertical_and_slash"],
                           p=[0.3, 0.35, 0.1, 0.25] if vs_ok else [0.4, 0.45, 0.15, 0.0])
@@ -58,7 +61,7 @@ def _draw(i: int):
     return B, H, Hkv, S_q, S_k, D, dtype, sink, pats
 
 
-@pytest.mark.parametrize("i", range(N_CASES))
+@pytest.mark.parametrize("i", range(N_CASES + N_WIDE_CASES))
 def test_random_layer(gpu_device, i):
     from minference import _abi
     from minference.modules.minference_forward import build_layer_plan, run_layer_attention
@@ -109,8 +112,9 @@ def test_random_layer(gpu_device, i):
             assert np.array_equal(got_c[:, s], want_c), f"case {i} head {h}: counts differ"
 
 
-N_OP_CASES = 24      # head dims up to 128
-N_OP_WIDE_CASES = 8  # head dims 130 .. 256 (zero-padded to 256)
+N_OP_CASES = 24       # head dims up to 128
+N_OP_WIDE_CASES = 8   # head dims 130 .. 256 (zero-padded to 256)
+N_OP_BLOCK_CASES = 6  # block_sparse_attention with blocks of 128, 256 or 512 tokens
 
 
 def _draw_op(i: int):
@@ -129,22 +133,29 @@ def _draw_op(i: int):
         S_q = int(rng.integers(1, 2 * S_k + 2))
     n_init, n_local = int(rng.integers(0, 400)), int(rng.integers(1, 3000))
     topk = int(rng.integers(1, 60))
-    return B, H, S_q, S_k, D, dtype, op, n_init, n_local, topk
+    bs = 64
+    if i >= N_OP_CASES + N_OP_WIDE_CASES:
+        op, bs = "block", int(rng.choice([128, 256, 512]))
+        D = int(rng.choice([64, 80, 96, 128, 256]))
+        S_q = min(S_q, S_k)
+        topk = int(rng.integers(1, 12))
+    return B, H, S_q, S_k, D, dtype, op, n_init, n_local, topk, bs
 
 
-@pytest.mark.parametrize("i", range(N_OP_CASES + N_OP_WIDE_CASES))
+@pytest.mark.parametrize("i", range(N_OP_CASES + N_OP_WIDE_CASES + N_OP_BLOCK_CASES))
 def test_random_op(gpu_device, i):
-    """The op-level entry points (streaming_forward, block_sparse_attention,
-    dense_attention causal and not) at random shapes and head dims up to 256
-    (zero-padded to the built sizes), fp32 outputs against the oracle on the
+    """The op-level entry points (streaming_forward, block_sparse_attention
+    with blocks of 64 to 512 tokens, dense_attention causal and not) at random
+    shapes and head dims up to 256 (zero-padded to the built sizes), fp32
+    outputs against the oracle on the
     unpadded inputs (ops/streaming_kernel_npu.py:349-397,
     ops/block_sparse_kernel_npu.py:609-709, backend_npu/attention.py:192-255)."""
     from minference import block_sparse_attention, dense_attention, streaming_forward
     from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
 
-    B, H, S_q, S_k, D, dtype, op, n_init, n_local, topk = _draw_op(i)
+    B, H, S_q, S_k, D, dtype, op, n_init, n_local, topk, bs = _draw_op(i)
     print(f"[random op] case {i}: {op} B={B} H={H} S_q={S_q} S_k={S_k} D={D} {dtype_tag(dtype)} "
-          f"n_init={n_init} n_local={n_local} topk={topk}", flush=True)
+          f"n_init={n_init} n_local={n_local} topk={topk} block={bs}", flush=True)
     q, k, v = make_qkv(B, H, S_q, S_k, D, dtype, seed=5000 + i, sink_scale=8.0,
                        use_rope=S_q <= S_k)
     dq, dk, dv = to_dev(gpu_device, q, k, v)
@@ -154,12 +165,13 @@ def test_random_op(gpu_device, i):
         streaming_forward(dq, dk, dv, n_init, n_local, out=out)
         ref = O.streaming_attention(qn, kn, vn, n_init, n_local)
     elif op == "block":
-        n_kb = math.ceil(S_k / 64)
-        ids = select_block_sparse_topk_indices(dq, dk, topk).cpu().numpy()
-        ref_ids, _ = O.select_block_sparse_topk_indices(qn, kn, min(topk, n_kb), dtype_tag(dtype))
+        n_kb = math.ceil(S_k / bs)
+        ids = select_block_sparse_topk_indices(dq, dk, topk, bs).cpu().numpy()
+        ref_ids, _ = O.select_block_sparse_topk_indices(qn, kn, min(topk, n_kb), dtype_tag(dtype),
+                                                        block=bs)
         assert np.array_equal(ids, ref_ids), f"case {i}: ids differ"
-        block_sparse_attention(dq, dk, dv, topk, out=out)
-        ref = O.block_sparse_from_indices(qn, kn, vn, ref_ids)
+        block_sparse_attention(dq, dk, dv, topk, bs, out=out)
+        ref = O.block_sparse_from_indices(qn, kn, vn, ref_ids, block=bs)
     elif op == "dense":
         dense_attention(dq, dk, dv, out=out)
         ref = O.dense_causal(qn, kn, vn)
