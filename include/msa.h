@@ -36,7 +36,7 @@ extern "C" {
 #define MSA_E_NULL (-1)        /* a required pointer is NULL */
 #define MSA_E_RANK (-2)        /* shape mismatch between q/k/v/o */
 #define MSA_E_DTYPE (-3)       /* unsupported or mismatched dtype */
-#define MSA_E_HEAD_DIM (-4)    /* D not in {64, 96, 128, 256} ({64, 96, 128} for vertical_and_slash) */
+#define MSA_E_HEAD_DIM (-4)    /* D not in {64, 96, 128, 256, 512} ({64, 96, 128} for vertical_and_slash) */
 #define MSA_E_ALIGN (-5)       /* D stride != 1, rows not 16-byte aligned or row stride >= 2^24 */
 #define MSA_E_BLOCK (-6)       /* unsupported block size */
 #define MSA_E_TOPK (-7)        /* topk < 1 or topk > n_kv_blocks */
@@ -73,7 +73,7 @@ extern "C" {
 
 typedef struct msa_tensor4 {
   void* data;
-  int64_t size[4];   /* B, H, S, D (D = 64, 96, 128 or 256) */
+  int64_t size[4];   /* B, H, S, D (D = 64, 96, 128, 256 or 512) */
   int64_t stride[4]; /* elements */
   int32_t dtype;     /* MSA_DTYPE_* */
   int32_t reserved;

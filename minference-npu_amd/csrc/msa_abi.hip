@@ -26,7 +26,7 @@ int elem_size(int dtype) {
   }
 }
 
-bool head_dim_ok(int64_t d) { return d == 64 || d == 96 || d == 128 || d == 256; }
+bool head_dim_ok(int64_t d) { return d == 64 || d == 96 || d == 128 || d == 256 || d == 512; }
 // vertical_and_slash estimator and attention: up to 128
 bool vs_head_dim_ok(int64_t d) { return d == 64 || d == 96 || d == 128; }
 
@@ -77,7 +77,7 @@ const char* msa_status_str(int status) {
     case MSA_E_NULL: return "a required pointer is NULL";
     case MSA_E_RANK: return "shape mismatch between q, k, v and o";
     case MSA_E_DTYPE: return "unsupported or mismatched dtype (q/k/v must be bf16 or fp16; o same or fp32)";
-    case MSA_E_HEAD_DIM: return "head_dim must be 64, 96, 128 or 256 (vertical_and_slash: 64, 96 or 128)";
+    case MSA_E_HEAD_DIM: return "head_dim must be 64, 96, 128, 256 or 512 (vertical_and_slash: 64, 96 or 128)";
     case MSA_E_ALIGN: return "head_dim stride must be 1, rows 16-byte aligned and the row stride below 2^24";
     case MSA_E_BLOCK: return "block size must be 64, 128, 256 or 512";
     case MSA_E_TOPK: return "topk must be in [1, n_kv_blocks]";
@@ -296,9 +296,9 @@ static int cus_per_xcd() {
 // The attention kernel reads K in place, from the caller's rows, when every
 // offset of one kv head's padded rows fits 31 bits and the rows do not
 // overlap; otherwise the staging writes K in operand order first.  D = 256
-// always takes staged K: its kernel reads every tile's K once per wave, and
-// a staged operand is 8 whole cache lines where an in-place one touches 16
-// half lines.
+// and 512 always take staged K: their kernel reads every tile's K once per
+// wave, and a staged operand is 8 whole cache lines where an in-place one
+// touches 16 half lines.
 static bool k_in_place(const msa_tensor4* k) {
   const int64_t D = k->size[3], ss = k->stride[2];
   const int64_t s_pad = cdiv(k->size[2], MSA_BLOCK) * MSA_BLOCK;

@@ -211,7 +211,7 @@ __global__ __launch_bounds__(256) void stage_kernel(StageParams P) {
       const int l = gi & 63;
       const int cks = gi >> 6;  // chunk * NDB + ks
       const int c = cks / SS::NDB, ks = cks - c * SS::NDB;
-      // D = 256: the keys of each 32-key span in attn_wide_kernel's order
+      // D > 128: the keys of each 32-key span in attn_wide_kernel's order
       // (8 (r / 4) + r % 4, then 8 (r / 4) + 4 + r % 4), so that each of its
       // K operands is one whole 16-key chunk
       const int q = 16 * c + (l & 15);
@@ -282,11 +282,13 @@ hipError_t launch_stage(const StageParams& p, int dtype, int D, hipStream_t st) 
     if (D == 64) return launch_stage_t<Bf16, 64>(p, st);
     if (D == 96) return launch_stage_t<Bf16, 96>(p, st);
     if (D == 256) return launch_stage_t<Bf16, 256>(p, st);
+    if (D == 512) return launch_stage_t<Bf16, 512>(p, st);
     return launch_stage_t<Bf16, 128>(p, st);
   }
   if (D == 64) return launch_stage_t<F16, 64>(p, st);
   if (D == 96) return launch_stage_t<F16, 96>(p, st);
   if (D == 256) return launch_stage_t<F16, 256>(p, st);
+  if (D == 512) return launch_stage_t<F16, 512>(p, st);
   return launch_stage_t<F16, 128>(p, st);
 }
 
@@ -295,11 +297,13 @@ hipError_t launch_vscale(const StageParams& p, int dtype, int D, hipStream_t st)
     if (D == 64) return launch_vscale_t<Bf16, 64>(p, st);
     if (D == 96) return launch_vscale_t<Bf16, 96>(p, st);
     if (D == 256) return launch_vscale_t<Bf16, 256>(p, st);
+    if (D == 512) return launch_vscale_t<Bf16, 512>(p, st);
     return launch_vscale_t<Bf16, 128>(p, st);
   }
   if (D == 64) return launch_vscale_t<F16, 64>(p, st);
   if (D == 96) return launch_vscale_t<F16, 96>(p, st);
   if (D == 256) return launch_vscale_t<F16, 256>(p, st);
+  if (D == 512) return launch_vscale_t<F16, 512>(p, st);
   return launch_vscale_t<F16, 128>(p, st);
 }
 
@@ -1041,9 +1045,9 @@ void attn_kernel(AttnParams P) {
 }
 
 // ---------------------------------------------------------------------------
-// Head dim 256 (the ops zero-pad head dims 129..255 to it).  The same work
-// items and tile walk as attn_kernel; the O of 64 rows x 256 dims does not
-// fit one wave, so wave w owns the 16 query rows 16w .. 16w+15 and walks
+// Head dims 256 and 512 (the ops zero-pad head dims 129..511 to them).  The
+// same work items and tile walk as attn_kernel; the O of 64 rows x D does
+// not fit one wave, so wave w owns the 16 query rows 16w .. 16w+15 and walks
 // every key of the item's tiles itself (no merge).  Each 32-key span of a
 // tile gives two 16x16x32 QK accumulators whose rows are the keys
 //   A: 8 (r / 4) + (r % 4),   B: 8 (r / 4) + 4 + (r % 4)   (r = accumulator row)
@@ -1053,11 +1057,12 @@ void attn_kernel(AttnParams P) {
 // operand of the 16x16x32 PV product as they stand.  V comes from the staged
 // 32x32x16 operand layout, one 16-byte granule per lane.  The row max is
 // exact per tile (O rescaled when it grows), P biased to 2^kPBias like
-// attn_kernel; fully masked rows give 0.
-template <typename T, bool OUT_F32>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+// attn_kernel; fully masked rows give 0.  At D = 512 one wave per SIMD (the
+// O accumulators and two K chunks take about 450 registers).
+template <typename T, bool OUT_F32, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D > 256 ? 1 : 2)))
 void attn_wide_kernel(AttnParams P) {
-  constexpr int D = 256;
+  static_assert(D == 256 || D == 512, "wide head dims");
   constexpr int NKS = D / 32;  // QK k-steps
   constexpr int NDO = D / 16;  // PV output blocks of 16 dims
   constexpr int NDB = D / 32;  // staged V blocks of 32 dims per 16-key chunk
@@ -1178,24 +1183,37 @@ void attn_wide_kernel(AttnParams P) {
 
   // K of the next virtual chunk is requested before the current one's QK
   // (two register sets); the next tile's first chunk before the softmax
+  // (at D = 512 one K register set: two would not fit beside O and V)
   u32x4 k0[NKS], k1[NKS];
   int t = total > 0 ? seq.template finish<false>(seq.fetch(0)) : 0;
-  load_k(t, 0, k0);
+  if constexpr (D <= 256) load_k(t, 0, k0);
   for (int p = 0; p < total; ++p) {
     // positions past the end repeat the last tile (loads never consumed)
     const int tn = seq.template finish<false>(seq.fetch(p + 1));
     // scores of the tile: s[kh][ab] (lane: keys 8 lr + 4 ab + i of span kh)
     f32x4 s[2][2];
-    load_k(t, 1, k1);
-    s[0][0] = qk(k0);
-    load_k(t, 2, k0);
-    s[0][1] = qk(k1);
-    load_k(t, 3, k1);
-    s[1][0] = qk(k0);
     u32x4 vr[NDO];  // V of span 0, in flight under the last QK and the softmax
-    load_v(t, 0, vr);
-    load_k(tn, 0, k0);
-    s[1][1] = qk(k1);
+    if constexpr (D > 256) {
+      load_k(t, 0, k0);
+      s[0][0] = qk(k0);
+      load_k(t, 1, k0);
+      s[0][1] = qk(k0);
+      load_k(t, 2, k0);
+      s[1][0] = qk(k0);
+      load_v(t, 0, vr);
+      load_k(t, 3, k0);
+      s[1][1] = qk(k0);
+    } else {
+      load_k(t, 1, k1);
+      s[0][0] = qk(k0);
+      load_k(t, 2, k0);
+      s[0][1] = qk(k1);
+      load_k(t, 3, k1);
+      s[1][0] = qk(k0);
+      load_v(t, 0, vr);
+      load_k(tn, 0, k0);
+      s[1][1] = qk(k1);
+    }
     // visibility (every tile: the walk has no separate unmasked part here)
     float mx = -__builtin_inff();
 #pragma unroll
@@ -1268,7 +1286,7 @@ void attn_wide_kernel(AttnParams P) {
   }
 }
 
-template <typename T, bool OUT_F32>
+template <typename T, bool OUT_F32, int D>
 static hipError_t launch_wide_t(const AttnParams& p, hipStream_t st) {
   int64_t items = int64_t(p.n_qb) * p.batch * p.heads;
   if (p.n_hl) {
@@ -1277,7 +1295,7 @@ static hipError_t launch_wide_t(const AttnParams& p, hipStream_t st) {
     items = 8 * int64_t(longest);
   }
   if (items == 0) return hipSuccess;
-  hipLaunchKernelGGL((attn_wide_kernel<T, OUT_F32>), dim3(uint32_t(items)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((attn_wide_kernel<T, OUT_F32, D>), dim3(uint32_t(items)), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -1306,7 +1324,8 @@ static hipError_t launch_attn_t(const AttnParams& p, hipStream_t st) {
 
 template <typename T, bool OUT_F32, bool VS>
 static hipError_t launch_attn_d(const AttnParams& p, int D, hipStream_t st) {
-  if (D == 256) return VS ? hipErrorInvalidValue : launch_wide_t<T, OUT_F32>(p, st);
+  if (D == 256) return VS ? hipErrorInvalidValue : launch_wide_t<T, OUT_F32, 256>(p, st);
+  if (D == 512) return VS ? hipErrorInvalidValue : launch_wide_t<T, OUT_F32, 512>(p, st);
   if (D == 64) return launch_attn_t<T, OUT_F32, 64, VS>(p, st);
   if (D == 96) return launch_attn_t<T, OUT_F32, 96, VS>(p, st);
   return launch_attn_t<T, OUT_F32, 128, VS>(p, st);

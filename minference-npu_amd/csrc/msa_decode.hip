@@ -189,9 +189,9 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams P) {
     mine[64 * NL * 8 + 1] = l;
   }
   __syncthreads();
-  // thread t < D: element d = t of O, summing every (wave, piece) whose
-  // piece covers d, each wave scaled by exp2(m_w - M)
-  if (tid < D) {
+  // elements d = t, t + 256, ... of O (thread t), summing every (wave,
+  // piece) whose piece covers d, each wave scaled by exp2(m_w - M)
+  for (int d = tid; d < D; d += 256) {
     float mw[4], M = -__builtin_inff();
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams P) {
       M = fmaxf(M, mw[v]);
     }
     float L = 0.0f, acc = 0.0f;
-    const int d = tid, dp = d & ~7, du = d & 7;
+    const int dp = d & ~7, du = d & 7;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const float f = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mw[v] - M);
@@ -277,12 +277,12 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams P) {
     *reinterpret_cast<float4*>(&acc_g[g][4 * c]) = float4{a0, a1, a2, a3};
   }
   __syncthreads();
-  if (tid < D) {
+  for (int d = tid; d < D; d += 256) {
     float acc = 0.0f;
 #pragma unroll
-    for (int q = 0; q < G; ++q) acc += acc_g[q][tid];
+    for (int q = 0; q < G; ++q) acc += acc_g[q][d];
     const float r = L > 0.0f ? acc / L : 0.0f;
-    const int64_t off = b * P.o_sb + int64_t(h) * P.o_sh + tid;
+    const int64_t off = b * P.o_sb + int64_t(h) * P.o_sh + d;
     if constexpr (OUT_F32) {
       reinterpret_cast<float*>(P.o)[off] = r;
     } else {
@@ -306,6 +306,7 @@ static hipError_t launch_decode_d(const DecodeParams& p, int D, hipStream_t st) 
   if (D == 64) return launch_decode_t<T, OUT_F32, 64>(p, st);
   if (D == 96) return launch_decode_t<T, OUT_F32, 96>(p, st);
   if (D == 256) return launch_decode_t<T, OUT_F32, 256>(p, st);
+  if (D == 512) return launch_decode_t<T, OUT_F32, 512>(p, st);
   return launch_decode_t<T, OUT_F32, 128>(p, st);
 }
 

@@ -680,11 +680,13 @@ hipError_t launch_pool(const PoolParams& p, int dtype, int D, hipStream_t st) {
     if (D == 64) return launch_pool_t<Bf16, 64>(p, st);
     if (D == 96) return launch_pool_t<Bf16, 96>(p, st);
     if (D == 256) return launch_pool_t<Bf16, 256>(p, st);
+    if (D == 512) return launch_pool_t<Bf16, 512>(p, st);
     return launch_pool_t<Bf16, 128>(p, st);
   }
   if (D == 64) return launch_pool_t<F16, 64>(p, st);
   if (D == 96) return launch_pool_t<F16, 96>(p, st);
   if (D == 256) return launch_pool_t<F16, 256>(p, st);
+  if (D == 512) return launch_pool_t<F16, 512>(p, st);
   return launch_pool_t<F16, 128>(p, st);
 }
 
@@ -714,11 +716,13 @@ hipError_t launch_score(const ScoreParams& p, int dtype, int D, hipStream_t st) 
     if (D == 64) return launch_score_d<Bf16, 64>(p, st);
     if (D == 96) return launch_score_d<Bf16, 96>(p, st);
     if (D == 256) return launch_score_d<Bf16, 256>(p, st);
+    if (D == 512) return launch_score_d<Bf16, 512>(p, st);
     return launch_score_d<Bf16, 128>(p, st);
   }
   if (D == 64) return launch_score_d<F16, 64>(p, st);
   if (D == 96) return launch_score_d<F16, 96>(p, st);
   if (D == 256) return launch_score_d<F16, 256>(p, st);
+  if (D == 512) return launch_score_d<F16, 512>(p, st);
   return launch_score_d<F16, 128>(p, st);
 }
 

@@ -14,8 +14,8 @@ namespace msa {
 //   k_pool [batch*n_slots][n_kb][D]      (entry b * n_slots + i: the i-th
 //                                         distinct kv head of the slots)
 // Blocks per pooling workgroup: one thread per (block, 16-byte chunk of a
-// row), 16 blocks up to D = 128, 8 at D = 256.
-__host__ __device__ constexpr int pool_blocks_for(int D) { return D > 128 ? 8 : 16; }
+// row), 16 blocks up to D = 128, 8 at D = 256, 4 at D = 512.
+__host__ __device__ constexpr int pool_blocks_for(int D) { return D > 256 ? 4 : D > 128 ? 8 : 16; }
 
 struct PoolParams {
   const void* q;

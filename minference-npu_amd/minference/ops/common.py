@@ -17,7 +17,7 @@ ALLOWED_HEAD_DIMS = (16, 32, 64, 128, 256, 512)
 
 # Head dims the HIP kernels are built for; the ops take any head_dim up to the
 # largest of them by zero-padding q, k and v to the next one.
-SUPPORTED_HEAD_DIMS = (64, 96, 128, 256)
+SUPPORTED_HEAD_DIMS = (64, 96, 128, 256, 512)
 # vertical_and_slash (estimator and attention) is built up to 128
 VS_HEAD_DIMS = (64, 96, 128)
 SUPPORTED_DTYPES = (torch.bfloat16, torch.float16)

@@ -149,12 +149,14 @@ def test_attention_validation(mutate, expected):
 
 
 def test_head_dim_256_accepted_and_vs_refused():
-    """D = 256 passes the attention and estimator checks (failing later, on
+    """D = 256 and 512 pass the attention and estimator checks (failing later, on
     the deliberately small workspace); 160 is refused; vertical_and_slash
     (estimator and attention) stays at D <= 128."""
     lib = _abi.load_library()
     d256 = [1, 4, 256, 256]
     assert attn(t4(d256), t4(d256), t4(d256), t4(d256), heads(4), 4, wsb=100) == _abi.MSA_E_WORKSPACE
+    d512 = [1, 4, 256, 512]
+    assert attn(t4(d512), t4(d512), t4(d512), t4(d512), heads(4), 4, wsb=100) == _abi.MSA_E_WORKSPACE
     d160 = [1, 4, 256, 160]
     assert attn(t4(d160), t4(d160), t4(d160), t4(d160), heads(4), 4) == _abi.MSA_E_HEAD_DIM
     assert est(t4(d256), t4(d256), [0], [2], 2, wsb=100) == _abi.MSA_E_WORKSPACE
@@ -392,17 +394,18 @@ def test_skip_kind_is_exempt_from_head_checks():
 
 
 def test_head_dim_padding_helpers():
-    """Head dims up to 256 run at the next built size (zero padding); the
+    """Head dims up to 512 run at the next built size (zero padding); the
     scale keeps the reference's rule for the original head_dim;
     vertical_and_slash takes the built sizes up to 128 only."""
     import torch
 
     from minference.ops import common as C
 
-    assert [C.kernel_head_dim(d) for d in (1, 40, 64, 65, 80, 96, 97, 112, 128, 129, 160, 256)] == \
-        [64, 64, 64, 96, 96, 96, 128, 128, 128, 256, 256, 256]
+    assert [C.kernel_head_dim(d) for d in (1, 40, 64, 65, 80, 96, 97, 112, 128, 129, 160, 256,
+                                           257, 512)] == \
+        [64, 64, 64, 96, 96, 96, 128, 128, 128, 256, 256, 256, 512, 512]
     with pytest.raises(NotImplementedError):
-        C.kernel_head_dim(257)
+        C.kernel_head_dim(513)
     C.require_kernel_head_dim(256, "x")
     with pytest.raises(NotImplementedError):
         C.require_kernel_head_dim(256, "vertical_and_slash", C.VS_HEAD_DIMS)

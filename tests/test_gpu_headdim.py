@@ -4,7 +4,7 @@ The reference pads head_dim to 16/32/64/128/256/512 before its kernels
 (minference/ops/streaming_kernel_npu.py:377-381,
 minference/ops/block_sparse_kernel_npu.py:651-656) and cuts the output back.
 This build pads q, k and v with zeros to the next built size (64, 96, 128,
-256),
+256, 512),
 which changes no dot product and no pooled mean, and keeps the scale of the
 original head_dim by the reference's rule: (next allowed size)^-0.5 for
 stream_llm / block_sparse, 1/sqrt(D) for dense and decode.  Checked against
@@ -24,7 +24,7 @@ from msa_data import make_qkv, np32
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
-DIMS = (40, 80, 112, 160, 200, 256)
+DIMS = (40, 80, 112, 160, 200, 256, 320, 512)
 
 
 def _err(out, ref):
@@ -71,7 +71,7 @@ def test_padded_head_dim_ops(gpu_device, D):
 def test_unbuilt_paths_refuse_other_head_dims(gpu_device):
     """vertical_and_slash (its estimator divides by the kernel's sqrt(D)) runs
     at 64, 96 and 128 only, the patched forward at the built head dims only;
-    beyond 256 nothing runs."""
+    beyond 512 nothing runs."""
     from minference import streaming_forward
     from minference.ops.vertical_slash_kernel import vertical_and_slash_attention
 
@@ -79,7 +79,7 @@ def test_unbuilt_paths_refuse_other_head_dims(gpu_device):
         q = torch.zeros(1, 2, 128, d, dtype=torch.bfloat16, device=gpu_device)
         with pytest.raises(NotImplementedError):
             vertical_and_slash_attention(q, q, q, 64, 64)
-    q = torch.zeros(1, 2, 128, 300, dtype=torch.bfloat16, device=gpu_device)
+    q = torch.zeros(1, 2, 128, 600, dtype=torch.bfloat16, device=gpu_device)
     with pytest.raises(NotImplementedError):
         streaming_forward(q, q, q, 64, 128)
 

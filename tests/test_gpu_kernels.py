@@ -474,6 +474,7 @@ MIXED_SHAPES = [
     (1, 8, 8, 130, 4000, 96, torch.float16),     # short chunk after a long cache
     (1, 4, 2, 700, 700, 256, torch.bfloat16),    # D 256 (the row-split kernel), GQA
     (1, 6, 3, 300, 1100, 256, torch.float16),    # D 256, chunked prefill, fp16
+    (1, 4, 2, 500, 500, 512, torch.bfloat16),    # D 512 (one wave per SIMD)
 ]
 
 
