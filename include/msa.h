@@ -69,7 +69,7 @@ extern "C" {
 #define MSA_VS_MAX_SEQ 131072 /* longest S of a vertical_and_slash head */
 
 #define MSA_MAX_HEADS 128 /* head descriptors per msa_layer_attention call */
-#define MSA_BLOCK 64      /* tile of the attention kernels; estimator blocks are 64, 128, 256 or 512 */
+#define MSA_BLOCK 64      /* tile of the attention kernels; estimator blocks are multiples of it */
 
 typedef struct msa_tensor4 {
   void* data;
@@ -112,9 +112,9 @@ size_t msa_estimate_workspace_bytes(int64_t batch, int32_t n_slots, int64_t s_q,
 /* Block top-k estimator for the block_sparse heads of a layer (one call for
  * all of them).  Replaces _select_block_sparse_topk_indices
  * (minference/ops/block_sparse_kernel_npu.py:230-263): block-token mean
- * pooling of Q and K in the input dtype (rounded to it; block = 64, 128, 256
- * or 512 tokens, the reference's block_size; ids, n_qb and n_kv_blocks are
- * in those blocks), fp32 pooled scores
+ * pooling of Q and K in the input dtype (rounded to it; block = a multiple
+ * of 64 tokens, the reference's block_size; ids, n_qb and n_kv_blocks are in
+ * those blocks), fp32 pooled scores
  * q_pool.k_pool * score_scale, block-causal mask in the q-block frame, top-k
  * per query block, ids sorted ascending.  Ties break to the lower block id.
  *   slot_heads[s] (host array) = head index in q for slot s, s < n_slots

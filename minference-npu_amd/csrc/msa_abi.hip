@@ -79,7 +79,7 @@ const char* msa_status_str(int status) {
     case MSA_E_DTYPE: return "unsupported or mismatched dtype (q/k/v must be bf16 or fp16; o same or fp32)";
     case MSA_E_HEAD_DIM: return "head_dim must be 64, 96, 128, 256 or 512 (vertical_and_slash: 64, 96 or 128)";
     case MSA_E_ALIGN: return "head_dim stride must be 1, rows 16-byte aligned and the row stride below 2^24";
-    case MSA_E_BLOCK: return "block size must be 64, 128, 256 or 512";
+    case MSA_E_BLOCK: return "block size must be a multiple of 64";
     case MSA_E_TOPK: return "topk must be in [1, n_kv_blocks]";
     case MSA_E_HEADS: return "bad head count, head index or head kind";
     case MSA_E_WORKSPACE: return "workspace missing or too small";
@@ -199,9 +199,7 @@ int msa_block_estimate_ex(const msa_tensor4* q, const msa_tensor4* k, const int3
   flags &= MSA_SELECT_FORCE_FIRST | MSA_SELECT_FORCE_DIAG;
   int st = check_qk(q, k);
   if (st != MSA_OK) return st;
-  if (block != MSA_BLOCK && block != 2 * MSA_BLOCK && block != 4 * MSA_BLOCK &&
-      block != 8 * MSA_BLOCK)
-    return MSA_E_BLOCK;
+  if (block < MSA_BLOCK || block % MSA_BLOCK != 0 || block > kMaxSeq) return MSA_E_BLOCK;
   if (!slot_heads || !idx || !cnt) return MSA_E_NULL;
   if (n_slots <= 0 || n_slots > kMaxHeads) return MSA_E_HEADS;
   const int64_t n_kb_blk = cdiv(k->size[2], block);

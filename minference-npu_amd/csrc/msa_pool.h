@@ -3,11 +3,11 @@
 //
 // Reference semantics: _select_block_sparse_topk_indices,
 // MInference-NPU/minference/ops/block_sparse_kernel_npu.py:240-252: the mean
-// of each block of block_size rows (64, 128, 256 or 512) in the input dtype
-// (a partial last block is zero padded and still divided by block_size), i.e.
-// the fp32 mean rounded to bf16/fp16.  The block sums are accumulated in
-// fp64, exact for 16-bit inputs, so the result is the correctly rounded mean
-// whatever the summation order; dividing by a power of two is exact.
+// of each block of block_size rows (a multiple of 64) in the input dtype (a
+// partial last block is zero padded and still divided by block_size), i.e.
+// the fp32 sum divided by block_size and rounded to bf16/fp16.  The block
+// sums are accumulated in fp64, exact for 16-bit inputs, so the sum does not
+// depend on the summation order.
 #pragma once
 
 #include "msa_common.h"
@@ -58,14 +58,14 @@ __device__ inline void pool_block_group(const uint16_t* base, int64_t ss, int64_
         acc[2 * e + 1] += double(T::to_float(uint16_t(v[u][e] >> 16)));
       }
   }
-  // mean in fp32 (sum / brows is exact: a power of two), then rounded to the
-  // input dtype
-  const float inv = 1.0f / float(brows);
+  // mean: the fp32 sum divided by brows (IEEE division, as torch's mean
+  // divides), then rounded to the input dtype
+  const float n = float(brows);
   u32x4 out;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const uint32_t lo = T::from_float(float(acc[2 * e]) * inv);
-    const uint32_t hi = T::from_float(float(acc[2 * e + 1]) * inv);
+    const uint32_t lo = T::from_float(float(acc[2 * e]) / n);
+    const uint32_t hi = T::from_float(float(acc[2 * e + 1]) / n);
     out[e] = lo | (hi << 16);
   }
   store16(dst + int64_t(blk) * D + c * 8, out);

@@ -31,15 +31,12 @@ _DEFAULT_BLOCK_SIZE = 64
 
 
 # Block sizes of the selector and the token mask: the attention kernels walk
-# 64-token tiles, so a block of 64 m tokens is m consecutive tiles; the
-# pooling divides by the block size exactly, as a power of two.
-BLOCK_SIZES = (64, 128, 256, 512)
-
-
+# 64-token tiles, so a block of 64 m tokens is m consecutive tiles.
 def _check_block_size(block_size: int) -> None:
-    if int(block_size) not in BLOCK_SIZES:
+    bs = int(block_size)
+    if bs < _abi.MSA_BLOCK or bs % _abi.MSA_BLOCK:
         raise NotImplementedError(
-            f"block_size={block_size}: the MI355X kernels take block sizes {BLOCK_SIZES}"
+            f"block_size={block_size}: the MI355X kernels take multiples of {_abi.MSA_BLOCK}"
         )
 
 
@@ -220,7 +217,7 @@ def block_sparse_attention(
         q, k, v:     ``[B, H, S, D]`` (BNSD), RoPE applied, ``repeat_kv``-ed.
         topk_blocks: K blocks kept per query block (clamped to >= 1 and to the
                      number of K blocks, as in the reference).
-        block_size:  64, 128, 256 or 512 tokens (the attention kernels walk
+        block_size:  a multiple of 64 tokens (the attention kernels walk
                      64-token tiles; a larger block is its consecutive tiles).
         out:         optional output (q's dtype or float32).
         force_first, force_diag: keep block 0 / the diagonal block in every

@@ -182,7 +182,7 @@ def pool_blocks(x: np.ndarray, dtype: str, block: int = BLOCK) -> np.ndarray:
     nb = x.shape[-2] // block
     xr = x.reshape(*x.shape[:-2], nb, block, x.shape[-1]).astype(np.float64)
     s = xr.sum(axis=-2).astype(np.float32)
-    mean = (s * np.float32(1.0 / block)).astype(np.float32)
+    mean = (s / np.float32(block)).astype(np.float32)
     return round_to(mean, dtype)
 
 

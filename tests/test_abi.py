@@ -249,7 +249,8 @@ def test_attention_block_slot_range():
     [
         ({"block": 32}, _abi.MSA_E_BLOCK),
         ({"block": 96}, _abi.MSA_E_BLOCK),
-        ({"block": 1024}, _abi.MSA_E_BLOCK),
+        ({"block": 1000}, _abi.MSA_E_BLOCK),
+        ({"block": 0}, _abi.MSA_E_BLOCK),
         ({"block": 128, "topk_max": 3}, _abi.MSA_E_TOPK),  # 256 tokens -> 2 blocks of 128
         ({"topk_max": 0}, _abi.MSA_E_TOPK),
         ({"topk_max": 5}, _abi.MSA_E_TOPK),  # 256 tokens -> 4 blocks

@@ -23,7 +23,8 @@ def test_streaming_reference_matches_oracle(S, n_init, n_local, D):
 
 @pytest.mark.parametrize("S,topk,D,block", [(1000, 4, 96, 64), (640, 100, 64, 64),
                                              (1000, 3, 96, 128), (1100, 2, 96, 256),
-                                             (1500, 2, 64, 512)])
+                                             (1500, 2, 64, 512), (1000, 3, 96, 192),
+                                             (1600, 2, 96, 320)])
 def test_block_reference_matches_oracle(S, topk, D, block):
     q, k, v = make_qkv(1, 2, S, S, D, torch.bfloat16, seed=7, sink_scale=8.0)
     ids = R.select_blocks(R._padded(q), R._padded(k), topk, block).numpy()

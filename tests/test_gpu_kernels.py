@@ -239,6 +239,8 @@ LARGE_BLOCK_CASES = [
     (128, 1, 2, 300, 1100, 96, 3, torch.bfloat16, None, False, False),    # chunk
     (256, 1, 2, 500, 2000, 64, 100, torch.bfloat16, None, False, False),  # top-k clamped
     (128, 1, 2, 1000, 1000, 96, 2, torch.bfloat16, 8.0, True, True),
+    (192, 1, 3, 1000, 1000, 96, 3, torch.bfloat16, 8.0, False, False),  # not a power of two
+    (320, 1, 2, 700, 1700, 128, 2, torch.float16, None, False, False),   # and chunked
 ]
 
 
@@ -246,7 +248,7 @@ LARGE_BLOCK_CASES = [
                          ids=[str(c[:7]) + dtype_tag(c[7]) + ("-forced" if c[9] else "")
                               for c in LARGE_BLOCK_CASES])
 def test_block_sizes_above_64(gpu_device, case):
-    """Selector ids and counts bit-exact at 128/256/512-token blocks, and the
+    """Selector ids and counts bit-exact at blocks of 128 to 512 tokens, and the
     attention over those blocks within the bars of the 64-token path."""
     from minference import block_sparse_attention
     from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
@@ -273,9 +275,10 @@ def test_block_sizes_above_64(gpu_device, case):
     assert_close_lowp(out, ref, what=f"block {block} lowp {case[1:7]}")
 
 
-@pytest.mark.parametrize("block,s_q,s_k", [(128, 1000, 1000), (256, 300, 1300), (512, 1100, 1100)])
+@pytest.mark.parametrize("block,s_q,s_k", [(128, 1000, 1000), (256, 300, 1300), (512, 1100, 1100),
+                                           (192, 900, 900)])
 def test_block_fixed_indices_large_blocks(gpu_device, block, s_q, s_k):
-    """Fixed ids of 128/256/512-token blocks: out of range, negative, future
+    """Fixed ids of 128- to 512-token blocks: out of range, negative, future
     and repeated ids; chunked rows (S_q < S_k)."""
     from minference.ops.block_sparse_kernel import block_sparse_attention_with_indices
 

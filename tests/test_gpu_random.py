@@ -114,7 +114,7 @@ def test_random_layer(gpu_device, i):
 
 N_OP_CASES = 24       # head dims up to 128
 N_OP_WIDE_CASES = 8   # head dims 130 .. 256 (zero-padded to 256)
-N_OP_BLOCK_CASES = 6  # block_sparse_attention with blocks of 128, 256 or 512 tokens
+N_OP_BLOCK_CASES = 6  # block_sparse_attention with blocks of 128 to 512 tokens
 
 
 def _draw_op(i: int):
@@ -135,7 +135,7 @@ def _draw_op(i: int):
     topk = int(rng.integers(1, 60))
     bs = 64
     if i >= N_OP_CASES + N_OP_WIDE_CASES:
-        op, bs = "block", int(rng.choice([128, 256, 512]))
+        op, bs = "block", int(rng.choice([128, 192, 256, 320, 512]))
         D = int(rng.choice([64, 80, 96, 128, 256]))
         S_q = min(S_q, S_k)
         topk = int(rng.integers(1, 12))

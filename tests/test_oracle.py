@@ -58,7 +58,7 @@ def test_pool_matches_torch_mean(dtype, S):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("block,S", [(128, 300), (256, 1000), (512, 1100)])
+@pytest.mark.parametrize("block,S", [(128, 300), (192, 700), (256, 1000), (320, 1500), (512, 1100)])
 def test_pool_matches_torch_mean_large_blocks(dtype, block, S):
     q, _, _ = make_qkv(B=1, H=2, S_q=S, D=96, dtype=dtype, seed=S + block)
     pad = (-S) % block

@@ -79,7 +79,7 @@ def test_block_layer_schedule(monkeypatch):
 
 
 def test_tile_ids_keep_token_visibility():
-    """Ids of 128/256/512-token blocks expanded to 64-token tiles select the
+    """Ids of 128- to 512-token blocks expanded to 64-token tiles select the
     same (query, key) pairs: chunked and ragged shapes, ids out of range,
     negative and repeated."""
     import numpy as np
@@ -89,7 +89,7 @@ def test_tile_ids_keep_token_visibility():
 
     g = np.random.default_rng(3)
     for block, s_q, s_k in [(128, 300, 300), (256, 1000, 1000), (512, 700, 1500),
-                            (128, 100, 900), (256, 64, 64)]:
+                            (128, 100, 900), (256, 64, 64), (192, 500, 500), (320, 300, 1000)]:
         n_bq, n_bk = -(-s_q // block), -(-s_k // block)
         ids = g.integers(-2, n_bk + 2, size=(1, 2, n_bq, 4))
         n_qt, n_kt = -(-s_q // 64), -(-s_k // 64)
