@@ -1058,7 +1058,7 @@ void attn_kernel(AttnParams P) {
 // 32x32x16 operand layout, one 16-byte granule per lane.  The row max is
 // exact per tile (O rescaled when it grows), P biased to 2^kPBias like
 // attn_kernel; fully masked rows give 0.  At D = 512 one wave per SIMD (the
-// O accumulators and two K chunks take about 450 registers).
+// O accumulators, a K chunk and a V span take about 500 registers).
 template <typename T, bool OUT_F32, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D > 256 ? 1 : 2)))
 void attn_wide_kernel(AttnParams P) {
@@ -1152,15 +1152,32 @@ void attn_wide_kernel(AttnParams P) {
   float m = -1e30f;  // running (biased) max of the row in scaled log2 units
   float l = 0.0f;    // this lane's share of the row sum
 
+  // At D = 256 the workgroup copies each tile's staged K and V into LDS (the
+  // four waves read the same operands: each line then leaves L2 once per
+  // workgroup instead of once per wave; 64 KB, two workgroups per CU); at
+  // D = 512 every wave reads them from L2 itself (a 128 KB tile would leave
+  // one workgroup per CU, measured slower).
+  constexpr bool SHARED = D == 256;
+  constexpr int TILE_BYTES = 64 * D * 2;    // one tile of staged K (or V)
+  constexpr int G = TILE_BYTES / 16 / 256;  // 16-byte granules per thread and plane
+  __shared__ __align__(16) unsigned char sm[SHARED ? 2 * TILE_BYTES : 16];
+  auto lds16 = [&](int off) INLINE -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(sm + off);
+  };
   // K operand of virtual chunk vc (span vc / 2, half vc % 2) of tile t: the
   // staged chunk 4t + vc, whose row r is key 32 (vc / 2) + 8 (r / 4) +
   // 4 (vc % 2) + r % 4 of the tile; lane (lc, lr) of k-step ks holds
   // elements 32 ks + 8 lr .. +7 of row lc
   auto load_k = [&](int t, int vc, u32x4 (&kr)[NKS]) INLINE {
-    const uint32_t vo = uint32_t((4 * t + vc) * NKS * 1024 + lane * 16);
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-      kr[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo, 1024 * ks, 0));
+    for (int ks = 0; ks < NKS; ++ks) {
+      if constexpr (SHARED) {
+        kr[ks] = lds16((vc * NKS + ks) * 1024 + lane * 16);
+      } else {
+        const uint32_t vo = uint32_t((4 * t + vc) * NKS * 1024 + lane * 16);
+        kr[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo, 1024 * ks, 0));
+      }
+    }
   };
   auto qk = [&](const u32x4 (&kr)[NKS]) INLINE -> f32x4 {
     f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1172,48 +1189,50 @@ void attn_wide_kernel(AttnParams P) {
   // staged layout: chunk 4t + 2kh + lr / 2, block db / 2, lane 32 (lr % 2) +
   // 16 (db % 2) + lc
   auto load_v = [&](int t, int kh, u32x4 (&vr)[NDO]) INLINE {
-    const int c = 4 * t + 2 * kh + (lr >> 1);
+    const int c = 2 * kh + (lr >> 1);  // chunk within the tile
 #pragma unroll
     for (int db = 0; db < NDO; ++db) {
-      const uint32_t vo =
-          uint32_t(((c * NDB + (db >> 1)) * 64 + 32 * (lr & 1) + 16 * (db & 1) + lc) * 16);
-      vr[db] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vo, 0, 0));
+      const int go = ((c * NDB + (db >> 1)) * 64 + 32 * (lr & 1) + 16 * (db & 1) + lc) * 16;
+      if constexpr (SHARED) {
+        vr[db] = lds16(TILE_BYTES + go);
+      } else {
+        vr[db] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, uint32_t(t * TILE_BYTES + go), 0, 0));
+      }
     }
   };
 
-  // K of the next virtual chunk is requested before the current one's QK
-  // (two register sets); the next tile's first chunk before the softmax
-  // (at D = 512 one K register set: two would not fit beside O and V)
-  u32x4 k0[NKS], k1[NKS];
-  int t = total > 0 ? seq.template finish<false>(seq.fetch(0)) : 0;
-  if constexpr (D <= 256) load_k(t, 0, k0);
+  u32x4 k0[NKS];
   for (int p = 0; p < total; ++p) {
-    // positions past the end repeat the last tile (loads never consumed)
-    const int tn = seq.template finish<false>(seq.fetch(p + 1));
+    const int t = seq.template finish<false>(seq.fetch(p));
+    if constexpr (SHARED) {
+      __syncthreads();  // every wave has read the previous tile
+      u32x4 gk[G], gv[G];
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        const uint32_t go = uint32_t((tid + 256 * u) * 16);
+        gk[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, go, t * TILE_BYTES, 0));
+        gv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, go, t * TILE_BYTES, 0));
+      }
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        *reinterpret_cast<u32x4*>(sm + (tid + 256 * u) * 16) = gk[u];
+        *reinterpret_cast<u32x4*>(sm + TILE_BYTES + (tid + 256 * u) * 16) = gv[u];
+      }
+      __syncthreads();
+    }
     // scores of the tile: s[kh][ab] (lane: keys 8 lr + 4 ab + i of span kh)
     f32x4 s[2][2];
-    u32x4 vr[NDO];  // V of span 0, in flight under the last QK and the softmax
-    if constexpr (D > 256) {
-      load_k(t, 0, k0);
-      s[0][0] = qk(k0);
-      load_k(t, 1, k0);
-      s[0][1] = qk(k0);
-      load_k(t, 2, k0);
-      s[1][0] = qk(k0);
-      load_v(t, 0, vr);
-      load_k(t, 3, k0);
-      s[1][1] = qk(k0);
-    } else {
-      load_k(t, 1, k1);
-      s[0][0] = qk(k0);
-      load_k(t, 2, k0);
-      s[0][1] = qk(k1);
-      load_k(t, 3, k1);
-      s[1][0] = qk(k0);
-      load_v(t, 0, vr);
-      load_k(tn, 0, k0);
-      s[1][1] = qk(k1);
-    }
+    u32x4 vr[NDO];  // V of span 0, requested under the last QK
+    load_k(t, 0, k0);
+    s[0][0] = qk(k0);
+    load_k(t, 1, k0);
+    s[0][1] = qk(k0);
+    load_k(t, 2, k0);
+    s[1][0] = qk(k0);
+    load_v(t, 0, vr);
+    load_k(t, 3, k0);
+    s[1][1] = qk(k0);
     // visibility (every tile: the walk has no separate unmasked part here)
     float mx = -__builtin_inff();
 #pragma unroll
@@ -1262,7 +1281,6 @@ void attn_wide_kernel(AttnParams P) {
                                                        __builtin_bit_cast(f16x8, pb), o[db], 0,
                                                        0, 0);
     }
-    t = tn;
   }
   // row sum over the row's four lanes; O^T block db: lane l holds dims
   // 16 db + 4 lr .. +3 of row lc
