@@ -46,8 +46,8 @@ def _assert_rel(got: torch.Tensor, ref: np.ndarray, ref_abs: np.ndarray, what: s
     assert worst <= 1.0, f"{what}: error {worst:.2f} x the bound"
 
 
-@pytest.mark.parametrize("mag", [1.0e5, 1.0e6])
-def test_mixed_layer_v_beyond_fp16(gpu_device, mag):
+@pytest.mark.parametrize("D,mag", [(96, 1.0e5), (96, 1.0e6), (256, 1.0e5), (512, 1.0e6)])
+def test_mixed_layer_v_beyond_fp16(gpu_device, D, mag):
     """stream / block / dense heads of one launch, bf16 V holding +-mag
     entries in two of the four heads (the other two stay in range); the V
     exponents are 1 and 5.  (P reaches the PV product as fp16 with full
@@ -57,8 +57,8 @@ def test_mixed_layer_v_beyond_fp16(gpu_device, mag):
     from minference import _abi
     from minference.ops.block_sparse_kernel import select_block_sparse_topk_indices
 
-    print(f"[vrange] mixed layer mag={mag}", flush=True)
-    B, H, S, D = 1, 4, 1500, 96
+    print(f"[vrange] mixed layer D={D} mag={mag}", flush=True)
+    B, H, S = 1, 4, 1500
     q, k, v = make_qkv(B, H, S, S, D, torch.bfloat16, seed=17, sink_scale=8.0)
     v = _big_v(v, heads=(0, 2), mag=mag)
     assert v.float().abs().max() > 65504
@@ -111,14 +111,15 @@ def test_vertical_slash_v_beyond_fp16(gpu_device):
     _assert_rel(out, ref, ref_abs, "vertical_and_slash")
 
 
-def test_nan_and_inf_in_v_propagate(gpu_device):
+@pytest.mark.parametrize("D", [96, 256, 512])
+def test_nan_and_inf_in_v_propagate(gpu_device, D):
     """A NaN (Inf) at V[key, dim] makes that dim non-finite in every row that
     attends to the key; rows whose tiles never include the key stay exact, and
     no other dimension is touched."""
     from minference import streaming_forward
 
-    print("[vrange] nan/inf propagation", flush=True)
-    B, H, S, D = 1, 2, 1024, 96
+    print(f"[vrange] nan/inf propagation D={D}", flush=True)
+    B, H, S = 1, 2, 1024
     q, k, v = make_qkv(B, H, S, S, D, torch.bfloat16, seed=5)
     n_init, n_local = 64, 256
     kn_, dn_ = 300, 5    # NaN key / dim (head 0)
