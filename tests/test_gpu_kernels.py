@@ -623,3 +623,16 @@ def test_float32_inputs(gpu_device, rng):
     if rng == "fp16":
         ref = O.streaming_attention(np32(rq), np32(rk), np32(rv), 64, 256)
         assert_close_f32(streaming_forward(dq, dk, dv, 64, 256), ref, what="float32 stream")
+
+    # a padded head dim (200 -> 256) and a block of 128 tokens, same rule
+    q2, k2, v2 = make_qkv(1, 2, 500, 500, 200, torch.float32, seed=22, sink_scale=8.0)
+    d2 = to_dev(gpu_device, q2, k2, v2)
+    r2 = [t.to(torch.float16) for t in d2]
+    for name, call in {
+        "stream D200": lambda a, b, c, **o: streaming_forward(a, b, c, 32, 128, **o),
+        "block D200 bs128": lambda a, b, c, **o: block_sparse_attention(a, b, c, 2, 128, **o),
+    }.items():
+        got = call(*d2)
+        assert got.dtype == torch.float32 and got.shape == q2.shape, name
+        want = call(*r2, out=torch.empty(q2.shape, dtype=torch.float32, device=gpu_device))
+        assert torch.equal(got, want), f"{name}: differs from the call on rounded inputs"

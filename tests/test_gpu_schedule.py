@@ -137,40 +137,43 @@ def test_run_layer_attention_uses_split_schedule(gpu_device):
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("block", [64, 192])
 @pytest.mark.parametrize("flags", [0, 3])
-def test_estimator_passes_match_one_call(gpu_device, flags):
+def test_estimator_passes_match_one_call(gpu_device, flags, block):
     """MSA_ESTIMATE_POOL_ONLY then MSA_ESTIMATE_SELECT_ONLY (on another
     stream, ordered by an event) == one msa_block_estimate_ex call, ids and
-    counts bit for bit, with and without the forced first / diagonal blocks;
-    the pooling pass leaves idx and cnt untouched."""
+    counts bit for bit, with and without the forced first / diagonal blocks,
+    at 64- and 192-token blocks; the pooling pass leaves idx and cnt
+    untouched."""
     from minference import _abi
     from minference.modules.minference_forward import _side_stream
     from minference.ops.common import sparse_scale
 
-    print(f"[schedule] estimator passes flags={flags}", flush=True)
+    print(f"[schedule] estimator passes flags={flags} block={block}", flush=True)
     S = 2000
     kinds = ["block_sparse", "stream_llm", "block_sparse", "block_sparse"]
     plan, q, k, v = _layer(gpu_device, 4, 2, S, kinds, seed=11)
-    n_qb = math.ceil(S / 64)
+    n_qb = math.ceil(S / block)
     ns = len(plan.block_heads)
     topk = [3, 6, 5]
     idx = torch.empty((1, ns, n_qb, 6), dtype=torch.int32, device=gpu_device)
     cnt = torch.empty((1, ns, n_qb), dtype=torch.int32, device=gpu_device)
     ref_idx, ref_cnt = torch.full_like(idx, -5), torch.full_like(cnt, -5)
     sc = sparse_scale(96)
-    _abi.block_estimate(q, k, plan.block_heads, topk, 6, sc, ref_idx, ref_cnt, flags=flags)
+    _abi.block_estimate(q, k, plan.block_heads, topk, 6, sc, ref_idx, ref_cnt, flags=flags,
+                        block=block)
     ws = _abi.workspace(_abi.estimate_workspace_bytes(1, ns, S, S, 96), gpu_device)
     idx.fill_(-5)
     cnt.fill_(-5)
     _abi.block_estimate(q, k, plan.block_heads, topk, 6, sc, idx, cnt, ws,
-                        flags=flags | _abi.MSA_ESTIMATE_POOL_ONLY)
+                        flags=flags | _abi.MSA_ESTIMATE_POOL_ONLY, block=block)
     torch.cuda.synchronize()
     assert bool((idx == -5).all()) and bool((cnt == -5).all())
     side = _side_stream(q.device)
     side.wait_stream(torch.cuda.current_stream(q.device))
     with torch.cuda.stream(side):
         _abi.block_estimate(q, k, plan.block_heads, topk, 6, sc, idx, cnt, ws,
-                            flags=flags | _abi.MSA_ESTIMATE_SELECT_ONLY)
+                            flags=flags | _abi.MSA_ESTIMATE_SELECT_ONLY, block=block)
     torch.cuda.current_stream(q.device).wait_stream(side)
     torch.cuda.synchronize()
     assert torch.equal(idx, ref_idx) and torch.equal(cnt, ref_cnt)
